@@ -1,0 +1,461 @@
+// Ragged KV data movement for gfx950: compaction, per-head append, recall merge, archive
+// pack and multi-request batch append. Every kernel is a pure row gather, HBM-bound, so the
+// design goal is full-width (16-byte) coalesced accesses and as few index computations per
+// byte as possible:
+//   - a "lane group" of power-of-two lanes moves one row, each lane a 16-byte granule (or the
+//     widest granule the row size and pointers allow);
+//   - each lane group walks R consecutive output rows, so per-row index work (a binary search
+//     in compaction, a descriptor read in batch append) is amortised or incremental;
+//   - every index read from device memory is bounds-checked before it is dereferenced.
+#include "lr_common.hpp"
+
+namespace lr {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct RowLayout {
+  int64_t row_bytes;  // bytes per row (dim * element size)
+  int64_t chunks;     // granules per row
+  int lanes_log2;     // log2(lanes per row group), lanes <= 64
+  int rows_per_group; // consecutive rows walked by one lane group
+};
+
+inline int log2_ceil(int64_t v) {
+  int l = 0;
+  while ((int64_t{1} << l) < v) ++l;
+  return l;
+}
+
+// Lane-group geometry: up to 64 lanes per row, enough lane groups to fill 256 CUs.
+inline RowLayout make_layout(int64_t row_bytes, int granule, int64_t rows, int max_rows_per_group) {
+  RowLayout layout;
+  layout.row_bytes = row_bytes;
+  layout.chunks = row_bytes / granule;
+  layout.lanes_log2 = log2_ceil(layout.chunks < 64 ? layout.chunks : 64);
+  const int64_t lanes = int64_t{1} << layout.lanes_log2;
+  const int64_t target_groups = (int64_t{256} * 2048) / lanes;  // ~full residency on 256 CUs
+  int64_t r = ceil_div(rows, target_groups);
+  if (r < 1) r = 1;
+  if (r > max_rows_per_group) r = max_rows_per_group;
+  layout.rows_per_group = static_cast<int>(r);
+  return layout;
+}
+
+inline int64_t blocks_for(const RowLayout& layout, int64_t rows) {
+  const int64_t groups_per_block = kThreads >> layout.lanes_log2;
+  const int64_t groups = ceil_div(rows, layout.rows_per_group);
+  int64_t blocks = ceil_div(groups, groups_per_block);
+  if (blocks < 1) blocks = 1;
+  return blocks < kMaxGridX ? blocks : kMaxGridX;
+}
+
+template <int G>
+__device__ __forceinline__ void copy_row(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                         int64_t chunks, int lane, int lanes) {
+  using V = typename Granule<G>::type;
+  const V* s = reinterpret_cast<const V*>(src);
+  V* d = reinterpret_cast<V*>(dst);
+  for (int64_t c = lane; c < chunks; c += lanes) d[c] = s[c];
+}
+
+// Lane-group coordinates shared by the row kernels.
+struct GroupCoord {
+  int lane, lanes, group, groups_per_block;
+};
+
+__device__ __forceinline__ GroupCoord group_coord(int lanes_log2) {
+  GroupCoord g;
+  g.lanes = 1 << lanes_log2;
+  g.lane = threadIdx.x & (g.lanes - 1);
+  g.group = threadIdx.x >> lanes_log2;
+  g.groups_per_block = blockDim.x >> lanes_log2;
+  return g;
+}
+
+// ---------------------------------------------------------------------------------------
+// compact: output row r takes input row r + j, j = #{i : removed[i] - i <= r}
+// (the gather rule of csrc/scoring.cu:164-188). One binary search per lane group start, then
+// an incremental walk over the sorted removal list for the following rows.
+template <int G>
+__global__ __launch_bounds__(kThreads) void compact_kernel(
+    const uint8_t* __restrict__ keys, const uint8_t* __restrict__ values,
+    const float* __restrict__ positions, const int64_t* __restrict__ removed,
+    int64_t removed_count, int64_t rows_in, int64_t rows_out, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions) {
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t R = layout.rows_per_group;
+  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
+       first < rows_out;
+       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
+    int64_t lo = 0, hi = removed_count;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (removed[mid] - mid <= first) lo = mid + 1;
+      else hi = mid;
+    }
+    int64_t src = first + lo;
+    int64_t next = lo;  // removed[next] > src for a well-formed list
+    const int64_t end = first + R < rows_out ? first + R : rows_out;
+    for (int64_t row = first; row < end; ++row) {
+      if (row != first) {
+        ++src;
+        while (next < removed_count && removed[next] == src) {
+          ++src;
+          ++next;
+        }
+      }
+      if (src < 0 || src >= rows_in) break;
+      copy_row<G>(keys + src * layout.row_bytes, out_keys + row * layout.row_bytes,
+                  layout.chunks, gc.lane, gc.lanes);
+      copy_row<G>(values + src * layout.row_bytes, out_values + row * layout.row_bytes,
+                  layout.chunks, gc.lane, gc.lanes);
+      if (gc.lane == 0) out_positions[row] = positions[src];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Per-head ragged append (csrc/scoring.cu:130-162 and csrc/cache_legacy.cu:13-40): head h's
+// old rows move from src_start(h) to dst_start(h) = src_start(h) + h * added, followed by
+// `added` new rows. blockIdx.y = head; rows of a head are covered up to `covered_rows`.
+template <int G, bool kWithPositions>
+__global__ __launch_bounds__(kThreads) void head_append_kernel(
+    const uint8_t* __restrict__ cache_keys, const uint8_t* __restrict__ cache_values,
+    const float* __restrict__ positions, int64_t rows_in, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, const int32_t* __restrict__ starts,
+    const int32_t* __restrict__ lengths_or_next, int lengths_are_cumulative, int64_t heads,
+    int64_t added, int64_t covered_rows, int64_t logical_start, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
+    int32_t* __restrict__ out_lengths) {
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t head = blockIdx.y;
+  const int64_t old_start = starts[head];
+  const int64_t old_length = lengths_are_cumulative ? lengths_or_next[head + 1] - old_start
+                                                    : lengths_or_next[head];
+  const int64_t new_start = old_start + head * added;
+  if (out_cumulative != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    out_cumulative[head] = static_cast<int32_t>(new_start);
+    out_lengths[head] = static_cast<int32_t>(old_length + added);
+    if (head == heads - 1)
+      out_cumulative[heads] = static_cast<int32_t>(lengths_or_next[heads] + heads * added);
+  }
+  int64_t total = old_length + added;
+  if (total > covered_rows) total = covered_rows;
+  const int64_t rows_out = rows_in + heads * added;
+  const int64_t R = layout.rows_per_group;
+  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
+       first < total;
+       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
+    const int64_t end = first + R < total ? first + R : total;
+    for (int64_t p = first; p < end; ++p) {
+      const int64_t dst = new_start + p;
+      if (dst < 0 || dst >= rows_out) break;
+      if (p < old_length) {
+        const int64_t src = old_start + p;
+        if (src < 0 || src >= rows_in) break;
+        copy_row<G>(cache_keys + src * layout.row_bytes, out_keys + dst * layout.row_bytes,
+                    layout.chunks, gc.lane, gc.lanes);
+        if (cache_values != nullptr)
+          copy_row<G>(cache_values + src * layout.row_bytes, out_values + dst * layout.row_bytes,
+                      layout.chunks, gc.lane, gc.lanes);
+        if (kWithPositions && gc.lane == 0) out_positions[dst] = positions[src];
+      } else {
+        const int64_t src = head * added + (p - old_length);
+        copy_row<G>(new_keys + src * layout.row_bytes, out_keys + dst * layout.row_bytes,
+                    layout.chunks, gc.lane, gc.lanes);
+        if (new_values != nullptr)
+          copy_row<G>(new_values + src * layout.row_bytes, out_values + dst * layout.row_bytes,
+                      layout.chunks, gc.lane, gc.lanes);
+        if (kWithPositions && gc.lane == 0)
+          out_positions[dst] = static_cast<float>(logical_start + (p - old_length));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Indexed gathers. kMode selects the index rule:
+//   0 keep      (compact_flattened_kv, csrc/cache_legacy.cu:42-61): src = index[r]
+//   1 merge     (csrc/recall.cu:7-28): index[r] >= 0 existing row, else recalled[-index[r]-1]
+//   2 pack      (csrc/recall.cu:30-47): src = index[r], output interleaved [r, {K,V}]
+enum GatherMode { kKeep = 0, kMerge = 1, kPack = 2 };
+
+template <int G, int kMode>
+__global__ __launch_bounds__(kThreads) void gather_kernel(
+    const uint8_t* __restrict__ keys, const uint8_t* __restrict__ values,
+    const float* __restrict__ positions, int64_t rows_in, const int64_t* __restrict__ index,
+    int64_t rows_out, const uint8_t* __restrict__ recalled,
+    const float* __restrict__ recalled_positions, int64_t recalled_rows,
+    const int64_t* __restrict__ heads, int64_t layer, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int64_t* __restrict__ metadata) {
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t R = layout.rows_per_group;
+  const int64_t rb = layout.row_bytes;
+  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
+       first < rows_out;
+       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
+    const int64_t end = first + R < rows_out ? first + R : rows_out;
+    for (int64_t r = first; r < end; ++r) {
+      const int64_t source = index[r];
+      if (kMode == kMerge && source < 0) {
+        const int64_t restored = -source - 1;
+        if (restored >= recalled_rows) continue;
+        copy_row<G>(recalled + (2 * restored) * rb, out_keys + r * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        copy_row<G>(recalled + (2 * restored + 1) * rb, out_values + r * rb, layout.chunks,
+                    gc.lane, gc.lanes);
+        if (gc.lane == 0) out_positions[r] = recalled_positions[restored];
+        continue;
+      }
+      if (source < 0 || source >= rows_in) continue;
+      if (kMode == kPack) {
+        copy_row<G>(keys + source * rb, out_keys + (2 * r) * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        copy_row<G>(values + source * rb, out_keys + (2 * r + 1) * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        if (gc.lane == 0) {
+          metadata[3 * r] = layer;
+          metadata[3 * r + 1] = heads[r];
+          metadata[3 * r + 2] = static_cast<int64_t>(positions[source]);
+        }
+      } else {
+        copy_row<G>(keys + source * rb, out_keys + r * rb, layout.chunks, gc.lane, gc.lanes);
+        copy_row<G>(values + source * rb, out_values + r * rb, layout.chunks, gc.lane, gc.lanes);
+        if (kMode == kMerge && gc.lane == 0) out_positions[r] = positions[source];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// batch_append (csrc/batch_append.cu:8-34): blockIdx.y = (request, head) segment with the
+// reference's 7-word descriptor; the segment's old rows then its one new row are written
+// contiguously from the destination row.
+template <int G>
+__global__ __launch_bounds__(kThreads) void batch_append_kernel(
+    const int64_t* __restrict__ descriptors, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions) {
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t segment = blockIdx.y;
+  const int64_t* d = descriptors + segment * 7;
+  const uint8_t* keys = reinterpret_cast<const uint8_t*>(d[0]);
+  const uint8_t* values = reinterpret_cast<const uint8_t*>(d[1]);
+  const float* positions = reinterpret_cast<const float*>(d[2]);
+  const int64_t source = d[3], old_length = d[4], destination = d[5], logical = d[6];
+  int64_t total = old_length + 1;
+  if (total > max_rows) total = max_rows;
+  const int64_t R = layout.rows_per_group;
+  const int64_t rb = layout.row_bytes;
+  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
+       first < total;
+       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
+    const int64_t end = first + R < total ? first + R : total;
+    for (int64_t p = first; p < end; ++p) {
+      const int64_t dst = destination + p;
+      if (p < old_length) {
+        copy_row<G>(keys + (source + p) * rb, out_keys + dst * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        copy_row<G>(values + (source + p) * rb, out_values + dst * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        if (gc.lane == 0) out_positions[dst] = positions[source + p];
+      } else {
+        copy_row<G>(new_keys + segment * rb, out_keys + dst * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        copy_row<G>(new_values + segment * rb, out_values + dst * rb, layout.chunks, gc.lane,
+                    gc.lanes);
+        if (gc.lane == 0) out_positions[dst] = static_cast<float>(logical);
+      }
+    }
+  }
+}
+
+inline const uint8_t* bytes(const void* p) { return static_cast<const uint8_t*>(p); }
+inline uint8_t* bytes(void* p) { return static_cast<uint8_t*>(p); }
+
+}  // namespace
+}  // namespace lr
+
+using namespace lr;
+
+extern "C" int lr_compact(const void* keys, const void* values, const float* positions,
+                          int64_t rows, int64_t dim, int elem_bytes, const int64_t* removed,
+                          int64_t removed_count, void* out_keys, void* out_values,
+                          float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes), "Invalid KV layout");
+  LR_REQUIRE(rows >= 0 && dim > 0, "Invalid KV layout");
+  LR_REQUIRE(removed_count >= 0 && removed_count <= rows, "Invalid removals");
+  const int64_t rows_out = rows - removed_count;
+  if (rows_out == 0) return LR_OK;
+  LR_REQUIRE(keys && values && positions && out_keys && out_values && out_positions,
+             "Expected contiguous CUDA tensor");
+  LR_REQUIRE(removed_count == 0 || removed != nullptr, "Invalid removals");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {keys, values, out_keys, out_values});
+  const RowLayout layout = make_layout(row_bytes, g, rows_out, 8);
+  const int64_t blocks = blocks_for(layout, rows_out);
+  return dispatch_granule(g, [&]<int G>() {
+    compact_kernel<G><<<blocks, kThreads, 0, as_stream(stream)>>>(
+        bytes(keys), bytes(values), positions, removed, removed_count, rows, rows_out, layout,
+        bytes(out_keys), bytes(out_values), out_positions);
+    return check_launch("compact");
+  });
+}
+
+extern "C" int lr_append(const void* keys, const void* values, const float* positions,
+                         int64_t rows, const void* new_keys, const void* new_values,
+                         const int32_t* cumulative, int64_t heads, int64_t added, int64_t dim,
+                         int elem_bytes, int64_t logical_start, int64_t max_length,
+                         void* out_keys, void* out_values, float* out_positions,
+                         int32_t* out_cumulative, int32_t* out_lengths, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && rows >= 0 && dim > 0, "Invalid KV layout");
+  LR_REQUIRE(heads > 0 && added > 0 && max_length >= 0, "Invalid appended shape");
+  LR_REQUIRE(heads <= 65535, "Invalid appended shape");
+  LR_REQUIRE(new_keys && new_values && cumulative && out_keys && out_values && out_positions &&
+                 out_cumulative && out_lengths,
+             "Expected contiguous CUDA tensor");
+  LR_REQUIRE(rows == 0 || (keys && values && positions), "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {keys, values, new_keys, new_values, out_keys, out_values});
+  const int64_t covered = max_length + added;
+  const RowLayout layout = make_layout(row_bytes, g, covered * heads, 8);
+  int64_t bx = ceil_div(ceil_div(covered, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  if (bx < 1) bx = 1;
+  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads));
+  return dispatch_granule(g, [&]<int G>() {
+    head_append_kernel<G, true><<<grid, kThreads, 0, as_stream(stream)>>>(
+        bytes(keys), bytes(values), positions, rows, bytes(new_keys), bytes(new_values),
+        cumulative, cumulative, 1, heads, added, covered, logical_start, layout,
+        bytes(out_keys), bytes(out_values), out_positions, out_cumulative, out_lengths);
+    return check_launch("append");
+  });
+}
+
+extern "C" int lr_append_flattened_cache(const void* cache, int64_t rows, const void* states,
+                                         int64_t total_heads, int64_t new_length, int64_t dim,
+                                         int elem_bytes, const int32_t* head_lens,
+                                         const int32_t* cu_head_lens, void* out, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && rows >= 0 && dim > 0, "head_dim mismatch");
+  LR_REQUIRE(total_heads >= 0 && new_length >= 0 && total_heads <= 65535, "head count mismatch");
+  if (total_heads == 0 || (rows == 0 && new_length == 0)) return LR_OK;
+  LR_REQUIRE(states && head_lens && cu_head_lens && out, "states must be contiguous CUDA");
+  LR_REQUIRE(rows == 0 || cache, "cache must be CUDA");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {cache, states, out});
+  // Rows per head are bounded by the whole cache plus the new rows.
+  const int64_t covered = rows + new_length;
+  const RowLayout layout = make_layout(row_bytes, g, rows + total_heads * new_length, 8);
+  int64_t per_head = ceil_div(rows + total_heads * new_length, total_heads);
+  int64_t bx = ceil_div(ceil_div(per_head, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  if (bx < 1) bx = 1;
+  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(total_heads));
+  return dispatch_granule(g, [&]<int G>() {
+    head_append_kernel<G, false><<<grid, kThreads, 0, as_stream(stream)>>>(
+        bytes(cache), nullptr, nullptr, rows, bytes(states), nullptr, cu_head_lens, head_lens, 0,
+        total_heads, new_length, covered, 0, layout, bytes(out), nullptr, nullptr, nullptr,
+        nullptr);
+    return check_launch("append_flattened_cache");
+  });
+}
+
+extern "C" int lr_compact_flattened_kv(const void* keys, const void* values, int64_t rows,
+                                       int64_t dim, int elem_bytes,
+                                       const int64_t* keep_indices, int64_t keep_count,
+                                       void* out_keys, void* out_values, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && rows >= 0 && dim > 0, "K/V shape mismatch");
+  LR_REQUIRE(keep_count >= 0, "keep_indices must be rank one");
+  if (keep_count == 0) return LR_OK;
+  LR_REQUIRE(keys && values && keep_indices && out_keys && out_values,
+             "keep_indices must be contiguous CUDA");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {keys, values, out_keys, out_values});
+  const RowLayout layout = make_layout(row_bytes, g, keep_count, 8);
+  const int64_t blocks = blocks_for(layout, keep_count);
+  return dispatch_granule(g, [&]<int G>() {
+    gather_kernel<G, kKeep><<<blocks, kThreads, 0, as_stream(stream)>>>(
+        bytes(keys), bytes(values), nullptr, rows, keep_indices, keep_count, nullptr, nullptr, 0,
+        nullptr, 0, layout, bytes(out_keys), bytes(out_values), nullptr, nullptr);
+    return check_launch("compact_flattened_kv");
+  });
+}
+
+extern "C" int lr_merge(const void* keys, const void* values, const float* positions,
+                        int64_t rows, const void* recalled, const float* recalled_positions,
+                        int64_t recalled_rows, const int64_t* mapping, int64_t out_rows,
+                        int64_t dim, int elem_bytes, void* out_keys, void* out_values,
+                        float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && rows >= 0 && dim > 0, "Invalid K/V shape");
+  LR_REQUIRE(recalled_rows >= 0 && out_rows >= 0, "Invalid recalled shape");
+  if (out_rows == 0) return LR_OK;
+  LR_REQUIRE(mapping && out_keys && out_values && out_positions, "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {keys, values, recalled, out_keys, out_values});
+  const RowLayout layout = make_layout(row_bytes, g, out_rows, 8);
+  const int64_t blocks = blocks_for(layout, out_rows);
+  return dispatch_granule(g, [&]<int G>() {
+    gather_kernel<G, kMerge><<<blocks, kThreads, 0, as_stream(stream)>>>(
+        bytes(keys), bytes(values), positions, rows, mapping, out_rows, bytes(recalled),
+        recalled_positions, recalled_rows, nullptr, 0, layout, bytes(out_keys),
+        bytes(out_values), out_positions, nullptr);
+    return check_launch("merge");
+  });
+}
+
+extern "C" int lr_pack(const void* keys, const void* values, const float* positions,
+                       int64_t rows, const int64_t* indices, const int64_t* heads, int64_t count,
+                       int64_t dim, int elem_bytes, int64_t layer, void* payload,
+                       int64_t* metadata, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && rows >= 0 && dim > 0, "Invalid K/V shape");
+  LR_REQUIRE(count >= 0, "Invalid gather indices");
+  if (count == 0) return LR_OK;
+  LR_REQUIRE(keys && values && positions && indices && heads && payload && metadata,
+             "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {keys, values, payload});
+  const RowLayout layout = make_layout(row_bytes, g, count, 8);
+  const int64_t blocks = blocks_for(layout, count);
+  return dispatch_granule(g, [&]<int G>() {
+    gather_kernel<G, kPack><<<blocks, kThreads, 0, as_stream(stream)>>>(
+        bytes(keys), bytes(values), positions, rows, indices, count, nullptr, nullptr, 0, heads,
+        layer, layout, bytes(payload), nullptr, nullptr, metadata);
+    return check_launch("pack");
+  });
+}
+
+extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
+                               const void* new_keys, const void* new_values, int64_t dim,
+                               int elem_bytes, int64_t max_rows, void* out_keys,
+                               void* out_values, float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Only batched one-token append is supported");
+  LR_REQUIRE(segments > 0 && segments <= 65535, "Request metadata mismatch");
+  LR_REQUIRE(max_rows >= 1, "Invalid head length");
+  LR_REQUIRE(descriptors && new_keys && new_values && out_keys && out_values && out_positions,
+             "Contiguous CUDA states required");
+  const int64_t row_bytes = dim * elem_bytes;
+  // Descriptor pointers are required to share the alignment of the row size (a whole
+  // number of rows from a 16-byte aligned allocation), so only the row size and the
+  // pointers seen here bound the granule.
+  const int g = granule_for(row_bytes, {new_keys, new_values, out_keys, out_values});
+  const RowLayout layout = make_layout(row_bytes, g, max_rows * segments, 8);
+  int64_t bx = ceil_div(ceil_div(max_rows, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  if (bx < 1) bx = 1;
+  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(segments));
+  return dispatch_granule(g, [&]<int G>() {
+    batch_append_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+        descriptors, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
+        bytes(out_values), out_positions);
+    return check_launch("batch_append");
+  });
+}

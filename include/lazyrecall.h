@@ -1,0 +1,189 @@
+/*
+ * lazyrecall.h — C ABI of liblazyrecall_hip.so, the MI355X (gfx950) implementation of
+ * LazyRecall's KV-cache management hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are raw device pointers to contiguous, row-major storage that the
+ *     caller owns; the library never allocates or frees them. Sizes are element/row counts.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream). Every launch is
+ *     asynchronous on that stream; nothing here synchronises the host unless stated.
+ *   - Return value: LR_OK (0) on success. On failure a non-zero LR_ERR_* code is returned and
+ *     lr_last_error() gives a message for the calling thread. Argument checks happen on the host
+ *     before any launch, so an LR_ERR_INVALID return means nothing was enqueued.
+ *   - K/V element type is given as a byte width (`elem_bytes` in {2, 4, 8}) for pure data
+ *     movement, or as an LR_DTYPE_* code where arithmetic depends on it.
+ *   - Index arrays read on the device (removed rows, mappings, keep indices, descriptors) are
+ *     bounds-checked per row inside the kernels: an out-of-range index leaves that output row
+ *     unwritten instead of touching memory outside the operands.
+ *
+ * Reference citations are to wrnwwrnw/code_for_iclr27 (paths relative to its root).
+ */
+#ifndef LAZYRECALL_H
+#define LAZYRECALL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LR_OK 0
+#define LR_ERR_INVALID 1  /* bad argument; nothing enqueued */
+#define LR_ERR_HIP 2      /* the HIP runtime reported an error */
+
+#define LR_DTYPE_F32 0
+#define LR_DTYPE_F64 1
+#define LR_DTYPE_F16 2
+#define LR_DTYPE_BF16 3
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* lr_last_error(void);
+/* ABI revision of this header; bumped whenever a signature changes. */
+int lr_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * Module lazy_recall._C (csrc/bindings.cpp:20-29)
+ * ------------------------------------------------------------------------------------- */
+
+/* temporal_probabilities (csrc/scoring.cu:32-66, 205-233).
+ * logits [window, groups, length] of `logits_dtype` (F32/F16/BF16), projected [groups, length]
+ * f32, query_positions [window] i64, key_positions [length] f32.
+ * Writes probabilities [window, groups, length] f32 and output_projection [window, groups] f32. */
+int lr_temporal_probabilities(const void* logits, int logits_dtype, const float* projected,
+                              const int64_t* query_positions, const float* key_positions,
+                              int64_t window, int64_t groups, int64_t length, float scale,
+                              float* probabilities, float* output_projection, void* stream);
+
+/* temporal_risk (csrc/scoring.cu:68-128, 235-255). Writes result [last - first] f32. */
+int lr_temporal_risk(const float* probabilities, const float* output_projection,
+                     const float* projected, const float* margin, int64_t window, int64_t groups,
+                     int64_t length, int64_t first, int64_t last, double epsilon, float* result,
+                     void* stream);
+
+/* append (csrc/scoring.cu:130-162, 264-292). keys/values [rows, dim], positions [rows] f32,
+ * new_keys/new_values [1, heads, added, dim], cumulative [heads + 1] i32.
+ * Outputs: keys/values [rows + heads*added, dim], positions [rows + heads*added] f32,
+ * cumulative [heads + 1] i32, lengths [heads] i32. max_length sizes the grid exactly as the
+ * reference's `maximum_length` argument does. */
+int lr_append(const void* keys, const void* values, const float* positions, int64_t rows,
+              const void* new_keys, const void* new_values, const int32_t* cumulative,
+              int64_t heads, int64_t added, int64_t dim, int elem_bytes, int64_t logical_start,
+              int64_t max_length, void* out_keys, void* out_values, float* out_positions,
+              int32_t* out_cumulative, int32_t* out_lengths, void* stream);
+
+/* compact (csrc/scoring.cu:164-188, 294-314). removed [removed_count] i64, sorted, unique.
+ * Outputs [rows - removed_count, dim] and positions [rows - removed_count]. */
+int lr_compact(const void* keys, const void* values, const float* positions, int64_t rows,
+               int64_t dim, int elem_bytes, const int64_t* removed, int64_t removed_count,
+               void* out_keys, void* out_values, float* out_positions, void* stream);
+
+/* pool (csrc/scoring.cu:190-203, 316-329). Sliding max of odd `width` inside each segment
+ * [bounds[s], bounds[s+1]). bounds [segments + 1] i64 on the device; total = scores length. */
+int lr_pool(const float* scores, int64_t total, const int64_t* bounds, int64_t segments,
+            int64_t max_count, int64_t width, float* out, void* stream);
+
+/* merge (csrc/recall.cu:7-28, 54-84). mapping [out_rows] i64: >=0 selects an existing row,
+ * -(i+1) selects recalled row i. recalled [recalled_rows, 2, dim] (K at [i,0], V at [i,1]). */
+int lr_merge(const void* keys, const void* values, const float* positions, int64_t rows,
+             const void* recalled, const float* recalled_positions, int64_t recalled_rows,
+             const int64_t* mapping, int64_t out_rows, int64_t dim, int elem_bytes,
+             void* out_keys, void* out_values, float* out_positions, void* stream);
+
+/* pack (csrc/recall.cu:30-47, 86-111). Gathers rows `indices` into payload [count, 2, dim]
+ * and writes metadata [count, 3] i64 = (layer, heads[i], int64(positions[indices[i]])). */
+int lr_pack(const void* keys, const void* values, const float* positions, int64_t rows,
+            const int64_t* indices, const int64_t* heads, int64_t count, int64_t dim,
+            int elem_bytes, int64_t layer, void* payload, int64_t* metadata, void* stream);
+
+/* batch_append (csrc/batch_append.cu:8-94). `descriptors` is a DEVICE array of
+ * segments x 7 i64 in the reference's layout: {keys ptr, values ptr, positions ptr,
+ * source row, old length, destination row, logical position}. new_keys/new_values hold one
+ * row per segment ([segments, dim]). max_rows = max over segments of (old length + 1).
+ * Output rows are written at destination row .. destination row + old length. */
+int lr_batch_append(const int64_t* descriptors, int64_t segments, const void* new_keys,
+                    const void* new_values, int64_t dim, int elem_bytes, int64_t max_rows,
+                    void* out_keys, void* out_values, float* out_positions, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Module lazy_recall._legacy_C (csrc/cache_legacy.cu:304-308)
+ * ------------------------------------------------------------------------------------- */
+
+/* append_flattened_cache (csrc/cache_legacy.cu:13-40, 145-197). cache [rows, dim],
+ * states [total_heads, new_length, dim], head_lens/cu_head_lens i32 [total_heads (+1)].
+ * Output [rows + total_heads*new_length, dim]. */
+int lr_append_flattened_cache(const void* cache, int64_t rows, const void* states,
+                              int64_t total_heads, int64_t new_length, int64_t dim,
+                              int elem_bytes, const int32_t* head_lens,
+                              const int32_t* cu_head_lens, void* out, void* stream);
+
+/* compact_flattened_kv (csrc/cache_legacy.cu:42-61, 199-242). Gathers keep_indices
+ * [keep_count] i64 rows of keys/values [rows, dim] into out [keep_count, dim]. */
+int lr_compact_flattened_kv(const void* keys, const void* values, int64_t rows, int64_t dim,
+                            int elem_bytes, const int64_t* keep_indices, int64_t keep_count,
+                            void* out_keys, void* out_values, void* stream);
+
+/* decision_risk_scores (csrc/cache_legacy.cu:63-135, 244-302). probabilities [groups,
+ * candidates] f32, values [candidates, head_dim] of values_dtype, head_outputs and gradients
+ * [groups, head_dim] f32. Writes scores [candidates] f32. */
+int lr_decision_risk_scores(const float* probabilities, const void* values, int values_dtype,
+                            const float* head_outputs, const float* gradients, int64_t groups,
+                            int64_t candidates, int64_t head_dim, double base_margin,
+                            double epsilon, float* scores, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Module lazy_recall._host (csrc/host.cpp:5-18)
+ * ------------------------------------------------------------------------------------- */
+
+/* register_host / unregister_host (csrc/host.cpp:5-13): page-lock caller-owned host memory
+ * so copies from it run asynchronously on a side stream. */
+int lr_register_host(uint64_t address, uint64_t bytes);
+int lr_unregister_host(uint64_t address);
+
+/* ---------------------------------------------------------------------------------------
+ * Fused audit-step entry points. These have no single reference counterpart: each replaces a
+ * Python loop of reference calls (cited per function) with one or a few launches covering
+ * every (layer, KV head) segment.
+ * ------------------------------------------------------------------------------------- */
+
+/* One scored segment = one (layer, KV head). Device array of `segments` rows of
+ * LR_SEG_WORDS i64, written by the caller:
+ *   [0] keys ptr   (bf16 [length, dim], this head's rows of the layer's flat cache)
+ *   [1] values ptr (bf16 [length, dim])
+ *   [2] key positions ptr (f32 [length])
+ *   [3] queries ptr (bf16; group g, query w at  ptr + (g * query_group_stride + w) * dim)
+ *   [4] margin gradient ptr (f32 [groups, dim], this head's rows of the pre-projection gradient)
+ *   [5] length, [6] first candidate, [7] last candidate (exclusive; first < last <= length)
+ *   [8] output offset of this segment's first score
+ *   [9] row-stats offset (segment index * groups * window is the natural choice)
+ *   [10] projected-values offset (floats; needs groups * length floats)
+ *   [11] unused, must be 0 */
+#define LR_SEG_WORDS 12
+
+/* Bytes of workspace lr_score_segments needs. */
+size_t lr_score_workspace_bytes(int64_t segments, int64_t groups, int64_t window,
+                                int64_t projected_floats);
+
+/* Temporal decision-risk scores of every candidate of every segment; equal to the reference's
+ * per-head temporal_head_scores (src/lazy_recall/scoring.py:152-195: projected values GEMM,
+ * bf16 Q.K^T, temporal_probabilities, temporal_risk, maximum over query chunks) for all heads of
+ * compute_score_table (src/lazy_recall/scoring.py:218-287) at once, without materialising
+ * logits or probabilities. query_positions [window] i64, margin [1] f32 (device).
+ * query_group_stride is in rows of `dim` elements. scores gets sum(last - first) floats. */
+int lr_score_segments(const int64_t* segment_table, int64_t segments, int64_t groups,
+                      int64_t window, int64_t dim, int64_t max_length, int64_t max_candidates,
+                      int64_t query_group_stride, const int64_t* query_positions,
+                      const float* margin, float scale, double epsilon, void* workspace,
+                      size_t workspace_bytes, float* scores, void* stream);
+
+/* Test hook for the parity suite: the bf16 logits Q.K^T exactly as lr_score_segments forms them
+ * (same MFMA sequence), for one segment: out [groups, window, length] bf16 (raw, unscaled). */
+int lr_debug_segment_logits(const int64_t* segment_table, int64_t segment, int64_t groups,
+                            int64_t window, int64_t dim, int64_t length,
+                            int64_t query_group_stride, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAZYRECALL_H */

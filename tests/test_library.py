@@ -1,0 +1,74 @@
+"""The C-ABI library loads and exports every symbol include/lazyrecall.h declares; argument
+checks reject bad calls on the host (no GPU needed, nothing is launched); the torch mirror
+modules expose the reference's function names and reject CPU tensors like the reference."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from code_for_iclr27_amd import _C, _host, _legacy_C, _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "lazyrecall.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(lr_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_loader_agree():
+    assert declared_symbols() == sorted(_lib.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    library = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(library, name), name
+    assert library.lr_abi_version() == 1
+
+
+def test_invalid_arguments_fail_on_host():
+    library = _lib.load()
+    status = library.lr_compact(None, None, None, 10, 0, 2, None, 0, None, None, None, None)
+    assert status == 1 and "Invalid KV layout" in _lib.last_error()
+    status = library.lr_pool(None, 10, None, 1, 4, 2, None, None)
+    assert status == 1 and "Invalid pool configuration" in _lib.last_error()
+    status = library.lr_temporal_risk(None, None, None, None, 4, 2, 10, 5, 5, 1e-6, None, None)
+    assert status == 1 and "Invalid risk interval" in _lib.last_error()
+    assert library.lr_score_workspace_bytes(2, 4, 250, 1000) > 0
+
+
+def test_zero_work_calls_succeed_without_launching():
+    library = _lib.load()
+    assert library.lr_compact(None, None, None, 5, 8, 2, None, 5, None, None, None, None) == 0
+    assert library.lr_merge(None, None, None, 0, None, None, 0, None, 0, 8, 2, None, None, None, None) == 0
+
+
+def test_reference_function_names():
+    for name in ("temporal_probabilities", "temporal_risk", "append", "compact", "pool", "merge",
+                 "pack", "batch_append"):
+        assert callable(getattr(_C, name))
+    for name in ("append_flattened_cache", "compact_flattened_kv", "decision_risk_scores"):
+        assert callable(getattr(_legacy_C, name))
+    assert callable(_host.register_host) and callable(_host.unregister_host)
+
+
+def test_cpu_tensors_rejected_like_reference():
+    keys = torch.zeros(4, 8, dtype=torch.bfloat16)
+    positions = torch.zeros(4, 1)
+    with pytest.raises(RuntimeError, match="Expected contiguous CUDA tensor"):
+        _C.compact(keys, keys, positions, torch.zeros(0, dtype=torch.long))
+    with pytest.raises(RuntimeError, match="cache must be CUDA"):
+        _legacy_C.append_flattened_cache(keys, keys.view(1, 1, 4, 8), torch.zeros(1, dtype=torch.int32),
+                                         torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="Contiguous CUDA states required"):
+        _C.batch_append([keys], [keys], [positions], keys.view(1, 1, 4, 8)[:, :, :1],
+                        keys.view(1, 1, 4, 8)[:, :, :1], [[4]], [4])
+
+
+def test_register_host_failure_raises():
+    with pytest.raises(RuntimeError):
+        _host.register_host(0, 0)
