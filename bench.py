@@ -1,0 +1,314 @@
+#!/usr/bin/env python3
+"""Benchmark of the LazyRecall KV-management hot path on one MI355X.
+
+Headline (BASELINE.json metric): one full audit step on the Llama-3.1-8B cache (cfg1:
+32 layers x 8 KV heads x d128, 2250 tokens per head, window 250, G=4): temporal scores of all
+567,808 candidates -> Pool7 -> allocation-preserving selection of 64,000 slots -> compaction
+of every layer. value = algorithmic bytes of the step / measured step time (GB/s).
+
+Also reported on the same line:
+  roofline      the dominant kernel, timed with HIP events on its stream inside the timed loop
+  stages_us     every stage of the step, same events
+  cpu_baseline  the reference's CPU math path (LAZY_RECALL_BUILD_CUDA=0 semantics, restated in
+                oracle/cpu_path.py) on a bounded sample of the same workload, host cores
+  reinsert      cfg3 recall reinsertion: pinned-host -> HBM copy of 512 recalled K/V rows per
+                (layer, head) (link GB/s) and the merge of all 32 layers (HBM GB/s)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "audit-step KV GB/s (% of HBM peak) + reinsert GB/s, Llama-3.1-8B shape"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[1])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--config", default="cfg1")
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--cpu-seconds", type=float, default=10.0,
+                        help="target CPU work for the bounded CPU-baseline sample")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--no-reinsert", action="store_true", help="skip the cfg3 reinsertion")
+    return parser.parse_args()
+
+
+class EventTimer:
+    """Records a HIP event on the current stream at each mark (events are created up front,
+    outside the timed loop)."""
+
+    def __init__(self, torch, capacity=16):
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(capacity)]
+        self.marks = []
+
+    def mark(self, name):
+        event = self.events[len(self.marks)]
+        event.record()
+        self.marks.append((name, event))
+
+    def stages(self):
+        out = {}
+        for (_, a), (name, b) in zip(self.marks, self.marks[1:]):
+            out[name] = a.elapsed_time(b) * 1000.0  # us
+        return out
+
+
+def audit_bytes(cfg, rows_total, count, candidates_total, segments):
+    """Algorithmic HBM bytes of one audit step (K,V,Q,positions,gradients read once; scores,
+    pool and selection tables once; compaction reads and writes each kept row once)."""
+    T, d, W, G = cfg.length, cfg.dim, cfg.window, cfg.groups
+    heads = cfg.layers * cfg.heads
+    score = heads * (2 * T * d * 2 + W * G * d * 2 + T * 4 + W * 8 + G * d * 4) + candidates_total * 4
+    select = candidates_total * 4 * 4
+    kept = rows_total - count
+    compact = 2 * kept * d * 2 * 2 + kept * 4 * 2 + count * 8
+    return score + select + compact
+
+
+def cpu_baseline(torch, layers, qpos, margin, cfg, target_seconds):
+    from oracle import cpu_path
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    host = []
+    for layer in layers:
+        host.append(dict(keys=layer.keys.cpu(), values=layer.values.cpu(),
+                         positions=layer.positions.cpu(), head_lens=list(layer.head_lens),
+                         queries=layer.queries.cpu(), gradient=layer.gradient.cpu()))
+    qpos_c, margin_c = qpos.cpu(), margin.cpu().reshape(())
+    # calibrate on one layer, then run a whole audit step over as many layers as fit the budget
+    started = time.perf_counter()
+    cpu_path.audit_step_cpu(host[:1], qpos_c, margin_c, cfg.evict_per_head * cfg.heads,
+                            cfg.protect_recent, cfg.pool_kernel, cfg.epsilon)
+    per_layer = time.perf_counter() - started
+    n = max(1, min(len(host), int(target_seconds / max(per_layer, 1e-3))))
+    started = time.perf_counter()
+    cpu_path.audit_step_cpu(host[:n], qpos_c, margin_c, cfg.evict_per_head * cfg.heads * n,
+                            cfg.protect_recent, cfg.pool_kernel, cfg.epsilon)
+    seconds = time.perf_counter() - started
+    scaled = seconds * len(host) / n
+    return n, seconds, scaled, threads
+
+
+def reinsert_bench(torch, seed, reps=5):
+    """cfg3: 32 layers x 8 heads x 33,792 resident tokens, 512 recalled tokens per head held in
+    pinned host memory, reinserted at random hole positions (recall/planning.py merge rule)."""
+    import numpy as np
+
+    from code_for_iclr27_amd import _C, planning
+
+    L, H, d, T, M = 32, 8, 128, 33792, 512
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed + 3)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 3)
+    layers, mappings, positions_all, meta_rows = [], [], [], []
+    for layer in range(L):
+        keys = torch.randn((H * T, d), generator=gen, device=dev).to(torch.bfloat16)
+        values = torch.randn((H * T, d), generator=gen, device=dev).to(torch.bfloat16)
+        pos_parts, meta = [], []
+        for head in range(H):
+            holes = rng.choice(T + M, M, replace=False)
+            keep = np.ones(T + M, bool)
+            keep[holes] = False
+            pos_parts.append(np.flatnonzero(keep))
+            meta.extend((layer, head, int(p)) for p in holes)
+        old = np.concatenate(pos_parts)
+        meta = np.asarray(meta, dtype=np.int64)
+        mapping, lengths = planning.merge_plan(old, [T] * H, meta)
+        positions = torch.from_numpy(old.astype(np.float32)).to(dev)
+        layers.append((keys, values, positions))
+        mappings.append(torch.from_numpy(mapping).to(dev))
+        meta_rows.append(meta)
+    total = L * H * M
+    payload_host = torch.empty((total, 2, d), dtype=torch.bfloat16, pin_memory=True)
+    payload_host.copy_(torch.randn((total, 2, d), generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16))
+    meta_host = torch.empty((total, 3), dtype=torch.int64, pin_memory=True)
+    meta_host.copy_(torch.from_numpy(np.concatenate(meta_rows)))
+    payload = torch.empty((total, 2, d), dtype=torch.bfloat16, device=dev)
+    meta_dev = torch.empty((total, 3), dtype=torch.int64, device=dev)
+    link, merge, outputs = [], [], None
+    for rep in range(reps + 1):
+        torch.cuda.synchronize()
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        e0.record()
+        payload.copy_(payload_host, non_blocking=True)
+        meta_dev.copy_(meta_host, non_blocking=True)
+        e1.record()
+        recalled_positions = meta_dev[:, 2].to(torch.float32)
+        outputs = []
+        for layer in range(L):
+            keys, values, positions = layers[layer]
+            rows = slice(layer * H * M, (layer + 1) * H * M)
+            outputs.append(_C.merge(keys, values, positions, payload[rows],
+                                    recalled_positions[rows], mappings[layer]))
+        e2.record()
+        torch.cuda.synchronize()
+        if rep:  # first repetition warms up
+            link.append(e0.elapsed_time(e1) / 1e3)
+            merge.append(e1.elapsed_time(e2) / 1e3)
+    link_bytes = total * (2 * d * 2 + 3 * 8)
+    n_rows, m_rows = H * T, H * M
+    merge_bytes = L * ((n_rows + m_rows) * 2 * d * 2 * 2 + (n_rows + m_rows) * (4 + 4 + 8))
+    link_s, merge_s = float(np.median(link)), float(np.median(merge))
+    # spot check: every layer's merged positions ascend within each head
+    check = outputs[0][2].reshape(H, T + M).cpu().numpy()
+    assert (np.diff(check, axis=1) > 0).all(), "reinserted positions are not ordered"
+    return {
+        "workload": "cfg3: 32 layers x 8 KV heads x 33,792 tokens, 512 recalled per (layer, head)",
+        "h2d_GBps": round(link_bytes / link_s / 1e9, 2),
+        "h2d_ms": round(link_s * 1e3, 3),
+        "h2d_bytes": link_bytes,
+        "merge_GBps": round(merge_bytes / merge_s / 1e9, 1),
+        "merge_ms": round(merge_s * 1e3, 3),
+        "merge_hbm_fraction": round(merge_bytes / merge_s / 1e9 / HBM_PEAK_GBPS, 3),
+        "merge_bytes": merge_bytes,
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): "
+              "this build has no multi-GPU path; run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from code_for_iclr27_amd import audit, workloads
+
+    dev = torch.device("cuda:0")
+    cfg = workloads.CONFIGS[args.config]
+    layers, qpos, margin = workloads.make_audit(cfg, dev, seed=args.seed, generator_device="cuda")
+    step = audit.AuditStep()
+
+    def run(timer=None):
+        return step.run(layers, qpos, margin, cfg.count, cfg.protect_recent, cfg.pool_kernel,
+                        cfg.epsilon, timer=timer)
+
+    for _ in range(args.warmup):
+        outcome = run()
+    torch.cuda.synchronize()
+    timers = [EventTimer(torch) for _ in range(args.steps)]
+    for timer in timers:  # create the device events before the timed region
+        for event in timer.events:
+            event.record()
+    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
+    started = time.perf_counter()
+    step_ends = []
+    for timer in timers:
+        outcome = run(timer)  # returns after the step's final device->host copy
+        step_ends.append(time.perf_counter())
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - started
+    gc.enable()
+    step_ms = np.diff([started] + step_ends) * 1e3
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    stage_sums = {}
+    for timer in timers:
+        for name, us in timer.stages().items():
+            stage_sums[name] = stage_sums.get(name, 0.0) + us
+    stages = {name: total / len(timers) for name, total in stage_sums.items()}
+    rows_total = sum(layer.keys.size(0) for layer in layers)
+    candidates = int(outcome.scores.numel())
+    segments = len(outcome.segments)
+    nbytes = audit_bytes(cfg, rows_total, outcome.removed, candidates, segments)
+    value = nbytes / (ms_per_step / 1e3) / 1e9
+
+    # dominant kernel roofline: the largest stage
+    dominant = max(stages, key=stages.get)
+    W, G, d = cfg.window, cfg.groups, cfg.dim
+    if dominant in ("column_scores", "row_stats"):
+        keys = candidates if dominant == "column_scores" else rows_total
+        flops = 2.0 * W * G * d * keys
+        achieved = flops / (stages[dominant] / 1e6) / 1e12
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1),
+                    "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                    "algorithmic_flops": flops}
+    else:
+        stage_bytes = {"compact": 2 * (rows_total - outcome.removed) * d * 2 * 2,
+                       "projected_values": rows_total * d * 2}.get(dominant, nbytes)
+        achieved = stage_bytes / (stages[dominant] / 1e6) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: audit step score->pool7->select->compact",
+                   "layers": cfg.layers, "kv_heads": cfg.heads, "head_dim": d, "groups": G,
+                   "tokens_per_head": cfg.length, "window": W, "evicted": outcome.removed,
+                   "candidates": candidates, "batch": 1, "parallelism": "single GPU"},
+        "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes": nbytes,
+        "stages_us": {k: round(v, 1) for k, v in stages.items()},
+        "step_ms_min_median_max": [round(float(np.min(step_ms)), 3), round(float(np.median(step_ms)), 3),
+                                   round(float(np.max(step_ms)), 3)],
+        "roofline": roofline,
+    }
+
+    if not args.no_reinsert:
+        del outcome
+        torch.cuda.empty_cache()
+        line["reinsert"] = reinsert_bench(torch, args.seed)
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        n, seconds, scaled, threads = cpu_baseline(torch, layers, qpos, margin, cfg, args.cpu_seconds)
+        line["cpu_baseline"] = {
+            "value": round(nbytes / scaled / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{cfg.name}: full audit step over the first {n} of {cfg.layers} layers "
+                       f"({n * cfg.heads} heads) took {seconds:.2f} s on the host, scaled by "
+                       f"{cfg.layers}/{n} to {scaled:.2f} s per audit step"),
+            "cpu_model": _cpu_model(),
+        }
+    print(json.dumps(line), flush=True)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    main()

@@ -18,6 +18,7 @@ LIBRARY_PATH = Path(__file__).resolve().parent / "liblazyrecall_hip.so"
 LR_OK = 0
 LR_DTYPE_F32, LR_DTYPE_F64, LR_DTYPE_F16, LR_DTYPE_BF16 = 0, 1, 2, 3
 LR_SEG_WORDS = 12
+LR_HEAD_WORDS = 6
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -47,10 +48,15 @@ SIGNATURES = {
     "lr_unregister_host": [_U64],
     "lr_score_workspace_bytes": [_I64, _I64, _I64, _I64],
     "lr_score_segments": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _F, _D, _P, _SZ,
-                          _P, _P],
+                          _P, _P, _I, _P],
     "lr_debug_segment_logits": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "lr_select_workspace_bytes": [_I64, _I64, _I64],
+    "lr_select_refine": [_P, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P, _P,
+                         _P],
+    "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
 }
-_RESTYPES = {"lr_last_error": ctypes.c_char_p, "lr_score_workspace_bytes": ctypes.c_size_t}
+_RESTYPES = {"lr_last_error": ctypes.c_char_p, "lr_score_workspace_bytes": ctypes.c_size_t,
+             "lr_select_workspace_bytes": ctypes.c_size_t}
 
 _library = None
 

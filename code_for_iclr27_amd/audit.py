@@ -1,0 +1,192 @@
+"""One LazyRecall audit step on the GPU: score -> Pool7 -> select -> compact.
+
+Mirrors LazyController.run_audit (src/lazy_recall/controller.py:140-159) for the KV work it
+drives: compute_score_table (scoring.py:198-308), pool_score_table (scoring.py:322-353),
+allocation_preserving_references / refine_arrays (scoring.py:356-361, selection.py:52-88) and
+the immediate removal LazyRecallCache.remove_positions (cache.py:92-180) of every layer.
+
+The reference runs these as a Python loop of ~4 launches per (layer, head), per-segment
+torch.topk calls with device->host copies, host list -> tensor copies per layer and one
+compaction launch per layer. Here the host builds one int64 metadata block (segment table,
+pool bounds, segment ends, head table), uploads it once from pinned memory, and enqueues:
+3 scoring kernels, 1 pool kernel, 9 selection kernels and 1 compaction kernel covering all
+layers. The only synchronisation is the final copy of the per-segment quotas, which the host
+needs to describe the new ragged layout (as the reference's metadata rebuild does).
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _C, _lib
+from .scoring import LayerState, ScoreSegment, ScoreTable, SegmentPlan, plan_segments
+from .selection import DeviceSelection, SelectWorkspace, select_refine
+
+
+def pool_score_table(table: ScoreTable, kernel_size: int = 7) -> ScoreTable:
+    """scoring.py:322-335 (GPU branch) with this package's ``_C.pool``."""
+    if kernel_size <= 0 or kernel_size % 2 == 0:
+        raise ValueError("pool kernel must be a positive odd integer")
+    started = time.perf_counter()
+    bounds = torch.tensor([0] + list(table.cumulative_ends), dtype=torch.int64,
+                          device=table.scores.device)
+    scores = _C.pool(table.scores.contiguous(), bounds,
+                     max(segment.count for segment in table.segments), kernel_size)
+    return ScoreTable(scores, list(table.segments), list(table.cumulative_ends),
+                      table.score_ms + (time.perf_counter() - started) * 1000.0)
+
+
+@dataclass
+class AuditOutcome:
+    layers: List[LayerState]          # compacted layers (views into one packed K/V/pos buffer)
+    head_lens: List[List[int]]
+    scores: torch.Tensor              # raw temporal scores [S]
+    pooled: torch.Tensor              # Pool7 scores [S]
+    selection: Optional[DeviceSelection]
+    segments: List[ScoreSegment]
+    cumulative_ends: List[int]
+    removed: int
+
+
+class _Workspace:
+    def __init__(self):
+        self.buffers = {}
+
+    def get(self, name: str, nbytes: int, device) -> torch.Tensor:
+        buffer = self.buffers.get(name)
+        if buffer is None or buffer.numel() < nbytes or buffer.device != device:
+            buffer = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=device)
+            self.buffers[name] = buffer
+        return buffer
+
+
+class AuditStep:
+    """Reusable audit-step runner (keeps its scratch buffers between calls)."""
+
+    def __init__(self):
+        self.workspace = _Workspace()
+        self.select_workspace = SelectWorkspace()
+
+    def run(self, layers: Sequence[LayerState], query_positions: torch.Tensor,
+            margin: torch.Tensor, count: int, protect_recent: int = 32, pool_kernel: int = 7,
+            denominator_epsilon: float = 1e-6, check_finite: bool = True,
+            timer=None) -> AuditOutcome:
+        """``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
+        stage, on the current stream, for per-stage event timing."""
+        mark = timer.mark if timer is not None else (lambda name: None)
+        if pool_kernel <= 0 or pool_kernel % 2 == 0:
+            raise ValueError("pool kernel must be a positive odd integer")
+        plan = plan_segments(layers, protect_prompt=True, protect_recent=protect_recent)
+        device = layers[0].keys.device
+        stream = torch.cuda.current_stream(device).cuda_stream
+        segments = len(plan.segments)
+        lengths = plan.head_lengths                                   # [L, H]
+        layer_count, head_count = lengths.shape
+        heads = layer_count * head_count
+        dim = plan.dim
+        elem = 2
+
+        # --- one int64 metadata block, uploaded once -----------------------------------
+        ends = np.asarray(plan.cumulative_ends, dtype=np.int64)
+        starts = plan.table[:, 6].copy()
+        segment_index = np.full(heads, -1, dtype=np.int64)
+        segment_index[plan.layer_of * head_count + plan.head_of] = np.arange(segments)
+        bases = (np.cumsum(lengths, axis=1) - lengths).reshape(-1)
+        layer_of_slot = np.repeat(np.arange(layer_count), head_count)
+        head_table = np.zeros((heads, _lib.LR_HEAD_WORDS), dtype=np.int64)
+        head_table[:, 0] = plan.pointers[layer_of_slot, 0] + bases * dim * elem
+        head_table[:, 1] = plan.pointers[layer_of_slot, 1] + bases * dim * elem
+        head_table[:, 2] = plan.pointers[layer_of_slot, 2] + bases * 4
+        head_table[:, 3] = lengths.reshape(-1)
+        head_table[:, 4] = segment_index
+        max_length = int(lengths.max())
+        pool_bounds = np.concatenate(([0], ends))
+        block = np.concatenate((plan.table.reshape(-1), pool_bounds, ends, starts,
+                                head_table.reshape(-1)))
+        device_block = _C.upload_int64(block, device)
+        cursor = plan.table.size
+        table_d = device_block[:cursor]
+        bounds_d = device_block[cursor:cursor + segments + 1]
+        cursor += segments + 1
+        ends_d = device_block[cursor:cursor + segments]
+        cursor += segments
+        starts_d = device_block[cursor:cursor + segments]
+        cursor += segments
+        heads_d = device_block[cursor:cursor + head_table.size]
+        # quotas and the non-finite score count come back in one small copy at the end
+        info = torch.zeros((segments + 1,), dtype=torch.int64, device=device)
+        nonfinite = info[segments:].view(torch.int32)[:1]
+
+        # --- scores ------------------------------------------------------------------------
+        total = plan.total
+        score_bytes = _lib.load().lr_score_workspace_bytes(
+            segments, plan.groups, plan.window, segments * plan.groups * plan.max_length)
+        score_ws = self.workspace.get("score", score_bytes, device)
+        scores = torch.empty((2 * total,), dtype=torch.float32, device=device)
+        raw, pooled = scores[:total], scores[total:]
+        margin = margin.to(device=device, dtype=torch.float32).reshape(1)
+        stage_names = ("projected_values", "row_stats", "column_scores")
+        stage_masks = (1, 2, 4) if timer is not None else (7,)
+        mark("start")
+        for index, stages in enumerate(stage_masks):
+            _lib.call("lr_score_segments", table_d.data_ptr(), segments, plan.groups,
+                      plan.window, dim, plan.max_length, plan.max_candidates, plan.window,
+                      query_positions.data_ptr(), margin.data_ptr(), float(1.0 / math.sqrt(dim)),
+                      float(denominator_epsilon), score_ws.data_ptr(), score_bytes,
+                      raw.data_ptr(), nonfinite.data_ptr(), stages, stream)
+            mark(stage_names[index] if timer is not None else "score")
+
+        # --- Pool7 -------------------------------------------------------------------------
+        _lib.call("lr_pool", raw.data_ptr(), total, bounds_d.data_ptr(), segments,
+                  plan.max_candidates, pool_kernel, pooled.data_ptr(), stream)
+        mark("pool")
+
+        # --- selection ---------------------------------------------------------------------
+        count = min(max(0, int(count)), total)
+        coordinates = [(s.layer, s.head) for s in plan.segments]
+        selection = select_refine(raw, pooled, plan.cumulative_ends, starts, coordinates, count,
+                                  ends_device=ends_d, starts_device=starts_d,
+                                  workspace=self.select_workspace, quotas_out=info[:segments])
+        mark("select")
+
+        # --- compaction of every layer -----------------------------------------------------
+        total_rows = sum(layer.keys.size(0) for layer in layers)
+        out_rows = total_rows - count
+        out_keys = torch.empty((out_rows, dim), dtype=layers[0].keys.dtype, device=device)
+        out_values = torch.empty_like(out_keys)
+        out_positions = torch.empty((out_rows,), dtype=torch.float32, device=device)
+        if selection is not None:
+            _lib.call("lr_compact_heads", heads_d.data_ptr(), heads, selection.quotas.data_ptr(),
+                      selection.offsets.data_ptr(), selection.removed_positions.data_ptr(), dim,
+                      elem, max_length, out_rows, out_keys.data_ptr(), out_values.data_ptr(),
+                      out_positions.data_ptr(), stream)
+            mark("compact")
+        else:
+            out_keys.copy_(torch.cat([layer.keys for layer in layers]))
+            out_values.copy_(torch.cat([layer.values for layer in layers]))
+            out_positions.copy_(torch.cat([layer.positions.reshape(-1) for layer in layers]))
+        host_info = info.cpu().numpy()  # the step's only synchronisation
+        quotas = host_info[:segments]
+        bad = int(host_info[segments:].view(np.int32)[0])
+        if check_finite and bad:
+            raise RuntimeError("LazyRecall produced non-finite scores; refusing to construct a deletion queue")
+
+        # --- new ragged layout (host metadata, views into the packed buffers) ----------------
+        removed_per_slot = np.where(segment_index >= 0, quotas[np.maximum(segment_index, 0)], 0)
+        kept = (head_table[:, 3] - removed_per_slot).reshape(layer_count, head_count)
+        layer_rows = kept.sum(axis=1).tolist()
+        new_lens = kept.tolist()
+        key_views = torch.split(out_keys, layer_rows)
+        value_views = torch.split(out_values, layer_rows)
+        position_views = torch.split(out_positions, layer_rows)
+        new_layers = [LayerState(k, v, p, lens, layer.prompt_lens, layer.queries, layer.gradient)
+                      for k, v, p, lens, layer in zip(key_views, value_views, position_views,
+                                                      new_lens, layers)]
+        return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan.segments,
+                            plan.cumulative_ends, count)

@@ -275,6 +275,71 @@ __global__ __launch_bounds__(kThreads) void batch_append_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Audit-step compaction of every (layer, KV head) in one launch (the per-layer loop of
+// cache.py:113-178). blockIdx.y = head slot; each head keeps its rows minus the sorted
+// head-relative removal list of its score segment, and lands in one packed output at
+// sum over earlier head slots of (length - quota), derived here from the quotas.
+template <int G>
+__global__ __launch_bounds__(kThreads) void compact_heads_kernel(
+    const int64_t* __restrict__ head_table, const int64_t* __restrict__ quotas,
+    const int64_t* __restrict__ offsets, const int64_t* __restrict__ removed_positions,
+    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions) {
+  __shared__ int64_t partial[kThreads / 64];
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t head = blockIdx.y;
+  // output start of this head slot
+  int64_t before = 0;
+  for (int64_t h = threadIdx.x; h < head; h += kThreads) {
+    const int64_t* row = head_table + h * LR_HEAD_WORDS;
+    before += row[3] - (row[4] >= 0 ? quotas[row[4]] : 0);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o, 64);
+  if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = before;
+  __syncthreads();
+  int64_t out_start = 0;
+  for (int w = 0; w < kThreads / 64; ++w) out_start += partial[w];
+  const int64_t* row = head_table + head * LR_HEAD_WORDS;
+  const uint8_t* keys = reinterpret_cast<const uint8_t*>(row[0]);
+  const uint8_t* values = reinterpret_cast<const uint8_t*>(row[1]);
+  const float* positions = reinterpret_cast<const float*>(row[2]);
+  const int64_t length = row[3], segment = row[4];
+  const int64_t removed_count = segment >= 0 ? quotas[segment] : 0;
+  const int64_t* removed = segment >= 0 ? removed_positions + offsets[segment] : nullptr;
+  const int64_t rows_out = length - removed_count;
+  const int64_t R = layout.rows_per_group;
+  const int64_t rb = layout.row_bytes;
+  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
+       first < rows_out;
+       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
+    int64_t lo = 0, hi = removed_count;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (removed[mid] - mid <= first) lo = mid + 1;
+      else hi = mid;
+    }
+    int64_t src = first + lo;
+    int64_t next = lo;
+    const int64_t end = first + R < rows_out ? first + R : rows_out;
+    for (int64_t r = first; r < end; ++r) {
+      if (r != first) {
+        ++src;
+        while (next < removed_count && removed[next] == src) {
+          ++src;
+          ++next;
+        }
+      }
+      if (src < 0 || src >= length) break;
+      const int64_t dst = out_start + r;
+      copy_row<G>(keys + src * rb, out_keys + dst * rb, layout.chunks, gc.lane, gc.lanes);
+      copy_row<G>(values + src * rb, out_values + dst * rb, layout.chunks, gc.lane, gc.lanes);
+      if (gc.lane == 0) out_positions[dst] = positions[src];
+    }
+  }
+}
+
 inline const uint8_t* bytes(const void* p) { return static_cast<const uint8_t*>(p); }
 inline uint8_t* bytes(void* p) { return static_cast<uint8_t*>(p); }
 
@@ -457,5 +522,32 @@ extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
         descriptors, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
         bytes(out_values), out_positions);
     return check_launch("batch_append");
+  });
+}
+
+extern "C" int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* quotas,
+                                const int64_t* offsets, const int64_t* removed_positions,
+                                int64_t dim, int elem_bytes, int64_t max_length,
+                                int64_t total_out_rows, void* out_keys, void* out_values,
+                                float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Invalid KV layout");
+  LR_REQUIRE(heads > 0 && heads <= 65535 && max_length >= 0, "Invalid head table");
+  if (total_out_rows == 0 || max_length == 0) return LR_OK;
+  LR_REQUIRE(head_table && quotas && offsets && removed_positions && out_keys && out_values &&
+                 out_positions,
+             "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  // Head rows are whole rows of 256-byte aligned allocations; the outputs bound the granule.
+  const int g = granule_for(row_bytes, {out_keys, out_values});
+  const RowLayout layout = make_layout(row_bytes, g, total_out_rows, 8);
+  int64_t bx = ceil_div(ceil_div(max_length, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  if (bx < 1) bx = 1;
+  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads));
+  return dispatch_granule(g, [&]<int G>() {
+    compact_heads_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+        head_table, quotas, offsets, removed_positions, layout, bytes(out_keys),
+        bytes(out_values), out_positions);
+    return check_launch("compact_heads");
   });
 }

@@ -90,35 +90,39 @@ __device__ __forceinline__ double risk64(double margin, double probability, doub
 }
 
 // ---------------------------------------------------------------------------------------
-// 1. Projected values pv[g, t] = grad[g] . V[t] for every key of every segment.
+// 1. Projected values pv[g, t] = grad[g] . V[t] for every key of every segment. A lane group
+// of D/8 lanes reads one V row with 16-byte loads (fully coalesced); each lane forms its
+// 8-column partial dot product per group and the group reduces across its lanes.
 template <int D>
 __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __restrict__ table,
                                                                int64_t groups,
-                                                               float* __restrict__ pv) {
+                                                               float* __restrict__ pv,
+                                                               int* __restrict__ nonfinite) {
+  constexpr int LPR = D / 8;         // lanes per row
+  constexpr int RPB = 256 / LPR;     // rows per block step
   __shared__ float grad[kMaxGroups * D];
   const Segment seg = load_segment(table, blockIdx.y);
+  if (nonfinite != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *nonfinite = 0;
   for (int64_t i = threadIdx.x; i < groups * D; i += 256) grad[i] = seg.gradient[i];
   __syncthreads();
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= seg.length) return;
-  const bf16x8* row = reinterpret_cast<const bf16x8*>(seg.values + t * D);
+  const int lane = threadIdx.x % LPR;
+  const int64_t row_slot = threadIdx.x / LPR;
   float* out = pv + seg.pv_offset;
-  for (int64_t g0 = 0; g0 < groups; g0 += 4) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-    for (int c = 0; c < D / 8; ++c) {
-      const bf16x8 v = row[c];
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * RPB + row_slot; t < seg.length;
+       t += static_cast<int64_t>(gridDim.x) * RPB) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(seg.values + t * D + 8 * lane);
+    float x[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = static_cast<float>(v[e]);
+    for (int e = 0; e < 8; ++e) x[e] = static_cast<float>(v[e]);
+    for (int64_t g = 0; g < groups; ++g) {
+      const float* w = grad + g * D + 8 * lane;
+      float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (g0 + j < groups) acc[j] = __builtin_fmaf(grad[(g0 + j) * D + 8 * c + e], x, acc[j]);
-      }
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w[e], x[e], acc);
+#pragma unroll
+      for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, LPR);
+      if (lane == 0) out[g * seg.length + t] = acc;
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (g0 + j < groups) out[(g0 + j) * seg.length + t] = acc[j];
   }
 }
 
@@ -301,7 +305,7 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     const int64_t* __restrict__ table, int64_t groups, int64_t window, int64_t query_stride,
     const int64_t* __restrict__ query_positions, const float* __restrict__ margin, float scale,
     int64_t tiles_per_segment, const float* __restrict__ pv, const float4* __restrict__ stats,
-    float* __restrict__ scores) {
+    float* __restrict__ scores, int* __restrict__ nonfinite) {
   constexpr int KS = D / 16;
   constexpr int ROW = D + 8;
   __shared__ __bf16 q_lds[2][32 * ROW];
@@ -458,6 +462,7 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     score = static_cast<float>(fmax(risk64(m, p, base, mn), risk64(m, p, base, mx)));
   }
   scores[seg.out_offset + (key - seg.first)] = score;
+  if (nonfinite != nullptr && !isfinite(score)) atomicAdd(nonfinite, 1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -505,20 +510,31 @@ template <int D>
 int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t window,
                  int64_t max_length, int64_t max_candidates, int64_t query_stride,
                  const int64_t* query_positions, const float* margin, float scale, float eps,
-                 float4* stats, float* pv, float* scores, hipStream_t stream) {
-  dim3 pv_grid(static_cast<unsigned>(ceil_div(max_length, 256)), static_cast<unsigned>(segments));
-  projected_values_kernel<D><<<pv_grid, 256, 0, stream>>>(table, groups, pv);
-  if (int rc = check_launch("projected_values")) return rc;
-  const int64_t qtiles = ceil_div(window, 32);
-  const int64_t wg_per_segment = ceil_div(groups * qtiles, 4);
-  row_stats_kernel<D><<<static_cast<unsigned>(segments * wg_per_segment), 256, 0, stream>>>(
-      table, groups, window, query_stride, query_positions, scale, eps, wg_per_segment, pv, stats);
-  if (int rc = check_launch("row_stats")) return rc;
-  const int64_t tiles = ceil_div(max_candidates, kTileKeys);
-  column_scores_kernel<D><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
-      table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
-      scores);
-  return check_launch("column_scores");
+                 float4* stats, float* pv, float* scores, int* nonfinite, int stages,
+                 hipStream_t stream) {
+  if (stages & 1) {
+    constexpr int rows_per_block = 256 / (D / 8);
+    dim3 pv_grid(static_cast<unsigned>(ceil_div(max_length, 4 * rows_per_block)),
+                 static_cast<unsigned>(segments));
+    projected_values_kernel<D><<<pv_grid, 256, 0, stream>>>(table, groups, pv, nonfinite);
+    if (int rc = check_launch("projected_values")) return rc;
+  }
+  if (stages & 2) {
+    const int64_t qtiles = ceil_div(window, 32);
+    const int64_t wg_per_segment = ceil_div(groups * qtiles, 4);
+    row_stats_kernel<D><<<static_cast<unsigned>(segments * wg_per_segment), 256, 0, stream>>>(
+        table, groups, window, query_stride, query_positions, scale, eps, wg_per_segment, pv,
+        stats);
+    if (int rc = check_launch("row_stats")) return rc;
+  }
+  if (stages & 4) {
+    const int64_t tiles = ceil_div(max_candidates, kTileKeys);
+    column_scores_kernel<D><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
+        table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
+        scores, nonfinite);
+    if (int rc = check_launch("column_scores")) return rc;
+  }
+  return LR_OK;
 }
 
 }  // namespace
@@ -538,7 +554,8 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
                                  int64_t max_candidates, int64_t query_group_stride,
                                  const int64_t* query_positions, const float* margin,
                                  float scale, double epsilon, void* workspace,
-                                 size_t workspace_bytes, float* scores, void* stream) {
+                                 size_t workspace_bytes, float* scores, int32_t* nonfinite,
+                                 int stages, void* stream) {
   clear_error();
   LR_REQUIRE(segments > 0 && groups > 0 && window > 0, "Empty attention dimensions");
   LR_REQUIRE(groups <= kMaxGroups, "At most 16 query heads per KV head are supported");
@@ -548,6 +565,7 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
              "Invalid candidate interval");
   LR_REQUIRE(query_group_stride >= window, "Invalid query layout");
   LR_REQUIRE(epsilon > 0.0, "Chunk size and denominator epsilon must be positive");
+  LR_REQUIRE(stages >= 0 && stages <= 7, "stages is a bitmask of 1 | 2 | 4");
   LR_REQUIRE(segment_table && query_positions && margin && workspace && scores,
              "Expected contiguous CUDA tensor");
   LR_REQUIRE(segments * ceil_div(max_candidates, kTileKeys) < (int64_t{1} << 31),
@@ -565,15 +583,15 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
     case 64:
       return launch_score<64>(segment_table, segments, groups, window, max_length, max_candidates,
                               query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                              scores, s);
+                              scores, nonfinite, stages == 0 ? 7 : stages, s);
     case 128:
       return launch_score<128>(segment_table, segments, groups, window, max_length, max_candidates,
                                query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                               scores, s);
+                               scores, nonfinite, stages == 0 ? 7 : stages, s);
     default:
       return launch_score<256>(segment_table, segments, groups, window, max_length, max_candidates,
                                query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                               scores, s);
+                               scores, nonfinite, stages == 0 ? 7 : stages, s);
   }
 }
 

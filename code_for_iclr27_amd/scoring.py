@@ -105,6 +105,10 @@ class SegmentPlan:
     max_length: int
     max_candidates: int
     projected_floats: int
+    layer_of: Optional[np.ndarray] = None   # segment -> layer
+    head_of: Optional[np.ndarray] = None    # segment -> KV head
+    head_lengths: Optional[np.ndarray] = None  # [layers, heads] lengths of every head
+    pointers: Optional[np.ndarray] = None   # [layers, 5] keys/values/positions/queries/gradient
 
     @property
     def total(self) -> int:
@@ -116,75 +120,106 @@ def _require(condition: bool, message: str) -> None:
         raise RuntimeError(message)
 
 
+def _validate_layer(layer: LayerState, hq: int, window: int, dim: int, device) -> None:
+    """Detailed checks with the error messages; only run when the fast check fails."""
+    keys, values, positions = layer.keys, layer.values, layer.positions
+    for tensor in (keys, values, positions, layer.queries, layer.gradient):
+        _require(tensor.is_cuda and tensor.is_contiguous() and tensor.device == device,
+                 "Expected contiguous CUDA tensor")
+    _require(keys.dtype == torch.bfloat16 and values.dtype == torch.bfloat16
+             and layer.queries.dtype == torch.bfloat16,
+             "The fused scorer takes bf16 keys, values and queries")
+    _require(keys.dim() == 2 and keys.shape == values.shape and keys.size(1) == dim,
+             "Invalid KV layout")
+    _require(positions.dtype == torch.float32 and positions.numel() == keys.size(0),
+             "Invalid positions")
+    _require(tuple(layer.queries.shape) == (hq, window, dim), "Historical query-head count changed")
+    _require(layer.gradient.dtype == torch.float32 and tuple(layer.gradient.shape) == (hq, dim),
+             "Invalid margin gradient")
+    for tensor in (keys, values, layer.queries):
+        _require(tensor.data_ptr() % 16 == 0, "bf16 operands must be 16-byte aligned")
+    heads = len(layer.head_lens)
+    _require(heads > 0 and hq % heads == 0, "Query heads must be a multiple of KV heads")
+    _require(int(np.sum(layer.head_lens)) == keys.size(0), "Position/KV lengths differ")
+    raise RuntimeError("Inconsistent layer state")
+
+
 def plan_segments(layers: Sequence[LayerState], protect_prompt: bool = True,
                   protect_recent: int = 32) -> SegmentPlan:
-    """Validate the layers and build the device segment table (host side, no GPU work)."""
+    """Validate the layers and build the device segment table (host side, no GPU work).
+    Every head of every layer is planned in one vectorised pass."""
     _require(len(layers) > 0, "No layers to score")
     first_layer = layers[0]
     hq, window, dim = first_layer.queries.shape
     device = first_layer.keys.device
-    words = _lib.LR_SEG_WORDS
-    rows_out, segments, ends, head_starts = [], [], [], []
-    running = projected = 0
-    max_length = max_candidates = 0
-    groups = None
-    for layer_index, layer in enumerate(layers):
-        keys, values, positions = layer.keys, layer.values, layer.positions
-        for tensor in (keys, values, positions, layer.queries, layer.gradient):
-            _require(tensor.is_cuda and tensor.is_contiguous() and tensor.device == device,
-                     "Expected contiguous CUDA tensor")
-        _require(keys.dtype == torch.bfloat16 and values.dtype == torch.bfloat16
-                 and layer.queries.dtype == torch.bfloat16,
-                 "The fused scorer takes bf16 keys, values and queries")
-        _require(keys.dim() == 2 and keys.shape == values.shape and keys.size(1) == dim,
-                 "Invalid KV layout")
-        _require(positions.dtype == torch.float32 and positions.numel() == keys.size(0),
-                 "Invalid positions")
-        _require(layer.queries.shape == (hq, window, dim), "Historical query-head count changed")
-        _require(layer.gradient.dtype == torch.float32 and layer.gradient.shape == (hq, dim),
-                 "Invalid margin gradient")
-        for tensor in (keys, values, layer.queries):
-            _require(tensor.data_ptr() % 16 == 0, "bf16 operands must be 16-byte aligned")
-        heads = len(layer.head_lens)
-        _require(heads > 0 and hq % heads == 0, "Query heads must be a multiple of KV heads")
-        layer_groups = hq // heads
-        _require(groups is None or groups == layer_groups, "Group count differs between layers")
-        groups = layer_groups
-        lengths = np.asarray(layer.head_lens, dtype=np.int64)
-        _require(int(lengths.sum()) == keys.size(0), "Position/KV lengths differ")
-        bounds = np.concatenate(([0], np.cumsum(lengths)))
-        for head in range(heads):
-            length = int(lengths[head])
-            start = 0
-            if protect_prompt and layer.prompt_lens is not None:
-                start = int(layer.prompt_lens[head])
-            end = max(start, length - protect_recent)
-            if end <= start:
-                continue
-            base = int(bounds[head])
-            row = np.zeros(words, dtype=np.int64)
-            row[0] = keys.data_ptr() + base * dim * 2
-            row[1] = values.data_ptr() + base * dim * 2
-            row[2] = positions.data_ptr() + base * 4
-            row[3] = layer.queries.data_ptr() + head * groups * window * dim * 2
-            row[4] = layer.gradient.data_ptr() + head * groups * dim * 4
-            row[5], row[6], row[7] = length, start, end
-            row[8] = running
-            row[9] = len(segments) * groups * window
-            row[10] = projected
-            rows_out.append(row)
-            count = end - start
-            segments.append(ScoreSegment(layer_index, head, start, count))
-            head_starts.append(base)
-            running += count
-            ends.append(running)
-            projected += groups * length
-            max_length = max(max_length, length)
-            max_candidates = max(max_candidates, count)
-    if not segments:
+    bf16, f32 = torch.bfloat16, torch.float32
+    count = len(layers)
+    pointers = np.empty((count, 5), dtype=np.int64)
+    rows = np.empty(count, dtype=np.int64)
+    heads = len(first_layer.head_lens)
+    lengths_list, prompts_list = [], []
+    any_prompt = False
+    qshape, gshape = (hq, window, dim), (hq, dim)
+    for index, layer in enumerate(layers):
+        k, v, p, q, g = layer.keys, layer.values, layer.positions, layer.queries, layer.gradient
+        kp, vp, qp = k.data_ptr(), v.data_ptr(), q.data_ptr()
+        ok = (k.dtype == bf16 and v.dtype == bf16 and q.dtype == bf16 and p.dtype == f32
+              and g.dtype == f32 and k.device == device and v.device == device
+              and p.device == device and q.device == device and g.device == device
+              and k.dim() == 2 and k.shape == v.shape and k.shape[1] == dim
+              and p.numel() == k.shape[0] and q.shape == qshape and g.shape == gshape
+              and k.is_contiguous() and v.is_contiguous() and p.is_contiguous()
+              and q.is_contiguous() and g.is_contiguous() and (kp | vp | qp) % 16 == 0
+              and len(layer.head_lens) == heads and k.is_cuda)
+        if not ok:
+            _require(len(layer.head_lens) == heads, "Every layer must have the same number of KV heads")
+            _validate_layer(layer, hq, window, dim, device)
+        pointers[index] = (kp, vp, p.data_ptr(), qp, g.data_ptr())
+        rows[index] = k.shape[0]
+        lengths_list.append(layer.head_lens)
+        if protect_prompt and layer.prompt_lens is not None:
+            any_prompt = True
+        prompts_list.append(layer.prompt_lens)
+    _require(heads > 0 and hq % heads == 0, "Query heads must be a multiple of KV heads")
+    groups = hq // heads
+    lengths = np.asarray(lengths_list, dtype=np.int64)                      # [L, H]
+    if not np.array_equal(lengths.sum(axis=1), rows):
+        for layer in layers:
+            _validate_layer(layer, hq, window, dim, device)
+    bases = np.cumsum(lengths, axis=1) - lengths                            # row of each head
+    starts = np.zeros_like(lengths)
+    if any_prompt:
+        for index, prompt in enumerate(prompts_list):
+            if prompt is not None:
+                starts[index] = np.asarray(prompt, dtype=np.int64)
+    ends = np.maximum(starts, lengths - protect_recent)
+    layer_of, head_of = np.nonzero(ends > starts)                            # row-major order
+    if not layer_of.size:
         raise RuntimeError("No eligible KV remains after prompt/recent protection")
-    return SegmentPlan(np.stack(rows_out), segments, ends, head_starts, groups, window, dim,
-                       max_length, max_candidates, projected)
+    base = bases[layer_of, head_of]
+    seg_lengths = lengths[layer_of, head_of]
+    seg_starts = starts[layer_of, head_of]
+    seg_ends = ends[layer_of, head_of]
+    counts = seg_ends - seg_starts
+    table = np.zeros((layer_of.size, _lib.LR_SEG_WORDS), dtype=np.int64)
+    table[:, 0] = pointers[layer_of, 0] + base * dim * 2
+    table[:, 1] = pointers[layer_of, 1] + base * dim * 2
+    table[:, 2] = pointers[layer_of, 2] + base * 4
+    table[:, 3] = pointers[layer_of, 3] + head_of * groups * window * dim * 2
+    table[:, 4] = pointers[layer_of, 4] + head_of * groups * dim * 4
+    table[:, 5] = seg_lengths
+    table[:, 6] = seg_starts
+    table[:, 7] = seg_ends
+    cumulative = np.cumsum(counts)
+    table[:, 8] = cumulative - counts
+    table[:, 9] = np.arange(layer_of.size, dtype=np.int64) * groups * window
+    projected = np.cumsum(groups * seg_lengths)
+    table[:, 10] = projected - groups * seg_lengths
+    segments = list(map(ScoreSegment, layer_of.tolist(), head_of.tolist(), seg_starts.tolist(),
+                        counts.tolist()))
+    return SegmentPlan(table, segments, cumulative.tolist(), base.tolist(), groups, window, dim,
+                       int(seg_lengths.max()), int(counts.max()), int(projected[-1]),
+                       layer_of, head_of, lengths, pointers)
 
 
 def score_plan(plan: SegmentPlan, query_positions: torch.Tensor, margin: torch.Tensor,
@@ -206,7 +241,7 @@ def score_plan(plan: SegmentPlan, query_positions: torch.Tensor, margin: torch.T
                   plan.dim, plan.max_length, plan.max_candidates, plan.window,
                   query_positions.data_ptr(), margin.data_ptr(),
                   float(1.0 / math.sqrt(plan.dim)), float(denominator_epsilon),
-                  workspace.data_ptr(), workspace_bytes, scores.data_ptr(),
+                  workspace.data_ptr(), workspace_bytes, scores.data_ptr(), None, 0,
                   _lib.stream_of(scores))
     return scores
 

@@ -1,0 +1,157 @@
+"""Allocation-preserving selection on the GPU (src/lazy_recall/selection.py).
+
+``ArrayReferences`` keeps the reference's queue type and API (selection.py:8-39).
+``select_refine`` runs refine_arrays + transplant (selection.py:42-88) entirely on the device
+(``lr_select_refine``) and returns device tensors without synchronising; ``refine_arrays``
+wraps it with the reference's signature and host return values.
+
+Tie rule: where equal scores straddle a bottom-k cut, the lower index is taken (the order of
+a stable sort by (score, index)). The reference defers to torch.topk, whose choice inside such
+a tie group is unspecified; outside tie groups the two agree exactly.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass
+from typing import List, Sequence as Seq
+
+import numpy as np
+import torch
+
+from . import _C, _lib
+
+
+class ArrayReferences(Sequence):
+    """selection.py:8-39: parallel (score, segment, position) columns of a deletion queue."""
+
+    def __init__(self, scores, segments, positions, coordinates):
+        self.scores = np.asarray(scores)
+        self.segments = np.asarray(segments, dtype=np.int64)
+        self.positions = np.asarray(positions, dtype=np.int64)
+        self.coordinates = np.asarray(coordinates, dtype=np.int64).reshape(-1, 2)
+        if len(self.scores) != len(self.segments) or len(self.scores) != len(self.positions):
+            raise ValueError("Queue column lengths differ")
+
+    def __len__(self):
+        return len(self.positions)
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            return ArrayReferences(self.scores[index], self.segments[index],
+                                   self.positions[index], self.coordinates)
+        layer, head = self.coordinates[self.segments[index]]
+        return (float(self.scores[index]), int(layer), int(head), int(self.positions[index]))
+
+    def groups(self):
+        """Per (layer, head), the sorted positions of its queued slots."""
+        if not len(self):
+            return {}
+        order = np.argsort(self.segments, kind="stable")
+        sorted_segments = self.segments[order]
+        boundaries = np.flatnonzero(sorted_segments[1:] != sorted_segments[:-1]) + 1
+        grouped = {}
+        for indexes in np.split(order, boundaries):
+            layer, head = self.coordinates[self.segments[indexes[0]]]
+            grouped[(int(layer), int(head))] = np.sort(self.positions[indexes])
+        return grouped
+
+
+@dataclass
+class DeviceSelection:
+    """Result of lr_select_refine, resident on the device."""
+    values: torch.Tensor             # f32 [count] ascending raw scores
+    segments: torch.Tensor           # i64 [count]
+    positions: torch.Tensor          # i64 [count] transplanted refined positions
+    quotas: torch.Tensor             # i64 [S] picks per segment
+    offsets: torch.Tensor            # i64 [S + 1] exclusive prefix of quotas
+    removed_positions: torch.Tensor  # i64 [count] per-segment ascending positions
+    changed: torch.Tensor            # i64 [S] refined picks absent from the raw picks
+    coordinates: List[tuple]
+
+    def references(self) -> ArrayReferences:
+        return ArrayReferences(self.values.cpu().numpy(), self.segments.cpu().numpy(),
+                               self.positions.cpu().numpy(), self.coordinates)
+
+    def change_counts(self):
+        changed = self.changed.cpu().numpy()
+        return int(changed.sum()), int(np.count_nonzero(changed))
+
+
+class SelectWorkspace:
+    """Grow-only device workspace reused across calls on one stream."""
+
+    def __init__(self):
+        self.buffer = None
+
+    def get(self, nbytes: int, device) -> torch.Tensor:
+        if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
+            self.buffer = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=device)
+        return self.buffer
+
+
+_workspace = SelectWorkspace()
+
+
+def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[int],
+                  position_starts: Seq[int], coordinates, count: int,
+                  ends_device: torch.Tensor | None = None,
+                  starts_device: torch.Tensor | None = None,
+                  workspace: SelectWorkspace | None = None,
+                  quotas_out: torch.Tensor | None = None) -> DeviceSelection | None:
+    """Launch the device selection; returns None when nothing is selected. ``ends_device`` /
+    ``starts_device`` may be passed pre-uploaded (i64 device tensors); ``quotas_out`` (i64
+    device [segments]) receives the quotas when given."""
+    total = raw.numel()
+    segments = len(cumulative_ends)
+    count = min(max(0, int(count)), total)
+    if not count:
+        return None
+    if not (raw.is_cuda and pooled.is_cuda and raw.is_contiguous() and pooled.is_contiguous()
+            and raw.dtype == torch.float32 and pooled.dtype == torch.float32
+            and pooled.numel() == total):
+        raise RuntimeError("Allocation and refinement layouts differ")
+    device = raw.device
+    if ends_device is None or starts_device is None:
+        table = _C.upload_int64(np.stack((np.asarray(cumulative_ends, np.int64),
+                                          np.asarray(position_starts, np.int64))), device)
+        ends_device, starts_device = table[0], table[1]
+    workspace = workspace or _workspace
+    nbytes = _lib.load().lr_select_workspace_bytes(total, segments, count)
+    buffer = workspace.get(nbytes, device)
+    out = torch.empty((3 * count + 2 * segments + 1,), dtype=torch.int64, device=device)
+    values = torch.empty((count,), dtype=torch.float32, device=device)
+    seg_ids, positions, removed = out[:count], out[count:2 * count], out[2 * count:3 * count]
+    quotas = out[3 * count:3 * count + segments] if quotas_out is None else quotas_out
+    offsets_changed = torch.empty((2 * segments + 1,), dtype=torch.int64, device=device)
+    offsets, changed = offsets_changed[:segments + 1], offsets_changed[segments + 1:]
+    _lib.call("lr_select_refine", raw.data_ptr(), pooled.data_ptr(), total,
+              ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
+              buffer.data_ptr(), buffer.numel(), values.data_ptr(), seg_ids.data_ptr(),
+              positions.data_ptr(), quotas.data_ptr(), offsets.data_ptr(), removed.data_ptr(),
+              changed.data_ptr(), _lib.stream_of(raw))
+    return DeviceSelection(values, seg_ids, positions, quotas, offsets, removed, changed,
+                           list(coordinates))
+
+
+def refine_arrays(allocation, refinement, count):
+    """selection.py:52-88 signature: (ArrayReferences, changed, changed_heads)."""
+    if (allocation.segments != refinement.segments
+            or allocation.cumulative_ends != refinement.cumulative_ends):
+        raise ValueError("Allocation and refinement layouts differ")
+    coordinates = [(segment.layer, segment.head) for segment in allocation.segments]
+    if len(set(coordinates)) != len(coordinates):
+        raise ValueError("Each physical head must have exactly one score segment")
+    ends = np.asarray(allocation.cumulative_ends, dtype=np.int64)
+    starts = np.concatenate(([0], ends[:-1]))
+    if ends[-1] != allocation.scores.numel() or any(
+            end - start != segment.count for start, end, segment in zip(starts, ends, allocation.segments)):
+        raise ValueError("Invalid segment bounds")
+    result = select_refine(allocation.scores.contiguous(), refinement.scores.contiguous(),
+                           allocation.cumulative_ends,
+                           [segment.position_start for segment in allocation.segments],
+                           coordinates, count)
+    if result is None:
+        return ArrayReferences([], [], [], coordinates), 0, 0
+    changed, changed_heads = result.change_counts()
+    return result.references(), changed, changed_heads

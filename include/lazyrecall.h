@@ -169,18 +169,57 @@ size_t lr_score_workspace_bytes(int64_t segments, int64_t groups, int64_t window
  * bf16 Q.K^T, temporal_probabilities, temporal_risk, maximum over query chunks) for all heads of
  * compute_score_table (src/lazy_recall/scoring.py:218-287) at once, without materialising
  * logits or probabilities. query_positions [window] i64, margin [1] f32 (device).
- * query_group_stride is in rows of `dim` elements. scores gets sum(last - first) floats. */
+ * query_group_stride is in rows of `dim` elements. scores gets sum(last - first) floats.
+ * nonfinite (device i32, may be NULL) receives the number of non-finite scores, so callers can
+ * refuse a table (src/lazy_recall/scoring.py:292-293) without a separate reduction.
+ * stages: 0 (or 7) runs the whole scorer; otherwise a bitmask of 1 = projected values,
+ * 2 = row statistics, 4 = column scores, run in that order (for per-kernel timing; each stage
+ * needs the earlier ones to have run on the same workspace). */
 int lr_score_segments(const int64_t* segment_table, int64_t segments, int64_t groups,
                       int64_t window, int64_t dim, int64_t max_length, int64_t max_candidates,
                       int64_t query_group_stride, const int64_t* query_positions,
                       const float* margin, float scale, double epsilon, void* workspace,
-                      size_t workspace_bytes, float* scores, void* stream);
+                      size_t workspace_bytes, float* scores, int32_t* nonfinite, int stages,
+                      void* stream);
 
 /* Test hook for the parity suite: the bf16 logits Q.K^T exactly as lr_score_segments forms them
  * (same MFMA sequence), for one segment: out [groups, window, length] bf16 (raw, unscaled). */
 int lr_debug_segment_logits(const int64_t* segment_table, int64_t segment, int64_t groups,
                             int64_t window, int64_t dim, int64_t length,
                             int64_t query_group_stride, uint16_t* out, void* stream);
+
+/* Bytes of workspace lr_select_refine needs for a table of `total` scores. */
+size_t lr_select_workspace_bytes(int64_t total, int64_t segments, int64_t count);
+
+/* Allocation-preserving Pool7 selection (src/lazy_recall/selection.py:52-88,
+ * refine_arrays + transplant) on the device. raw/pooled [total] f32 score tables,
+ * segment_ends [segments] i64 (cumulative ends) and position_starts [segments] i64 (device).
+ * count in [1, total]. Ties at the cut go to the lower index in both bottom-k steps.
+ * Outputs (device): out_values f32 [count] ascending raw scores; out_segments i64 [count];
+ * out_positions i64 [count] (position_start + refined local index, transplanted);
+ * quotas i64 [segments]; offsets i64 [segments + 1] (exclusive prefix of quotas);
+ * removed_positions i64 [count] (each segment's refined positions, ascending, at its offset);
+ * changed i64 [segments] (refined picks absent from the raw picks). */
+int lr_select_refine(const float* raw, const float* pooled, int64_t total,
+                     const int64_t* segment_ends, const int64_t* position_starts,
+                     int64_t segments, int64_t count, void* workspace, size_t workspace_bytes,
+                     float* out_values, int64_t* out_segments, int64_t* out_positions,
+                     int64_t* quotas, int64_t* offsets, int64_t* removed_positions,
+                     int64_t* changed, void* stream);
+
+/* One head slot per (layer, KV head), LR_HEAD_WORDS i64 each (device):
+ *   [0] keys ptr, [1] values ptr, [2] positions ptr (this head's first row),
+ *   [3] length, [4] score-segment index or -1, [5] unused (0). */
+#define LR_HEAD_WORDS 6
+
+/* Removes every segment's `removed_positions` (from lr_select_refine) from its head and packs
+ * all heads, in head-slot order, into one output [total_out_rows, dim] + positions
+ * [total_out_rows] f32 (the compaction loop of src/lazy_recall/cache.py:113-178 for all layers
+ * at once). max_length = largest head length. */
+int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* quotas,
+                     const int64_t* offsets, const int64_t* removed_positions, int64_t dim,
+                     int elem_bytes, int64_t max_length, int64_t total_out_rows,
+                     void* out_keys, void* out_values, float* out_positions, void* stream);
 
 #ifdef __cplusplus
 }
