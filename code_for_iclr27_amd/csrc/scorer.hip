@@ -22,6 +22,7 @@
 // in k-step ks, so each lane reads one contiguous half row. The accumulator element r of a
 // lane is (key 8*(r/4) + 4*half + r%4, query col).
 #include <cmath>
+#include <type_traits>
 
 #include "lr_common.hpp"
 
@@ -29,7 +30,18 @@ namespace lr {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Loads through the global address space (the segment table holds generic pointers; casting
+// lets the compiler emit global_load instead of flat_load).
+template <typename T>
+__device__ __forceinline__ T gload(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxGroups = 16;
@@ -73,6 +85,15 @@ __device__ __forceinline__ float logit_value(float acc, float scale) {
 }
 
 __device__ __forceinline__ int acc_key(int r, int half) { return 8 * (r >> 2) + 4 * half + (r & 3); }
+
+// logit_value for two accumulators at once: one v_cvt_pk_bf16_f32 per rounding step.
+__device__ __forceinline__ f32x2 logit_pair(float a, float b, float scale) {
+  const f32x2 v = {a, b};
+  const f32x2 once = __builtin_convertvector(__builtin_convertvector(v, bf16x2), f32x2) * scale;
+  return __builtin_convertvector(__builtin_convertvector(once, bf16x2), f32x2);
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ f32x16 mfma_tile_zero() {
   f32x16 z;
@@ -140,8 +161,10 @@ struct TileStager {
       const int c = threadIdx.x + 256 * i;
       const int row = c / (D / 8), part = c % (D / 8);
       data[i] = make_uint4(0, 0, 0, 0);
-      if (c < kChunks && row < valid_rows)
-        data[i] = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(row) * D + 8 * part);
+      if (c < kChunks && row < valid_rows) {
+        const u32x4 v = gload<u32x4>(base + static_cast<int64_t>(row) * D + 8 * part);
+        data[i] = make_uint4(v.x, v.y, v.z, v.w);
+      }
     }
   }
   __device__ __forceinline__ void store(__bf16* lds) const {
@@ -161,39 +184,41 @@ struct TileStager {
 // exp(z - m) and op = sum exp(z - m) * pv / S; {NaN x4} for a fully masked row.
 template <int D>
 __global__ __launch_bounds__(256) void row_stats_kernel(
-    const int64_t* __restrict__ table, int64_t groups, int64_t window, int64_t query_stride,
+    const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, float scale, float epsilon,
     int64_t wg_per_segment, const float* __restrict__ pv, float4* __restrict__ stats) {
   constexpr int KS = D / 16;
   constexpr int ROW = D + 8;
-  __shared__ __bf16 k_lds[2][32 * ROW];
-  __shared__ float pv_lds[2][kMaxGroups * 32];
-  __shared__ float kpos_lds[2][32];
+  __shared__ __bf16 k_lds[2][64 * ROW];
+  __shared__ float pv_lds[2][kMaxGroups * 64];
+  __shared__ float kpos_lds[2][64];
   __shared__ float kmax_lds[2];
 
-  const int64_t s = blockIdx.x / wg_per_segment;
-  const int64_t wg = blockIdx.x % wg_per_segment;
+  const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
+  const int per = static_cast<int>(wg_per_segment);
+  const int s = blockIdx.x / per;
+  const int wg = blockIdx.x - s * per;
   const Segment seg = load_segment(table, s);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int half = lane >> 5, col = lane & 31;
-  const int64_t qtiles = (window + 31) / 32;
-  const int64_t task = wg * 4 + wave;
+  const int qtiles = (window + 31) / 32;
+  const int task = wg * 4 + wave;
   const bool active = task < groups * qtiles;
-  const int64_t g = active ? task / qtiles : 0;
-  const int64_t query = (active ? task % qtiles : 0) * 32 + col;
+  const int g = active ? task / qtiles : 0;
+  const int query = (active ? task - (task / qtiles) * qtiles : 0) * 32 + col;
   const bool query_valid = active && query < window;
   const float query_position =
       query_valid ? static_cast<float>(query_positions[query]) : -INFINITY;
 
   bf16x8 qop[KS];
   {
-    const __bf16* qrow = seg.queries + (g * query_stride + query) * D + half * (D / 2);
+    const __bf16* qrow = seg.queries + (static_cast<int64_t>(g) * query_stride + query) * D + half * (D / 2);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       bf16x8 v;
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = static_cast<__bf16>(0.0f);
-      if (query_valid) v = *reinterpret_cast<const bf16x8*>(qrow + 8 * ks);
+      if (query_valid) v = gload<bf16x8>(qrow + 8 * ks);
       qop[ks] = v;
     }
   }
@@ -201,81 +226,108 @@ __global__ __launch_bounds__(256) void row_stats_kernel(
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) qmin = fminf(qmin, __shfl_xor(qmin, o, 64));
 
-  const int64_t length = seg.length;
-  const int64_t ktiles = (length + 31) / 32;
+  const int length = static_cast<int>(seg.length);
+  const int ktiles = (length + 63) / 64;  // 64-key stages: two 32-key MFMA tiles each
   const float* pv_seg = pv + seg.pv_offset;
 
-  TileStager<D> stager;
-  float pv_reg[2] = {0.0f, 0.0f};
+  TileStager<D> stager_a, stager_b;
+  float pv_reg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float kpos_reg = INFINITY;
-  auto fetch = [&](int64_t kt) {
-    const int64_t t0 = kt * 32;
-    stager.load(seg.keys + t0 * D, length - t0);
+  auto fetch = [&](int kt) {
+    const int t0 = kt * 64;
+    stager_a.load(seg.keys + static_cast<int64_t>(t0) * D, length - t0);
+    stager_b.load(seg.keys + static_cast<int64_t>(t0 + 32) * D, length - t0 - 32);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int idx = threadIdx.x + 256 * i;
-      const int gg = idx / 32, k = idx % 32;
-      pv_reg[i] = (gg < groups && t0 + k < length) ? pv_seg[gg * length + t0 + k] : 0.0f;
+      const int gg = idx >> 6, k = idx & 63;
+      pv_reg[i] = (gg < groups && t0 + k < length) ? gload<float>(pv_seg + static_cast<int64_t>(gg) * length + t0 + k) : 0.0f;
     }
-    kpos_reg = (threadIdx.x < 32 && t0 + threadIdx.x < length) ? seg.key_positions[t0 + threadIdx.x]
-                                                                : INFINITY;
+    kpos_reg = (threadIdx.x < 64 && t0 + static_cast<int>(threadIdx.x) < length)
+                   ? gload<float>(seg.key_positions + t0 + threadIdx.x)
+                   : INFINITY;
   };
   auto commit = [&](int buf) {
-    stager.store(k_lds[buf]);
+    stager_a.store(k_lds[buf]);
+    stager_b.store(k_lds[buf] + 32 * ROW);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int idx = threadIdx.x + 256 * i;
-      if (idx < kMaxGroups * 32) pv_lds[buf][idx] = pv_reg[i];
+      if (idx < kMaxGroups * 64) pv_lds[buf][idx] = pv_reg[i];
     }
-    if (threadIdx.x < 32) {
+    if (threadIdx.x < 64) {
       kpos_lds[buf][threadIdx.x] = kpos_reg;
       float m = kpos_reg;
 #pragma unroll
-      for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
       if (threadIdx.x == 0) kmax_lds[buf] = m;
     }
   };
 
   float m_run = -INFINITY, S = 0.0f, A = 0.0f;
+  // One 64-key stage: 32 logits of this lane (two 32-key tiles, keys acc_key(r, half)).
+  auto stage = [&](int buf, auto masked) {
+    constexpr bool kMask = decltype(masked)::value;
+    float z[32];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      bf16x8 a[KS];
+      const __bf16* arow = k_lds[buf] + (32 * t + col) * ROW + half * (D / 2);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) a[ks] = *reinterpret_cast<const bf16x8*>(arow + 8 * ks);
+      f32x16 acc = mfma_tile_zero();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], qop[ks], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const f32x2 v = logit_pair(acc[r], acc[r + 1], scale);
+        z[16 * t + r] = v.x;
+        z[16 * t + r + 1] = v.y;
+      }
+    }
+    if constexpr (kMask) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const f32x4 kp = *reinterpret_cast<const f32x4*>(&kpos_lds[buf][8 * c + 4 * half]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) z[4 * c + j] = kp[j] <= query_position ? z[4 * c + j] : -INFINITY;
+      }
+    }
+    float tile_max = z[0];
+#pragma unroll
+    for (int r = 1; r < 32; ++r) tile_max = fmaxf(tile_max, z[r]);
+    const float m_new = fmaxf(m_run, tile_max);
+    const float factor = (m_run == m_new) ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
+    S *= factor;
+    A *= factor;
+    const float nml = (m_new == -INFINITY) ? 0.0f : -m_new * kLog2e;
+    const float* pv_row = pv_lds[buf] + g * 64;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z[4 * c + j], kLog2e, nml));
+        S += e;
+        A = __builtin_fmaf(e, w[j], A);
+      }
+    }
+    m_run = m_new;
+  };
+
   fetch(0);
   commit(0);
   __syncthreads();
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
+  for (int kt = 0; kt < ktiles; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < ktiles) fetch(kt + 1);
+    const bool more = kt + 1 < ktiles;
+    if (more) fetch(kt + 1);
     if (active) {
-      f32x16 acc = mfma_tile_zero();
-      const __bf16* arow = k_lds[buf] + col * ROW + half * (D / 2);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + 8 * ks);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[ks], acc, 0, 0, 0);
-      }
-      const bool need_mask = kmax_lds[buf] > qmin;
-      float z[16];
-      float tile_max = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = logit_value(acc[r], scale);
-        if (need_mask) v = kpos_lds[buf][acc_key(r, half)] <= query_position ? v : -INFINITY;
-        z[r] = v;
-        tile_max = fmaxf(tile_max, v);
-      }
-      const float m_new = fmaxf(m_run, tile_max);
-      const float factor = (m_run == m_new) ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
-      S *= factor;
-      A *= factor;
-      const float nml = (m_new == -INFINITY) ? 0.0f : -m_new * kLog2e;
-      const float* pv_row = pv_lds[buf] + g * 32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z[r], kLog2e, nml));
-        S += e;
-        A = __builtin_fmaf(e, pv_row[acc_key(r, half)], A);
-      }
-      m_run = m_new;
+      if (uniform(kmax_lds[buf] > qmin ? 1 : 0)) stage(buf, std::true_type{});
+      else stage(buf, std::false_type{});
     }
-    if (kt + 1 < ktiles) commit(buf ^ 1);
+    if (more) commit(buf ^ 1);
     __syncthreads();
   }
   // Merge the two half-waves (same query, disjoint keys).
@@ -294,7 +346,7 @@ __global__ __launch_bounds__(256) void row_stats_kernel(
     const float weighted = A * f1 + A_other * f2;
     out = make_float4(-m * kLog2e, total, epsilon * total, weighted / total);
   }
-  stats[seg.stats_offset + g * window + query] = out;
+  stats[seg.stats_offset + static_cast<int64_t>(g) * window + query] = out;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -302,63 +354,66 @@ __global__ __launch_bounds__(256) void row_stats_kernel(
 // registers); streams the G * ceil(W/32) Q tiles through LDS in (query tile, group) order.
 template <int D>
 __global__ __launch_bounds__(256) void column_scores_kernel(
-    const int64_t* __restrict__ table, int64_t groups, int64_t window, int64_t query_stride,
+    const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, const float* __restrict__ margin, float scale,
     int64_t tiles_per_segment, const float* __restrict__ pv, const float4* __restrict__ stats,
     float* __restrict__ scores, int* __restrict__ nonfinite) {
   constexpr int KS = D / 16;
   constexpr int ROW = D + 8;
-  __shared__ __bf16 q_lds[2][32 * ROW];
+  __shared__ __bf16 q_lds[2][2][32 * ROW];
   __shared__ float pv_lds[kMaxGroups * kTileKeys];
   __shared__ float kpos_lds[kTileKeys];
   __shared__ int keybad_lds[kTileKeys];
   __shared__ float qmin_lds[kMaxQueryTiles];
 
-  const int64_t s = blockIdx.x / tiles_per_segment;
-  const int64_t tile = blockIdx.x % tiles_per_segment;
+  const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
+  const int per = static_cast<int>(tiles_per_segment);
+  const int s = blockIdx.x / per;
+  const int tile = blockIdx.x - s * per;
   const Segment seg = load_segment(table, s);
-  const int64_t count = seg.last - seg.first;
+  const int count = static_cast<int>(seg.last - seg.first);
   if (tile * kTileKeys >= count) return;  // uniform across the workgroup, before any barrier
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int half = lane >> 5, col = lane & 31;
-  const int64_t length = seg.length;
-  const int64_t key0 = seg.first + tile * kTileKeys;
-  const int64_t wave_key0 = key0 + wave * 32;
-  const int64_t qtiles = (window + 31) / 32;
+  const int length = static_cast<int>(seg.length);
+  const int key0 = static_cast<int>(seg.first) + tile * kTileKeys;
+  const int wave_key0 = key0 + wave * 32;
+  const int qtiles = (window + 31) / 32;
   const float* pv_seg = pv + seg.pv_offset;
+  const float4* stats_seg = stats + seg.stats_offset;
 
   // K operand of this wave's 32 keys.
   bf16x8 kop[KS];
   {
-    const int64_t key = wave_key0 + col;
-    const __bf16* krow = seg.keys + key * D + half * (D / 2);
+    const int key = wave_key0 + col;
+    const __bf16* krow = seg.keys + static_cast<int64_t>(key) * D + half * (D / 2);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       bf16x8 v;
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = static_cast<__bf16>(0.0f);
-      if (key < length) v = *reinterpret_cast<const bf16x8*>(krow + 8 * ks);
+      if (key < length) v = gload<bf16x8>(krow + 8 * ks);
       kop[ks] = v;
     }
   }
-  for (int64_t i = threadIdx.x; i < groups * kTileKeys; i += 256) {
-    const int64_t gg = i / kTileKeys, key = key0 + i % kTileKeys;
-    pv_lds[i] = key < length ? pv_seg[gg * length + key] : 0.0f;
+  for (int i = threadIdx.x; i < groups * kTileKeys; i += 256) {
+    const int gg = i / kTileKeys, key = key0 + (i - gg * kTileKeys);
+    pv_lds[i] = key < length ? gload<float>(pv_seg + static_cast<int64_t>(gg) * length + key) : 0.0f;
   }
   if (threadIdx.x < kTileKeys) {
-    const int64_t key = key0 + threadIdx.x;
-    kpos_lds[threadIdx.x] = key < length ? seg.key_positions[key] : INFINITY;
+    const int key = key0 + threadIdx.x;
+    kpos_lds[threadIdx.x] = key < length ? gload<float>(seg.key_positions + key) : INFINITY;
   }
-  for (int64_t i = threadIdx.x; i < qtiles; i += 256) {
+  for (int i = threadIdx.x; i < qtiles; i += 256) {
     float m = INFINITY;
-    for (int64_t w = i * 32; w < i * 32 + 32 && w < window; ++w)
+    for (int w = i * 32; w < i * 32 + 32 && w < window; ++w)
       m = fminf(m, static_cast<float>(query_positions[w]));
     qmin_lds[i] = m;
   }
   __syncthreads();
   if (threadIdx.x < kTileKeys) {
     int bad = 0;
-    for (int64_t gg = 0; gg < groups; ++gg) bad |= !isfinite(pv_lds[gg * kTileKeys + threadIdx.x]);
+    for (int gg = 0; gg < groups; ++gg) bad |= !isfinite(pv_lds[gg * kTileKeys + threadIdx.x]);
     keybad_lds[threadIdx.x] = bad;
   }
   // Largest candidate key position of this wave (keys at or past `last` never matter).
@@ -366,56 +421,69 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
 
-  const int64_t units = qtiles * groups;
-  TileStager<D> stager;
-  auto fetch = [&](int64_t u) {
-    const int64_t qt = u / groups, gg = u % groups;
-    stager.load(seg.queries + (gg * query_stride + qt * 32) * D, window - qt * 32);
+  // Units are (query tile, group) pairs in query-tile-major order; each LDS stage holds two
+  // consecutive units so that the MFMA chain of the second overlaps the epilogue of the first.
+  const int units = qtiles * groups;
+  TileStager<D> stager_a, stager_b;
+  auto fetch_unit = [&](TileStager<D>& st, int u) {
+    const int qt = u / groups, gg = u - qt * groups;
+    st.load(seg.queries + (static_cast<int64_t>(gg) * query_stride + qt * 32) * D, window - qt * 32);
   };
 
-  float drop[16], lo[16], hi[16];
+  float lo[16], hi[16], drop[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    drop[r] = 0.0f;
     lo[r] = INFINITY;
     hi[r] = -INFINITY;
+    drop[r] = 0.0f;
   }
   int row_bad = 0;
-  float query_position = 0.0f;
-  fetch(0);
-  stager.store(q_lds[0]);
+  const float* kpos_wave = kpos_lds + wave * 32;
+  fetch_unit(stager_a, 0);
+  if (units > 1) fetch_unit(stager_b, 1);
+  stager_a.store(q_lds[0][0]);
+  stager_b.store(q_lds[0][1]);
   __syncthreads();
-  for (int64_t u = 0; u < units; ++u) {
-    const int buf = u & 1;
-    if (u + 1 < units) fetch(u + 1);
-    const int64_t qt = u / groups, g = u % groups;
-    const int64_t query = qt * 32 + col;
+
+  // Epilogue of one unit: logits -> p -> ratio -> drop accumulation (and the min/max over
+  // queries after a query tile's last group).
+  auto finish_unit = [&](int u, const f32x16& acc) {
+    const int qt = u / groups, g = u - qt * groups;
+    const int query = qt * 32 + col;
     const bool query_valid = query < window;
-    if (g == 0) query_position = query_valid ? static_cast<float>(query_positions[query]) : 0.0f;
+    const float query_position = query_valid ? static_cast<float>(query_positions[query]) : 0.0f;
     float4 st = make_float4(0.0f, 1.0f, 1.0f, 0.0f);
     if (query_valid) {
-      st = stats[seg.stats_offset + g * window + query];
+      st = stats_seg[static_cast<int64_t>(g) * window + query];
       row_bad |= !(isfinite(st.x) && isfinite(st.y) && isfinite(st.w));
     }
-    f32x16 acc = mfma_tile_zero();
-    const __bf16* brow = q_lds[buf] + col * ROW + half * (D / 2);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(brow + 8 * ks);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], b, acc, 0, 0, 0);
-    }
-    const bool need_mask = kmax > qmin_lds[qt];
     const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
+    auto epilogue = [&](auto masked) {
+      constexpr bool kMask = decltype(masked)::value;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = acc_key(r, half);
-      float z = logit_value(acc[r], scale);
-      if (need_mask) z = kpos_lds[wave * 32 + key] <= query_position ? z : -INFINITY;
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
-      const float den = fmaxf(st.y - e, st.z);
-      const float ratio = e * __builtin_amdgcn_rcpf(den);
-      drop[r] = __builtin_fmaf(ratio, pv_row[key] - st.w, drop[r]);
-    }
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
+        f32x4 kp;
+        if constexpr (kMask) kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+          const int r = 4 * c + j;
+          f32x2 z = logit_pair(acc[r], acc[r + 1], scale);
+          if constexpr (kMask) {
+            z.x = kp[j] <= query_position ? z.x : -INFINITY;
+            z.y = kp[j + 1] <= query_position ? z.y : -INFINITY;
+          }
+          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(z.x, kLog2e, st.x));
+          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(z.y, kLog2e, st.x));
+          const float r0 = e0 * __builtin_amdgcn_rcpf(fmaxf(st.y - e0, st.z));
+          const float r1 = e1 * __builtin_amdgcn_rcpf(fmaxf(st.y - e1, st.z));
+          drop[r] = __builtin_fmaf(r0, w[j] - st.w, drop[r]);
+          drop[r + 1] = __builtin_fmaf(r1, w[j + 1] - st.w, drop[r + 1]);
+        }
+      }
+    };
+    if (uniform(kmax > qmin_lds[qt] ? 1 : 0)) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
     if (g == groups - 1) {
       if (query_valid) {
 #pragma unroll
@@ -427,7 +495,35 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) drop[r] = 0.0f;
     }
-    if (u + 1 < units) stager.store(q_lds[buf ^ 1]);
+  };
+
+  for (int u = 0, stage = 0; u < units; u += 2, ++stage) {
+    const int buf = stage & 1;
+    const bool has_b = u + 1 < units;
+    const bool more_a = u + 2 < units, more_b = u + 3 < units;
+    if (more_a) fetch_unit(stager_a, u + 2);
+    if (more_b) fetch_unit(stager_b, u + 3);
+    bf16x8 ba[KS], bb[KS];
+    const __bf16* rowa = q_lds[buf][0] + col * ROW + half * (D / 2);
+    const __bf16* rowb = q_lds[buf][1] + col * ROW + half * (D / 2);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) ba[ks] = *reinterpret_cast<const bf16x8*>(rowa + 8 * ks);
+    f32x16 acc_a = mfma_tile_zero();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      acc_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], ba[ks], acc_a, 0, 0, 0);
+    f32x16 acc_b = mfma_tile_zero();
+    if (has_b) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) bb[ks] = *reinterpret_cast<const bf16x8*>(rowb + 8 * ks);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        acc_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], bb[ks], acc_b, 0, 0, 0);
+    }
+    finish_unit(u, acc_a);
+    if (has_b) finish_unit(u + 1, acc_b);
+    if (more_a) stager_a.store(q_lds[buf ^ 1][0]);
+    if (more_b) stager_b.store(q_lds[buf ^ 1][1]);
     __syncthreads();
   }
   // Reduce over the 32 query lanes of each half (same keys, different queries).
@@ -450,7 +546,7 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     }
   }
   const int key_local = wave * 32 + acc_key(col, half);
-  const int64_t key = key0 + key_local;
+  const int key = key0 + key_local;
   if (key >= seg.last) return;
   float score;
   if (any_row_bad || keybad_lds[key_local] || !isfinite(mn) || !isfinite(mx)) {
