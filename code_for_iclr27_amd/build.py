@@ -29,6 +29,9 @@ COMPILE_FLAGS = [
     "-ffp-contract=off",
     # Packed-FP32 VALU forms are kept out of generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the scorer epilogues read every accumulator element, and
+    # the AGPR form would add one v_accvgpr_read per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -86,11 +86,17 @@ __device__ __forceinline__ float logit_value(float acc, float scale) {
 
 __device__ __forceinline__ int acc_key(int r, int half) { return 8 * (r >> 2) + 4 * half + (r & 3); }
 
-// logit_value for two accumulators at once: one v_cvt_pk_bf16_f32 per rounding step.
-__device__ __forceinline__ f32x2 logit_pair(float a, float b, float scale) {
-  const f32x2 v = {a, b};
-  const f32x2 once = __builtin_convertvector(__builtin_convertvector(v, bf16x2), f32x2) * scale;
-  return __builtin_convertvector(__builtin_convertvector(once, bf16x2), f32x2);
+// x rounded to bf16 (round to nearest even) and returned as f32 in one instruction: the pair
+// {0, x} packs bf16(0) = 0x0000 into the low half and bf16(x) into the high half, which is
+// exactly the f32 bit pattern of bf16(x).
+__device__ __forceinline__ float bf16_round_fast(float x) {
+  const f32x2 v = {0.0f, x};
+  return __builtin_bit_cast(float, __builtin_convertvector(v, bf16x2));
+}
+
+// logit_value with one conversion per rounding step (three VALU ops per logit).
+__device__ __forceinline__ float logit_fast(float acc, float scale) {
+  return bf16_round_fast(bf16_round_fast(acc) * scale);
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -182,8 +188,9 @@ struct TileStager {
 // workgroup streams all key tiles of its segment through LDS (double buffered).
 // Output per row (g, w): {-m*log2(e), S, eps*S, op} with m the masked row max, S the sum of
 // exp(z - m) and op = sum exp(z - m) * pv / S; {NaN x4} for a fully masked row.
+// Three waves per SIMD (at most 168 VGPRs) measure faster here than two without spills.
 template <int D>
-__global__ __launch_bounds__(256) void row_stats_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 3 : 1))) void row_stats_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, float scale, float epsilon,
     int64_t wg_per_segment, const float* __restrict__ pv, float4* __restrict__ stats) {
@@ -280,11 +287,7 @@ __global__ __launch_bounds__(256) void row_stats_kernel(
       for (int ks = 0; ks < KS; ++ks)
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], qop[ks], acc, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const f32x2 v = logit_pair(acc[r], acc[r + 1], scale);
-        z[16 * t + r] = v.x;
-        z[16 * t + r + 1] = v.y;
-      }
+      for (int r = 0; r < 16; ++r) z[16 * t + r] = logit_fast(acc[r], scale);
     }
     if constexpr (kMask) {
 #pragma unroll
@@ -351,7 +354,9 @@ __global__ __launch_bounds__(256) void row_stats_kernel(
 
 // ---------------------------------------------------------------------------------------
 // 3. Column scores. Workgroup = 128 candidate keys (4 waves x 32, K operand resident in
-// registers); streams the G * ceil(W/32) Q tiles through LDS in (query tile, group) order.
+// registers); streams the G * ceil(W/32) Q tiles through LDS in (query tile, group) order,
+// two tiles per stage, together with each tile's 32 row statistics and query positions, so
+// the inner loop never waits on global memory.
 template <int D>
 __global__ __launch_bounds__(256) void column_scores_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
@@ -361,10 +366,12 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
   constexpr int KS = D / 16;
   constexpr int ROW = D + 8;
   __shared__ __bf16 q_lds[2][2][32 * ROW];
+  __shared__ float4 st_lds[2][2][32];
+  __shared__ float qp_lds[2][2][32];
   __shared__ float pv_lds[kMaxGroups * kTileKeys];
   __shared__ float kpos_lds[kTileKeys];
   __shared__ int keybad_lds[kTileKeys];
-  __shared__ float qmin_lds[kMaxQueryTiles];
+  __shared__ int rowbad_lds;
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
   const int per = static_cast<int>(tiles_per_segment);
@@ -379,6 +386,7 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
   const int key0 = static_cast<int>(seg.first) + tile * kTileKeys;
   const int wave_key0 = key0 + wave * 32;
   const int qtiles = (window + 31) / 32;
+  const int units = qtiles * groups;
   const float* pv_seg = pv + seg.pv_offset;
   const float4* stats_seg = stats + seg.stats_offset;
 
@@ -404,12 +412,49 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     const int key = key0 + threadIdx.x;
     kpos_lds[threadIdx.x] = key < length ? gload<float>(seg.key_positions + key) : INFINITY;
   }
-  for (int i = threadIdx.x; i < qtiles; i += 256) {
-    float m = INFINITY;
-    for (int w = i * 32; w < i * 32 + 32 && w < window; ++w)
-      m = fminf(m, static_cast<float>(query_positions[w]));
-    qmin_lds[i] = m;
-  }
+  if (threadIdx.x == 0) rowbad_lds = 0;
+
+  // Stage loaders: all threads share the two Q tiles; lanes 0..63 of wave 0 carry the row
+  // statistics and query positions of the two units (lane / 32 = unit slot, lane % 32 = row).
+  TileStager<D> stager_a, stager_b;
+  float4 st_reg = make_float4(0.0f, 1.0f, 1.0f, 0.0f);
+  float qp_reg = INFINITY;
+  int bad_reg = 0;
+  auto fetch = [&](int u) {
+    {
+      const int qt = u / groups, gg = u - qt * groups;
+      stager_a.load(seg.queries + (static_cast<int64_t>(gg) * query_stride + qt * 32) * D,
+                    window - qt * 32);
+    }
+    if (u + 1 < units) {
+      const int qt = (u + 1) / groups, gg = (u + 1) - qt * groups;
+      stager_b.load(seg.queries + (static_cast<int64_t>(gg) * query_stride + qt * 32) * D,
+                    window - qt * 32);
+    }
+    if (threadIdx.x < 64) {
+      const int uu = u + (threadIdx.x >> 5);
+      const int qt = uu / groups, gg = uu - qt * groups;
+      const int query = qt * 32 + (threadIdx.x & 31);
+      st_reg = make_float4(0.0f, 1.0f, 1.0f, 0.0f);
+      qp_reg = INFINITY;
+      if (uu < units && query < window) {
+        st_reg = stats_seg[static_cast<int64_t>(gg) * window + query];
+        qp_reg = static_cast<float>(query_positions[query]);
+        bad_reg |= !(isfinite(st_reg.x) && isfinite(st_reg.y) && isfinite(st_reg.w));
+      }
+    }
+  };
+  auto commit = [&](int buf) {
+    stager_a.store(q_lds[buf][0]);
+    stager_b.store(q_lds[buf][1]);
+    if (threadIdx.x < 64) {
+      st_lds[buf][threadIdx.x >> 5][threadIdx.x & 31] = st_reg;
+      qp_lds[buf][threadIdx.x >> 5][threadIdx.x & 31] = qp_reg;
+    }
+  };
+  fetch(0);
+  __syncthreads();  // rowbad_lds cleared before any loader may set it
+  commit(0);
   __syncthreads();
   if (threadIdx.x < kTileKeys) {
     int bad = 0;
@@ -421,15 +466,6 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
 
-  // Units are (query tile, group) pairs in query-tile-major order; each LDS stage holds two
-  // consecutive units so that the MFMA chain of the second overlaps the epilogue of the first.
-  const int units = qtiles * groups;
-  TileStager<D> stager_a, stager_b;
-  auto fetch_unit = [&](TileStager<D>& st, int u) {
-    const int qt = u / groups, gg = u - qt * groups;
-    st.load(seg.queries + (static_cast<int64_t>(gg) * query_stride + qt * 32) * D, window - qt * 32);
-  };
-
   float lo[16], hi[16], drop[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -437,26 +473,14 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     hi[r] = -INFINITY;
     drop[r] = 0.0f;
   }
-  int row_bad = 0;
   const float* kpos_wave = kpos_lds + wave * 32;
-  fetch_unit(stager_a, 0);
-  if (units > 1) fetch_unit(stager_b, 1);
-  stager_a.store(q_lds[0][0]);
-  stager_b.store(q_lds[0][1]);
-  __syncthreads();
 
   // Epilogue of one unit: logits -> p -> ratio -> drop accumulation (and the min/max over
   // queries after a query tile's last group).
-  auto finish_unit = [&](int u, const f32x16& acc) {
+  auto finish_unit = [&](int u, int buf, int slot, const f32x16& acc) {
     const int qt = u / groups, g = u - qt * groups;
-    const int query = qt * 32 + col;
-    const bool query_valid = query < window;
-    const float query_position = query_valid ? static_cast<float>(query_positions[query]) : 0.0f;
-    float4 st = make_float4(0.0f, 1.0f, 1.0f, 0.0f);
-    if (query_valid) {
-      st = stats_seg[static_cast<int64_t>(g) * window + query];
-      row_bad |= !(isfinite(st.x) && isfinite(st.y) && isfinite(st.w));
-    }
+    const float4 st = st_lds[buf][slot][col];
+    const float query_position = qp_lds[buf][slot][col];
     const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
     auto epilogue = [&](auto masked) {
       constexpr bool kMask = decltype(masked)::value;
@@ -466,26 +490,20 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
         f32x4 kp;
         if constexpr (kMask) kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
 #pragma unroll
-        for (int j = 0; j < 4; j += 2) {
+        for (int j = 0; j < 4; ++j) {
           const int r = 4 * c + j;
-          f32x2 z = logit_pair(acc[r], acc[r + 1], scale);
-          if constexpr (kMask) {
-            z.x = kp[j] <= query_position ? z.x : -INFINITY;
-            z.y = kp[j + 1] <= query_position ? z.y : -INFINITY;
-          }
-          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(z.x, kLog2e, st.x));
-          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(z.y, kLog2e, st.x));
-          const float r0 = e0 * __builtin_amdgcn_rcpf(fmaxf(st.y - e0, st.z));
-          const float r1 = e1 * __builtin_amdgcn_rcpf(fmaxf(st.y - e1, st.z));
-          drop[r] = __builtin_fmaf(r0, w[j] - st.w, drop[r]);
-          drop[r + 1] = __builtin_fmaf(r1, w[j + 1] - st.w, drop[r + 1]);
+          float z = logit_fast(acc[r], scale);
+          if constexpr (kMask) z = kp[j] <= query_position ? z : -INFINITY;
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
+          const float ratio = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
+          drop[r] = __builtin_fmaf(ratio, w[j] - st.w, drop[r]);
         }
       }
     };
-    if (uniform(kmax > qmin_lds[qt] ? 1 : 0)) epilogue(std::true_type{});
+    if (__any(kmax > query_position)) epilogue(std::true_type{});
     else epilogue(std::false_type{});
     if (g == groups - 1) {
-      if (query_valid) {
+      if (qt * 32 + col < window) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           lo[r] = fminf(lo[r], drop[r]);
@@ -500,9 +518,8 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
   for (int u = 0, stage = 0; u < units; u += 2, ++stage) {
     const int buf = stage & 1;
     const bool has_b = u + 1 < units;
-    const bool more_a = u + 2 < units, more_b = u + 3 < units;
-    if (more_a) fetch_unit(stager_a, u + 2);
-    if (more_b) fetch_unit(stager_b, u + 3);
+    const bool more = u + 2 < units;
+    if (more) fetch(u + 2);
     bf16x8 ba[KS], bb[KS];
     const __bf16* rowa = q_lds[buf][0] + col * ROW + half * (D / 2);
     const __bf16* rowb = q_lds[buf][1] + col * ROW + half * (D / 2);
@@ -520,12 +537,14 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
       for (int ks = 0; ks < KS; ++ks)
         acc_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], bb[ks], acc_b, 0, 0, 0);
     }
-    finish_unit(u, acc_a);
-    if (has_b) finish_unit(u + 1, acc_b);
-    if (more_a) stager_a.store(q_lds[buf ^ 1][0]);
-    if (more_b) stager_b.store(q_lds[buf ^ 1][1]);
+    finish_unit(u, buf, 0, acc_a);
+    if (has_b) finish_unit(u + 1, buf, 1, acc_b);
+    if (more) commit(buf ^ 1);
     __syncthreads();
   }
+  if (bad_reg) rowbad_lds = 1;
+  __syncthreads();
+  const bool any_row_bad = rowbad_lds != 0;
   // Reduce over the 32 query lanes of each half (same keys, different queries).
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) {
@@ -535,7 +554,6 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
       hi[r] = fmaxf(hi[r], __shfl_xor(hi[r], o, 64));
     }
   }
-  const bool any_row_bad = __any(row_bad);
   if (col >= 16) return;
   float mn = lo[0], mx = hi[0];
 #pragma unroll
