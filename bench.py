@@ -6,9 +6,13 @@ Headline (BASELINE.json metric): one full audit step on the Llama-3.1-8B cache (
 567,808 candidates -> Pool7 -> allocation-preserving selection of 64,000 slots -> compaction
 of every layer. value = algorithmic bytes of the step / measured step time (GB/s).
 
+The step removes every selected slot at once, so the eviction queue it leaves is empty and its
+order is not computed (queue_order_ms_per_step times the step with that order computed too).
+
 Also reported on the same line:
   roofline      the dominant kernel, timed with HIP events on its stream inside the timed loop
-  stages_us     every stage of the step, same events
+                (the only events recorded there)
+  stages_us     every stage of the step, from separate steps with events between all stages
   cpu_baseline  the reference's CPU math path (LAZY_RECALL_BUILD_CUDA=0 semantics, restated in
                 oracle/cpu_path.py) on a bounded sample of the same workload, host cores
   reinsert      cfg3 recall reinsertion: pinned-host -> HBM copy of 512 recalled K/V rows per
@@ -47,18 +51,44 @@ def parse_args():
                         help="target CPU work for the bounded CPU-baseline sample")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-reinsert", action="store_true", help="skip the cfg3 reinsertion")
+    parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                        help="first run one plain elementwise copy (negation) of MIB MiB f32, "
+                             "the reference dispatch for scaling FETCH_SIZE / WRITE_SIZE counters")
     return parser.parse_args()
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "audit_kernels_cfg1_hbm_traffic.md")
+
+
+def measured_traffic(kernel, config):
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (lines `traffic_bytes_per_launch <config> <kernel> <bytes>`), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                parts = line.split()
+                if (len(parts) == 4 and parts[0] == "traffic_bytes_per_launch"
+                        and parts[1] == config and parts[2] == kernel):
+                    return int(parts[3])
+    except OSError:
+        pass
+    return None
 
 
 class EventTimer:
     """Records a HIP event on the current stream at each mark (events are created up front,
-    outside the timed loop)."""
+    outside the timed loop). With `only`, marks with other names record nothing: every event
+    record costs the GPU a few microseconds between kernels, so the timed steps bracket only
+    the dominant kernel."""
 
-    def __init__(self, torch, capacity=16):
+    def __init__(self, torch, capacity=16, only=None):
         self.events = [torch.cuda.Event(enable_timing=True) for _ in range(capacity)]
         self.marks = []
+        self.only = only
 
     def mark(self, name):
+        if self.only is not None and name not in self.only:
+            return
         event = self.events[len(self.marks)]
         event.record()
         self.marks.append((name, event))
@@ -196,64 +226,89 @@ def main():
     from code_for_iclr27_amd import audit, workloads
 
     dev = torch.device("cuda:0")
+    if args.copy_probe > 0:
+        source = torch.ones((args.copy_probe << 18,), dtype=torch.float32, device=dev)
+        target = torch.empty_like(source)
+        torch.neg(source, out=target)
+        torch.cuda.synchronize()
+        del source, target
     cfg = workloads.CONFIGS[args.config]
     layers, qpos, margin = workloads.make_audit(cfg, dev, seed=args.seed, generator_device="cuda")
     step = audit.AuditStep()
 
-    def run(timer=None):
+    def run(timer=None, queue_order=False):
         return step.run(layers, qpos, margin, cfg.count, cfg.protect_recent, cfg.pool_kernel,
-                        cfg.epsilon, timer=timer)
+                        cfg.epsilon, queue_order=queue_order, timer=timer)
+
+    def average_stages(timers):
+        sums = {}
+        for timer in timers:
+            for name, us in timer.stages().items():
+                sums[name] = sums.get(name, 0.0) + us
+        return {name: total / len(timers) for name, total in sums.items()}
+
+    def timed(steps, make_timer, queue_order=False):
+        timers = [make_timer() for _ in range(steps)]
+        for timer in timers:  # create the device events before the timed region
+            for event in timer.events:
+                event.record()
+        torch.cuda.synchronize()
+        gc.collect()
+        gc.disable()
+        started = time.perf_counter()
+        ends = []
+        for timer in timers:
+            outcome = run(timer, queue_order)  # returns after the step's device->host copy
+            ends.append(time.perf_counter())
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - started
+        gc.enable()
+        return outcome, timers, elapsed, np.diff([started] + ends) * 1e3
 
     for _ in range(args.warmup):
         outcome = run()
     torch.cuda.synchronize()
-    timers = [EventTimer(torch) for _ in range(args.steps)]
-    for timer in timers:  # create the device events before the timed region
-        for event in timer.events:
-            event.record()
-    torch.cuda.synchronize()
-    gc.collect()
-    gc.disable()
-    started = time.perf_counter()
-    step_ends = []
-    for timer in timers:
-        outcome = run(timer)  # returns after the step's final device->host copy
-        step_ends.append(time.perf_counter())
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - started
-    gc.enable()
-    step_ms = np.diff([started] + step_ends) * 1e3
+    # stage breakdown (not the timed region): every stage bracketed by events
+    _, breakdown, _, _ = timed(max(3, min(args.steps, 10)), lambda: EventTimer(torch))
+    stages = average_stages(breakdown)
+    order = list(stages)
+    dominant = max(stages, key=stages.get)
+    before = "start" if order.index(dominant) == 0 else order[order.index(dominant) - 1]
+    # timed region: K steps, events only around the dominant kernel
+    outcome, timers, elapsed, step_ms = timed(
+        args.steps, lambda: EventTimer(torch, only={before, dominant}))
     ms_per_step = elapsed * 1e3 / args.steps
-
-    stage_sums = {}
-    for timer in timers:
-        for name, us in timer.stages().items():
-            stage_sums[name] = stage_sums.get(name, 0.0) + us
-    stages = {name: total / len(timers) for name, total in stage_sums.items()}
+    dominant_us = average_stages(timers)[dominant]
+    # the same step with the eviction-queue order computed too (it is empty here: every
+    # selected slot is removed at once, so the removal sets do not depend on it)
+    queue_steps = max(3, min(args.steps, 20))
+    for _ in range(3):
+        run(queue_order=True)
+    _, _, queue_elapsed, _ = timed(queue_steps, lambda: EventTimer(torch, only=set()), True)
     rows_total = sum(layer.keys.size(0) for layer in layers)
     candidates = int(outcome.scores.numel())
     segments = len(outcome.segments)
     nbytes = audit_bytes(cfg, rows_total, outcome.removed, candidates, segments)
     value = nbytes / (ms_per_step / 1e3) / 1e9
 
-    # dominant kernel roofline: the largest stage
-    dominant = max(stages, key=stages.get)
+    # dominant kernel roofline, from the timed steps' events
     W, G, d = cfg.window, cfg.groups, cfg.dim
     if dominant in ("column_scores", "row_stats"):
         keys = candidates if dominant == "column_scores" else rows_total
         flops = 2.0 * W * G * d * keys
-        achieved = flops / (stages[dominant] / 1e6) / 1e12
+        achieved = flops / (dominant_us / 1e6) / 1e12
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1),
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                    "algorithmic_flops": flops}
+                    "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "traffic": measured_traffic(dominant, cfg.name), "algorithmic_flops": flops}
     else:
         stage_bytes = {"compact": 2 * (rows_total - outcome.removed) * d * 2 * 2,
                        "projected_values": rows_total * d * 2}.get(dominant, nbytes)
-        achieved = stage_bytes / (stages[dominant] / 1e6) / 1e9
+        achieved = stage_bytes / (dominant_us / 1e6) / 1e9
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None}
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                    "traffic": measured_traffic(dominant, cfg.name)}
 
     line = {
         "metric": METRIC,
@@ -275,6 +330,8 @@ def main():
         "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes": nbytes,
         "stages_us": {k: round(v, 1) for k, v in stages.items()},
+        "dominant_kernel_us": round(dominant_us, 1),
+        "queue_order_ms_per_step": round(queue_elapsed * 1e3 / queue_steps, 4),
         "step_ms_min_median_max": [round(float(np.min(step_ms)), 3), round(float(np.median(step_ms)), 3),
                                    round(float(np.max(step_ms)), 3)],
         "roofline": roofline,

@@ -9,9 +9,12 @@ The reference runs these as a Python loop of ~4 launches per (layer, head), per-
 torch.topk calls with device->host copies, host list -> tensor copies per layer and one
 compaction launch per layer. Here the host builds one int64 metadata block (segment table,
 pool bounds, segment ends, head table), uploads it once from pinned memory, and enqueues:
-3 scoring kernels, 1 pool kernel, 9 selection kernels and 1 compaction kernel covering all
+3 scoring kernels, 1 pool kernel, the selection kernels and 1 compaction kernel covering all
 layers. The only synchronisation is the final copy of the per-segment quotas, which the host
-needs to describe the new ragged layout (as the reference's metadata rebuild does).
+needs to describe the new ragged layout (as the reference's metadata rebuild does). The
+eviction-queue order (a per-segment sort and a merge of all segments' picks) is only needed
+for a non-empty lazy queue; on request it runs on a side stream while the compaction, which
+needs only the removal sets, runs on the current stream.
 """
 
 from __future__ import annotations
@@ -72,12 +75,27 @@ class AuditStep:
     def __init__(self):
         self.workspace = _Workspace()
         self.select_workspace = SelectWorkspace()
+        self.queue_streams = {}
+
+    def _queue_stream(self, device) -> torch.cuda.Stream:
+        """Side stream (default priority) for the eviction-queue order; the compaction, which
+        needs only the removal sets, runs meanwhile on the current stream."""
+        stream = self.queue_streams.get(device)
+        if stream is None:
+            stream = torch.cuda.Stream(device)
+            self.queue_streams[device] = stream
+        return stream
 
     def run(self, layers: Sequence[LayerState], query_positions: torch.Tensor,
             margin: torch.Tensor, count: int, protect_recent: int = 32, pool_kernel: int = 7,
             denominator_epsilon: float = 1e-6, check_finite: bool = True,
-            timer=None) -> AuditOutcome:
-        """``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
+            queue_order: bool = False, timer=None) -> AuditOutcome:
+        """Scores, selects and removes ``count`` slots. Every selected slot is removed now
+        (immediate == count in controller.run_audit, controller.py:148-158), so the lazy queue
+        ``references[immediate:]`` is empty and the removal sets are all the step needs; the
+        queue order (``outcome.selection.values/segments/positions``) is computed only with
+        ``queue_order=True``, on a side stream, overlapping the compaction.
+        ``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
         stage, on the current stream, for per-stage event timing."""
         mark = timer.mark if timer is not None else (lambda name: None)
         if pool_kernel <= 0 or pool_kernel % 2 == 0:
@@ -152,7 +170,9 @@ class AuditStep:
         coordinates = [(s.layer, s.head) for s in plan.segments]
         selection = select_refine(raw, pooled, plan.cumulative_ends, starts, coordinates, count,
                                   ends_device=ends_d, starts_device=starts_d,
-                                  workspace=self.select_workspace, quotas_out=info[:segments])
+                                  workspace=self.select_workspace, quotas_out=info[:segments],
+                                  queue=queue_order,
+                                  queue_stream=self._queue_stream(device) if queue_order else None)
         mark("select")
 
         # --- compaction of every layer -----------------------------------------------------
@@ -171,6 +191,9 @@ class AuditStep:
             out_keys.copy_(torch.cat([layer.keys for layer in layers]))
             out_values.copy_(torch.cat([layer.values for layer in layers]))
             out_positions.copy_(torch.cat([layer.positions.reshape(-1) for layer in layers]))
+        if selection is not None and selection.queue_ready is not None:
+            selection.wait_queue()  # join the queue order back before the step ends
+            mark("queue_join")
         host_info = info.cpu().numpy()  # the step's only synchronisation
         quotas = host_info[:segments]
         bad = int(host_info[segments:].view(np.int32)[0])

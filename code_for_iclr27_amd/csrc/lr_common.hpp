@@ -86,4 +86,16 @@ int dispatch_granule(int granule, F&& f) {
 
 inline bool valid_elem_bytes(int e) { return e == 2 || e == 4 || e == 8; }
 
+// MI355X dispatches consecutive workgroups of a grid round-robin over its 8 XCDs, each with its
+// own L2. This permutation of blockIdx.x gives XCD x (the blocks with blockIdx.x % 8 == x) one
+// contiguous range of logical block ids, in dispatch order, so workgroups that share inputs
+// (the tiles of one segment) share one L2. It is a bijection for any grid size, so results do
+// not depend on the dispatch policy.
+__device__ __forceinline__ unsigned xcd_local_block(unsigned block, unsigned blocks) {
+  constexpr unsigned kXcds = 8;
+  const unsigned xcd = block % kXcds, k = block / kXcds;
+  const unsigned per = blocks / kXcds, extra = blocks % kXcds;
+  return xcd * per + (xcd < extra ? xcd : extra) + k;
+}
+
 }  // namespace lr

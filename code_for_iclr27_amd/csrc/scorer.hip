@@ -203,8 +203,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
   const int per = static_cast<int>(wg_per_segment);
-  const int s = blockIdx.x / per;
-  const int wg = blockIdx.x - s * per;
+  const int block = static_cast<int>(xcd_local_block(blockIdx.x, gridDim.x));
+  const int s = block / per;
+  const int wg = block - s * per;
   const Segment seg = load_segment(table, s);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int half = lane >> 5, col = lane & 31;
@@ -375,8 +376,9 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
   const int per = static_cast<int>(tiles_per_segment);
-  const int s = blockIdx.x / per;
-  const int tile = blockIdx.x - s * per;
+  const int block = static_cast<int>(xcd_local_block(blockIdx.x, gridDim.x));
+  const int s = block / per;
+  const int tile = block - s * per;
   const Segment seg = load_segment(table, s);
   const int count = static_cast<int>(seg.last - seg.first);
   if (tile * kTileKeys >= count) return;  // uniform across the workgroup, before any barrier

@@ -187,102 +187,147 @@ __device__ void block_radix_sort(uint32_t* keys, uint32_t* values, uint32_t* tmp
   }
 }
 
-// k-th smallest key (1-based rank `k`) among the n keys produced by key_at(i). Returns
-// threshold key, count of keys strictly below it, and how many threshold-equal keys to take.
-template <int BLOCK, typename KeyAt>
-__device__ void block_radix_select(uint32_t n, uint32_t k, KeyAt key_at, SortLds<BLOCK>& lds,
-                                   uint32_t* threshold, uint32_t* less, uint32_t* take_equal) {
-  uint32_t prefix = 0, mask = 0, remaining = k, below = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = threadIdx.x; i < 256; i += BLOCK) lds.hist[i] = 0;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += BLOCK) {
-      const uint32_t key = key_at(i);
-      if ((key & mask) == prefix) atomicAdd(&lds.hist[(key >> shift) & 255u], 1u);
+// Exclusive scan of a pair of per-thread counts in thread order. Returns each count's offset and
+// the block totals in registers. Two barriers; `wave_sums` may be reused after the call.
+template <int BLOCK>
+__device__ __forceinline__ void block_scan_pair(uint32_t a, uint32_t b, uint32_t (*wave_sums)[2],
+                                                uint32_t& before_a, uint32_t& before_b,
+                                                uint32_t& total_a, uint32_t& total_b) {
+  constexpr int W = BLOCK / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t ia = a, ib = b;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t na = __shfl_up(ia, o, 64), nb = __shfl_up(ib, o, 64);
+    if (lane >= o) {
+      ia += na;
+      ib += nb;
     }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-      const int lane = threadIdx.x;
-      uint32_t c[4], s = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = lds.hist[4 * lane + j];
-        s += c[j];
-      }
-      uint32_t inc = s;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += v;
-      }
-      uint32_t run = inc - s;
-      // the lane whose 4 bins contain the crossing of `remaining` finishes the pass
-      if (run < remaining && inc >= remaining) {
-        uint32_t digit = 4 * lane;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (run + c[j] >= remaining) {
-            digit = 4 * lane + j;
-            break;
-          }
-          run += c[j];
-        }
-        lds.scalars[0] = digit;
-        lds.scalars[1] = run;
-      }
-    }
-    __syncthreads();
-    const uint32_t digit = lds.scalars[0], skipped = lds.scalars[1];
-    prefix |= digit << shift;
-    mask |= 255u << shift;
-    remaining -= skipped;
-    below += skipped;
-    __syncthreads();
   }
-  *threshold = prefix;
-  *less = below;
-  *take_equal = remaining;
+  if (lane == 63) {
+    wave_sums[wave][0] = ia;
+    wave_sums[wave][1] = ib;
+  }
+  __syncthreads();
+  uint32_t ba = 0, bb = 0, ta = 0, tb = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const uint32_t va = wave_sums[w][0], vb = wave_sums[w][1];
+    if (w < wave) {
+      ba += va;
+      bb += vb;
+    }
+    ta += va;
+    tb += vb;
+  }
+  __syncthreads();
+  before_a = ba + ia - a;
+  before_b = bb + ib - b;
+  total_a = ta;
+  total_b = tb;
 }
 
-// Ordered (stable) compaction helper: returns the rank of this thread's element among the
-// selected elements of its chunk plus everything selected before the chunk (*running, LDS).
-template <int BLOCK>
-__device__ __forceinline__ uint32_t block_ordered_rank(bool selected, SortLds<BLOCK>& lds,
-                                                       uint32_t* running) {
-  const uint32_t offset = block_exclusive_scan<BLOCK>(selected ? 1u : 0u, lds.wave_sums, &lds.scalars[2]);
-  const uint32_t base = *running;
+// Digit of a radix-select pass: the bin of `hist` (BINS bins, global or LDS) holding the
+// `remaining`-th key (1-based) and the number of keys in lower bins. The histogram must hold
+// at least `remaining` keys. All BLOCK threads call it; the result is uniform.
+template <int BINS, int BLOCK>
+__device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t remaining,
+                                           uint32_t (*wave_sums)[2], uint32_t* found,
+                                           uint32_t& digit, uint32_t& below) {
+  constexpr int PER = BINS / BLOCK;
+  static_assert(PER >= 1 && BINS % BLOCK == 0, "bins per thread");
+  if (threadIdx.x == 0) {
+    found[0] = BINS - 1;
+    found[1] = 0;
+  }
+  uint32_t c[PER], sum = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    c[j] = hist[threadIdx.x * PER + j];
+    sum += c[j];
+  }
+  uint32_t before, unused_b, total, unused_t;
+  block_scan_pair<BLOCK>(sum, 0u, wave_sums, before, unused_b, total, unused_t);
+  if (before < remaining && before + sum >= remaining) {
+    uint32_t run = before, d = threadIdx.x * PER + PER - 1;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      if (run + c[j] >= remaining) {
+        d = threadIdx.x * PER + j;
+        break;
+      }
+      run += c[j];
+    }
+    found[0] = d;
+    found[1] = run;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) *running = base + lds.scalars[2];
+  digit = found[0];
+  below = found[1];
   __syncthreads();
-  return base + offset;
 }
 
 // ---------------------------------------------------------------------------------------
-// Global threshold: 3 passes (11 + 11 + 10 bits) over all raw scores. Each pass is a
-// per-block histogram of the keys that match the prefix found so far, written without atomics,
-// then one workgroup sums the block histograms and extends the prefix by the digit where the
-// running count reaches the remaining rank.
-constexpr int kHistBlocks = 128;
+// Global threshold: the count-th smallest raw key, by three radix-select passes over all raw
+// scores (digits of 11, 11 and 10 bits, most significant first). Pass p histograms, per
+// workgroup in LDS, the keys that match the prefix found so far and adds the non-empty bins to
+// one global histogram with atomics. The next kernel finds pass p's digit itself, in every
+// workgroup (a scan of 2048 bins), so no launch is spent on reductions. states[p] is the
+// selection state before pass p; only workgroup 0 of the kernel that derives it writes it.
+constexpr int kHistBlocks = 256;
+constexpr int kHistStride = 2048;  // words per pass histogram
 
-__global__ __launch_bounds__(256) void select_init_kernel(SelectState* state, uint32_t count) {
+struct PassShape {
+  int bits, shift;
+};
+__host__ __device__ constexpr PassShape pass_shape(int pass) {
+  return pass == 0 ? PassShape{11, 21} : pass == 1 ? PassShape{11, 10} : PassShape{10, 0};
+}
+
+__global__ __launch_bounds__(256) void select_init_kernel(SelectState* __restrict__ states,
+                                                          uint32_t* __restrict__ hist,
+                                                          uint32_t count) {
+  for (int i = threadIdx.x; i < 3 * kHistStride; i += 256) hist[i] = 0;
   if (threadIdx.x == 0) {
-    state->prefix = 0;
-    state->mask = 0;
-    state->remaining = count;
-    state->less = 0;
-    state->done = 0;
+    SelectState st{};
+    st.remaining = count;
+    states[0] = st;
   }
 }
 
-template <int BITS, int SHIFT>
-__global__ __launch_bounds__(256) void select_block_histogram_kernel(
-    const float* __restrict__ scores, int64_t n, int64_t chunk,
-    const SelectState* __restrict__ state, uint32_t* __restrict__ block_hist) {
-  constexpr int BINS = 1 << BITS;
+// Extends `st` (the state before pass `pass`) by that pass's digit, read from its histogram.
+template <int PASS>
+__device__ __forceinline__ SelectState extend_state(SelectState st, const uint32_t* __restrict__ hist,
+                                                    uint32_t (*wave_sums)[2], uint32_t* found) {
+  constexpr PassShape shape = pass_shape(PASS);
+  uint32_t digit, below;
+  find_digit<1 << shape.bits, 256>(hist + PASS * kHistStride, st.remaining, wave_sums, found,
+                                   digit, below);
+  st.prefix |= digit << shape.shift;
+  st.mask |= ((1u << shape.bits) - 1u) << shape.shift;
+  st.less += below;
+  st.remaining -= below;
+  return st;
+}
+
+template <int PASS>
+__global__ __launch_bounds__(256) void select_pass_kernel(const float* __restrict__ scores,
+                                                          int64_t n, int64_t chunk,
+                                                          SelectState* __restrict__ states,
+                                                          uint32_t* __restrict__ hist) {
+  constexpr PassShape shape = pass_shape(PASS);
+  constexpr int BINS = 1 << shape.bits;
   __shared__ uint32_t local[BINS];
+  __shared__ uint32_t wave_sums[4][2];
+  __shared__ uint32_t found[2];
+  SelectState st = states[PASS == 0 ? 0 : PASS - 1];
+  if constexpr (PASS > 0) {
+    st = extend_state<PASS - 1>(st, hist, wave_sums, found);
+    if (blockIdx.x == 0 && threadIdx.x == 0) states[PASS] = st;
+  }
   for (int i = threadIdx.x; i < BINS; i += 256) local[i] = 0;
   __syncthreads();
-  const uint32_t prefix = state->prefix, mask = state->mask;
+  const uint32_t prefix = st.prefix, mask = st.mask;
   const int64_t begin = static_cast<int64_t>(blockIdx.x) * chunk;
   const int64_t end = begin + chunk < n ? begin + chunk : n;
   // chunk is a multiple of 1024 and scores is 16-byte aligned: float4 loads, 4 in flight
@@ -294,10 +339,10 @@ __global__ __launch_bounds__(256) void select_block_histogram_kernel(
       if (at + 3 < end) {
         q[u] = *reinterpret_cast<const float4*>(scores + at);
       } else {
-        q[u].x = at < end ? scores[at] : NAN;
-        q[u].y = at + 1 < end ? scores[at + 1] : NAN;
-        q[u].z = at + 2 < end ? scores[at + 2] : NAN;
-        q[u].w = at + 3 < end ? scores[at + 3] : NAN;
+        q[u].x = at < end ? scores[at] : 0.0f;
+        q[u].y = at + 1 < end ? scores[at + 1] : 0.0f;
+        q[u].z = at + 2 < end ? scores[at + 2] : 0.0f;
+        q[u].w = at + 3 < end ? scores[at + 3] : 0.0f;
       }
     }
 #pragma unroll
@@ -308,86 +353,44 @@ __global__ __launch_bounds__(256) void select_block_histogram_kernel(
       for (int j = 0; j < 4; ++j) {
         if (at + j < end) {
           const uint32_t key = float_key(v[j]);
-          if ((key & mask) == prefix) atomicAdd(&local[(key >> SHIFT) & (BINS - 1)], 1u);
+          if ((key & mask) == prefix) atomicAdd(&local[(key >> shape.shift) & (BINS - 1)], 1u);
         }
       }
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < BINS; i += 256) block_hist[static_cast<int64_t>(blockIdx.x) * BINS + i] = local[i];
-}
-
-template <int BITS, int SHIFT>
-__global__ __launch_bounds__(1024) void select_reduce_kernel(const uint32_t* __restrict__ block_hist,
-                                                             int blocks, SelectState* state) {
-  constexpr int BINS = 1 << BITS;
-  constexpr int PER = BINS / 1024 > 0 ? BINS / 1024 : 1;
-  __shared__ uint32_t wave_sums[16];
-  __shared__ uint32_t total;
-  uint32_t c[PER], sum = 0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int bin = threadIdx.x * PER + j;
-    uint32_t acc = 0;
-    if (bin < BINS)
-      for (int b = 0; b < blocks; ++b) acc += block_hist[static_cast<int64_t>(b) * BINS + bin];
-    c[j] = acc;
-    sum += acc;
-  }
-  const uint32_t before = block_exclusive_scan<1024>(sum, wave_sums, &total);
-  const uint32_t remaining = state->remaining;
-  __syncthreads();
-  if (before < remaining && before + sum >= remaining) {
-    uint32_t run = before;
-    int digit = threadIdx.x * PER + PER - 1;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      if (run + c[j] >= remaining) {
-        digit = threadIdx.x * PER + j;
-        break;
-      }
-      run += c[j];
-    }
-    state->prefix |= static_cast<uint32_t>(digit) << SHIFT;
-    state->mask |= static_cast<uint32_t>(BINS - 1) << SHIFT;
-    state->less += run;
-    state->remaining = remaining - run;
+  uint32_t* global_hist = hist + PASS * kHistStride;
+  for (int i = threadIdx.x; i < BINS; i += 256) {
+    const uint32_t c = local[i];
+    if (c) atomicAdd(&global_hist[i], c);
   }
 }
 
-// Per segment: how many raw keys are below / equal to the global threshold.
+// Per segment: how many raw keys are below / equal to the global threshold. Every workgroup
+// first finishes the threshold from the last pass histogram; workgroup 0 publishes it as
+// states[3] = {threshold, all-ones mask, threshold-equal keys to take, keys below}.
 __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
     const float* __restrict__ scores, const int64_t* __restrict__ ends,
-    const SelectState* __restrict__ state, uint32_t* __restrict__ seg_less,
-    uint32_t* __restrict__ seg_equal) {
-  __shared__ uint32_t sums[2][kSegThreads / 64];
+    SelectState* __restrict__ states, const uint32_t* __restrict__ hist,
+    uint32_t* __restrict__ seg_less, uint32_t* __restrict__ seg_equal) {
+  __shared__ uint32_t wave_sums[kSegThreads / 64][2];
+  __shared__ uint32_t found[2];
+  const SelectState st = extend_state<2>(states[2], hist, wave_sums, found);
+  if (blockIdx.x == 0 && threadIdx.x == 0) states[3] = st;
   const int64_t s = blockIdx.x;
   const int64_t begin = s == 0 ? 0 : ends[s - 1], end = ends[s];
-  const uint32_t threshold = state->prefix;
+  const uint32_t threshold = st.prefix;
   uint32_t less = 0, equal = 0;
   for (int64_t i = begin + threadIdx.x; i < end; i += kSegThreads) {
     const uint32_t key = float_key(scores[i]);
     less += key < threshold;
     equal += key == threshold;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    less += __shfl_xor(less, o, 64);
-    equal += __shfl_xor(equal, o, 64);
-  }
-  if ((threadIdx.x & 63) == 0) {
-    sums[0][threadIdx.x >> 6] = less;
-    sums[1][threadIdx.x >> 6] = equal;
-  }
-  __syncthreads();
+  uint32_t bl, be, total_less, total_equal;
+  block_scan_pair<kSegThreads>(less, equal, wave_sums, bl, be, total_less, total_equal);
   if (threadIdx.x == 0) {
-    uint32_t a = 0, b = 0;
-    for (int w = 0; w < kSegThreads / 64; ++w) {
-      a += sums[0][w];
-      b += sums[1][w];
-    }
-    seg_less[s] = a;
-    seg_equal[s] = b;
+    seg_less[s] = total_less;
+    seg_equal[s] = total_equal;
   }
 }
 
@@ -395,53 +398,85 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
 // segment order) and their exclusive prefix.
 __global__ __launch_bounds__(1024) void segment_plan_kernel(
     const uint32_t* __restrict__ seg_less, const uint32_t* __restrict__ seg_equal,
-    const SelectState* __restrict__ state, int64_t segments, uint32_t* __restrict__ take_equal,
+    const SelectState* __restrict__ states, int64_t segments, uint32_t* __restrict__ take_equal,
     int64_t* __restrict__ quotas, int64_t* __restrict__ offsets) {
-  __shared__ uint32_t wave_sums[16];
-  __shared__ uint32_t totals[2];
-  __shared__ uint32_t carry[2];
-  if (threadIdx.x == 0) carry[0] = carry[1] = 0;
-  __syncthreads();
-  const uint32_t need = state->remaining;
+  __shared__ uint32_t wave_sums[16][2];
+  const uint32_t need = states[3].remaining;
+  uint32_t carry_equal = 0, carry_quota = 0;
   for (int64_t base = 0; base < segments; base += 1024) {
     const int64_t s = base + threadIdx.x;
     const uint32_t eq = s < segments ? seg_equal[s] : 0;
-    const uint32_t eq_before = carry[0] + block_exclusive_scan<1024>(eq, wave_sums, &totals[0]);
+    uint32_t eq_before, unused, eq_total, unused_total;
+    block_scan_pair<1024>(eq, 0u, wave_sums, eq_before, unused, eq_total, unused_total);
+    eq_before += carry_equal;
     uint32_t take = 0;
     if (need > eq_before) take = need - eq_before < eq ? need - eq_before : eq;
     const uint32_t quota = s < segments ? seg_less[s] + take : 0;
-    const uint32_t quota_before = carry[1] + block_exclusive_scan<1024>(quota, wave_sums, &totals[1]);
+    uint32_t quota_before, quota_total;
+    block_scan_pair<1024>(quota, 0u, wave_sums, quota_before, unused, quota_total, unused_total);
+    quota_before += carry_quota;
     if (s < segments) {
       take_equal[s] = take;
       quotas[s] = quota;
       offsets[s] = quota_before;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      carry[0] += totals[0];
-      carry[1] += totals[1];
-    }
-    __syncthreads();
+    carry_equal += eq_total;
+    carry_quota += quota_total;
   }
-  if (threadIdx.x == 0) offsets[segments] = carry[1];
+  if (threadIdx.x == 0) offsets[segments] = carry_quota;
 }
 
-// One workgroup per segment with a non-zero quota:
-//   raw picks (index order) -> raw run sorted by raw key     (slot order inside the segment)
-//   pooled bottom-quota     -> removal positions (ascending) and refined picks sorted by
-//                              pooled key                    (what fills the segment's slots)
-__global__ __launch_bounds__(kSegThreads) void segment_select_kernel(
+// Radix select inside one workgroup: the k-th smallest (1-based) of the n keys key_at(i), by
+// three LDS-histogram passes (11, 11, 10 bits). Returns the key and how many keys equal to it
+// belong to the bottom k.
+template <typename KeyAt>
+__device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_at, uint32_t* hist,
+                                             uint32_t (*wave_sums)[2], uint32_t* found,
+                                             uint32_t& threshold, uint32_t& take_equal) {
+  SelectState st{};
+  st.remaining = k;
+  auto pass = [&](auto pass_index) {
+    constexpr PassShape shape = pass_shape(decltype(pass_index)::value);
+    constexpr int BINS = 1 << shape.bits;
+    for (int i = threadIdx.x; i < BINS; i += kSegThreads) hist[i] = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
+      const uint32_t key = key_at(i);
+      if ((key & st.mask) == st.prefix) atomicAdd(&hist[(key >> shape.shift) & (BINS - 1)], 1u);
+    }
+    __syncthreads();
+    uint32_t digit, below;
+    find_digit<BINS, kSegThreads>(hist, st.remaining, wave_sums, found, digit, below);
+    st.prefix |= digit << shape.shift;
+    st.mask |= static_cast<uint32_t>(BINS - 1) << shape.shift;
+    st.remaining -= below;
+  };
+  pass(std::integral_constant<int, 0>{});
+  pass(std::integral_constant<int, 1>{});
+  pass(std::integral_constant<int, 2>{});
+  threshold = st.prefix;
+  take_equal = st.remaining;
+}
+
+// ---------------------------------------------------------------------------------------
+// Removal sets. One workgroup per segment with a non-zero quota. Each thread owns one
+// contiguous run of the segment, so an ordered (index-order) compaction costs one block scan:
+//   raw picks:    key < T, or key == T among the first take_equal such keys in index order;
+//   pooled picks: the same rule against the segment's own pooled threshold (bottom-quota).
+// Writes the raw picks' keys (index order, for the queue), the pooled picks (index order:
+// removal positions ascending, their keys and local indexes for the queue), and the count of
+// pooled picks that are not raw picks.
+__global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
     const float* __restrict__ raw, const float* __restrict__ pooled,
     const int64_t* __restrict__ ends, const int64_t* __restrict__ position_starts,
-    const SelectState* __restrict__ state, const uint32_t* __restrict__ take_equal,
+    const SelectState* __restrict__ states, const uint32_t* __restrict__ take_equal,
     const int64_t* __restrict__ quotas, const int64_t* __restrict__ offsets,
     uint8_t* __restrict__ raw_flags, uint32_t* __restrict__ run_keys,
-    uint32_t* __restrict__ run_slots, uint32_t* __restrict__ refined_keys,
-    uint32_t* __restrict__ refined_local, uint32_t* __restrict__ tmp_keys,
-    uint32_t* __restrict__ tmp_values, int64_t* __restrict__ removed_positions,
-    int64_t* __restrict__ changed, uint32_t* __restrict__ segment_of) {
-  __shared__ SortLds<kSegThreads> lds;
-  __shared__ uint32_t running[2];
+    uint32_t* __restrict__ refined_keys, uint32_t* __restrict__ refined_local,
+    int64_t* __restrict__ removed_positions, int64_t* __restrict__ changed) {
+  __shared__ uint32_t hist[2048];
+  __shared__ uint32_t wave_sums[kSegThreads / 64][2];
+  __shared__ uint32_t found[2];
   const int64_t s = blockIdx.x;
   const uint32_t quota = static_cast<uint32_t>(quotas[s]);
   if (quota == 0) {
@@ -451,68 +486,125 @@ __global__ __launch_bounds__(kSegThreads) void segment_select_kernel(
   const int64_t begin = s == 0 ? 0 : ends[s - 1], end = ends[s];
   const uint32_t n = static_cast<uint32_t>(end - begin);
   const int64_t offset = offsets[s];
-  const uint32_t threshold = state->prefix, take = take_equal[s];
   const int64_t position_start = position_starts[s];
-  if (threadIdx.x == 0) running[0] = running[1] = 0;
-  __syncthreads();
+  const uint32_t per = (n + kSegThreads - 1) / kSegThreads;
+  const uint32_t lo = min(n, threadIdx.x * per), hi = min(n, lo + per);
+
   // raw picks in index order
-  for (uint32_t chunk = 0; chunk < n; chunk += kSegThreads) {
-    const uint32_t i = chunk + threadIdx.x;
-    const bool active = i < n;
-    const uint32_t key = active ? float_key(raw[begin + i]) : 0xffffffffu;
-    const bool equal = active && key == threshold;
-    const uint32_t equal_rank = block_ordered_rank<kSegThreads>(equal, lds, &running[1]);
-    const bool picked = active && (key < threshold || (equal && equal_rank < take));
-    const uint32_t rank = block_ordered_rank<kSegThreads>(picked, lds, &running[0]);
-    if (active) raw_flags[begin + i] = picked;
-    if (picked) {
-      run_keys[offset + rank] = key;
-      run_slots[offset + rank] = 0u;
+  {
+    const uint32_t threshold = states[3].prefix, take = take_equal[s];
+    uint32_t lt = 0, eq = 0;
+    for (uint32_t i = lo; i < hi; ++i) {
+      const uint32_t key = float_key(raw[begin + i]);
+      lt += key < threshold;
+      eq += key == threshold;
+    }
+    uint32_t lt_before, eq_before, lt_total, eq_total;
+    block_scan_pair<kSegThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
+    uint32_t rank = lt_before + min(take, eq_before);
+    uint32_t seen = eq_before;
+    for (uint32_t i = lo; i < hi; ++i) {
+      const uint32_t key = float_key(raw[begin + i]);
+      bool picked = key < threshold;
+      if (key == threshold) picked = seen++ < take;
+      raw_flags[begin + i] = picked;  // read back below by this same thread only
+      if (picked) run_keys[offset + rank++] = key;
     }
   }
-  __threadfence_block();
-  __syncthreads();
-  block_radix_sort<kSegThreads>(run_keys + offset, run_slots + offset, tmp_keys + offset,
-                                tmp_values + offset, quota, lds);
-  // Slot payload for the global sort: position in the concatenated runs, i.e. segment offset
-  // plus the rank in this segment's (key, index) order.
-  for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads) {
-    run_slots[offset + i] = static_cast<uint32_t>(offset + i);
-    segment_of[offset + i] = static_cast<uint32_t>(s);
+
+  // pooled picks: bottom-quota of the segment's pooled keys, in index order
+  uint32_t pthreshold, ptake;
+  block_select(n, quota, [&](uint32_t i) { return float_key(pooled[begin + i]); }, hist,
+               wave_sums, found, pthreshold, ptake);
+  uint32_t lt = 0, eq = 0;
+  for (uint32_t i = lo; i < hi; ++i) {
+    const uint32_t key = float_key(pooled[begin + i]);
+    lt += key < pthreshold;
+    eq += key == pthreshold;
   }
-  __syncthreads();
-  // refined picks: bottom-quota of the pooled scores
-  uint32_t pthreshold, pless, ptake;
-  block_radix_select<kSegThreads>(
-      n, quota, [&](uint32_t i) { return float_key(pooled[begin + i]); }, lds, &pthreshold,
-      &pless, &ptake);
-  if (threadIdx.x == 0) running[0] = running[1] = 0;
-  __syncthreads();
-  uint32_t moved = 0;
-  for (uint32_t chunk = 0; chunk < n; chunk += kSegThreads) {
-    const uint32_t i = chunk + threadIdx.x;
-    const bool active = i < n;
-    const uint32_t key = active ? float_key(pooled[begin + i]) : 0xffffffffu;
-    const bool equal = active && key == pthreshold;
-    const uint32_t equal_rank = block_ordered_rank<kSegThreads>(equal, lds, &running[1]);
-    const bool picked = active && (key < pthreshold || (equal && equal_rank < ptake));
-    const uint32_t rank = block_ordered_rank<kSegThreads>(picked, lds, &running[0]);
+  uint32_t lt_before, eq_before, lt_total, eq_total;
+  block_scan_pair<kSegThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
+  uint32_t rank = lt_before + min(ptake, eq_before);
+  uint32_t seen = eq_before, moved = 0;
+  for (uint32_t i = lo; i < hi; ++i) {
+    const uint32_t key = float_key(pooled[begin + i]);
+    bool picked = key < pthreshold;
+    if (key == pthreshold) picked = seen++ < ptake;
     if (picked) {
       refined_keys[offset + rank] = key;
       refined_local[offset + rank] = i;
       removed_positions[offset + rank] = position_start + i;
+      ++rank;
       moved += raw_flags[begin + i] ? 0u : 1u;
     }
   }
-  __threadfence_block();
+  uint32_t moved_before, unused, moved_total, unused_total;
+  block_scan_pair<kSegThreads>(moved, 0u, wave_sums, moved_before, unused, moved_total, unused_total);
+  if (threadIdx.x == 0) changed[s] = moved_total;
+}
+
+// ---------------------------------------------------------------------------------------
+// Queue order. Per segment, both pick lists are put in (key, index) order: the raw picks give
+// the segment's slots, the pooled picks what fills them (transplant). Lists of up to
+// kRankSortMax entries are rank-sorted in LDS (stable: equal keys keep index order); longer ones
+// use the block radix sort in global memory.
+constexpr uint32_t kRankSortMax = 1024;
+
+__device__ __forceinline__ void rank_sort_lds(uint32_t* keys, uint32_t* values, uint32_t n,
+                                              uint32_t* lds_keys, uint32_t* lds_values) {
+  for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
+    lds_keys[i] = keys[i];
+    lds_values[i] = values ? values[i] : 0u;
+  }
+  for (uint32_t i = n + threadIdx.x; i < ((n + 3) & ~3u); i += kSegThreads) lds_keys[i] = 0xffffffffu;
   __syncthreads();
-  const uint32_t moved_total =
-      block_exclusive_scan<kSegThreads>(moved, lds.wave_sums, &lds.scalars[3]);
-  (void)moved_total;
+  for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
+    const uint32_t key = lds_keys[i];
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < n; j += 4) {
+      const uint4 k4 = *reinterpret_cast<const uint4*>(lds_keys + j);
+      rank += (k4.x < key) | ((k4.x == key) & (j < i));
+      rank += (k4.y < key) | ((k4.y == key) & (j + 1 < i));
+      rank += (k4.z < key) | ((k4.z == key) & (j + 2 < i));
+      rank += (k4.w < key) | ((k4.w == key) & (j + 3 < i));
+    }
+    // padding keys are 0xffffffff at j >= n > i: never below `key`, never equal at a lower index
+    // unless key is 0xffffffff itself, in which case j < i fails for them
+    keys[rank] = key;
+    if (values) values[rank] = lds_values[i];
+  }
   __syncthreads();
-  if (threadIdx.x == 0) changed[s] = lds.scalars[3];
-  block_radix_sort<kSegThreads>(refined_keys + offset, refined_local + offset, tmp_keys + offset,
-                                tmp_values + offset, quota, lds);
+}
+
+__global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(
+    const int64_t* __restrict__ quotas, const int64_t* __restrict__ offsets,
+    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_slots,
+    uint32_t* __restrict__ refined_keys, uint32_t* __restrict__ refined_local,
+    uint32_t* __restrict__ tmp_keys, uint32_t* __restrict__ tmp_values,
+    uint32_t* __restrict__ segment_of) {
+  __shared__ uint32_t lds_keys[kRankSortMax];
+  __shared__ uint32_t lds_values[kRankSortMax];
+  __shared__ SortLds<kSegThreads> sort_lds;
+  const int64_t s = blockIdx.x;
+  const uint32_t quota = static_cast<uint32_t>(quotas[s]);
+  if (quota == 0) return;
+  const int64_t offset = offsets[s];
+  if (quota <= kRankSortMax) {
+    rank_sort_lds(run_keys + offset, nullptr, quota, lds_keys, lds_values);
+    rank_sort_lds(refined_keys + offset, refined_local + offset, quota, lds_keys, lds_values);
+  } else {
+    for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads) run_slots[offset + i] = 0u;
+    __syncthreads();
+    block_radix_sort<kSegThreads>(run_keys + offset, run_slots + offset, tmp_keys + offset,
+                                  tmp_values + offset, quota, sort_lds);
+    block_radix_sort<kSegThreads>(refined_keys + offset, refined_local + offset,
+                                  tmp_keys + offset, tmp_values + offset, quota, sort_lds);
+  }
+  // Slot payload for the global order: position in the concatenated runs.
+  for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads) {
+    run_slots[offset + i] = static_cast<uint32_t>(offset + i);
+    segment_of[offset + i] = static_cast<uint32_t>(s);
+  }
 }
 
 // Global slot order by merging the per-segment runs. Runs are concatenated in segment
@@ -589,8 +681,8 @@ __global__ __launch_bounds__(256) void emit_kernel(
 inline size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
 
 struct SelectWorkspace {
-  SelectState* state;
-  uint32_t* hist;
+  SelectState* states;  // [4]: before each threshold pass, then final
+  uint32_t* hist;       // [3][kHistStride]
   uint32_t* seg_less;
   uint32_t* seg_equal;
   uint32_t* take_equal;
@@ -609,8 +701,8 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
     off += align256(bytes);
     return r;
   };
-  w.state = reinterpret_cast<SelectState*>(take(sizeof(SelectState)));
-  w.hist = reinterpret_cast<uint32_t*>(take(size_t{kHistBlocks} * 2048 * 4));
+  w.states = reinterpret_cast<SelectState*>(take(4 * sizeof(SelectState)));
+  w.hist = reinterpret_cast<uint32_t*>(take(size_t{3} * kHistStride * 4));
   w.seg_less = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.seg_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.take_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
@@ -626,56 +718,37 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
   return w;
 }
 
-}  // namespace
-}  // namespace lr
-
-using namespace lr;
-
-extern "C" size_t lr_select_workspace_bytes(int64_t total, int64_t segments, int64_t count) {
-  if (total < 0 || segments < 0 || count < 0) return 0;
-  return carve(nullptr, total, segments, count).bytes;
-}
-
-extern "C" int lr_select_refine(const float* raw, const float* pooled, int64_t total,
-                                const int64_t* segment_ends, const int64_t* position_starts,
-                                int64_t segments, int64_t count, void* workspace,
-                                size_t workspace_bytes, float* out_values,
-                                int64_t* out_segments, int64_t* out_positions, int64_t* quotas,
-                                int64_t* offsets, int64_t* removed_positions, int64_t* changed,
-                                void* stream) {
-  clear_error();
-  LR_REQUIRE(total > 0 && segments > 0, "Invalid segment bounds");
-  LR_REQUIRE(count > 0 && count <= total, "Selection count must lie in [1, total]");
-  LR_REQUIRE(total < (int64_t{1} << 31), "Score table too large");
-  LR_REQUIRE(raw && pooled && segment_ends && position_starts && workspace && out_values &&
-                 out_segments && out_positions && quotas && offsets && removed_positions && changed,
-             "Expected contiguous CUDA tensor");
-  const SelectWorkspace w = carve(workspace, total, segments, count);
-  LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
-  const hipStream_t s = as_stream(stream);
-  const uint32_t k = static_cast<uint32_t>(count);
-  LR_REQUIRE((reinterpret_cast<uintptr_t>(raw) & 15) == 0, "Score table must be 16-byte aligned");
-  select_init_kernel<<<1, 64, 0, s>>>(w.state, k);
+int launch_sets(const float* raw, const float* pooled, int64_t total, const int64_t* segment_ends,
+                const int64_t* position_starts, int64_t segments, int64_t count,
+                const SelectWorkspace& w, int64_t* quotas, int64_t* offsets,
+                int64_t* removed_positions, int64_t* changed, hipStream_t s) {
+  select_init_kernel<<<1, 256, 0, s>>>(w.states, w.hist, static_cast<uint32_t>(count));
   if (int rc = check_launch("select_init")) return rc;
   const int64_t chunk = ceil_div(ceil_div(total, kHistBlocks), 1024) * 1024;
   const int blocks = static_cast<int>(ceil_div(total, chunk));
-  select_block_histogram_kernel<11, 21><<<blocks, 256, 0, s>>>(raw, total, chunk, w.state, w.hist);
-  select_reduce_kernel<11, 21><<<1, 1024, 0, s>>>(w.hist, blocks, w.state);
-  select_block_histogram_kernel<11, 10><<<blocks, 256, 0, s>>>(raw, total, chunk, w.state, w.hist);
-  select_reduce_kernel<11, 10><<<1, 1024, 0, s>>>(w.hist, blocks, w.state);
-  select_block_histogram_kernel<10, 0><<<blocks, 256, 0, s>>>(raw, total, chunk, w.state, w.hist);
-  select_reduce_kernel<10, 0><<<1, 1024, 0, s>>>(w.hist, blocks, w.state);
-  if (int rc = check_launch("select_histogram")) return rc;
-  segment_count_kernel<<<segments, kSegThreads, 0, s>>>(raw, segment_ends, w.state, w.seg_less,
-                                                        w.seg_equal);
-  segment_plan_kernel<<<1, 1024, 0, s>>>(w.seg_less, w.seg_equal, w.state, segments,
+  select_pass_kernel<0><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
+  select_pass_kernel<1><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
+  select_pass_kernel<2><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
+  if (int rc = check_launch("select_pass")) return rc;
+  segment_count_kernel<<<segments, kSegThreads, 0, s>>>(raw, segment_ends, w.states, w.hist,
+                                                        w.seg_less, w.seg_equal);
+  segment_plan_kernel<<<1, 1024, 0, s>>>(w.seg_less, w.seg_equal, w.states, segments,
                                          w.take_equal, quotas, offsets);
   if (int rc = check_launch("segment_plan")) return rc;
-  segment_select_kernel<<<segments, kSegThreads, 0, s>>>(
-      raw, pooled, segment_ends, position_starts, w.state, w.take_equal, quotas, offsets,
-      w.raw_flags, w.run_keys, w.run_slots, w.refined_keys, w.refined_local, w.tmp_keys,
-      w.tmp_values, removed_positions, changed, w.segment_of);
-  if (int rc = check_launch("segment_select")) return rc;
+  segment_pick_kernel<<<segments, kSegThreads, 0, s>>>(
+      raw, pooled, segment_ends, position_starts, w.states, w.take_equal, quotas, offsets,
+      w.raw_flags, w.run_keys, w.refined_keys, w.refined_local, removed_positions, changed);
+  return check_launch("segment_pick");
+}
+
+int launch_queue(const int64_t* position_starts, int64_t segments, int64_t count,
+                 const SelectWorkspace& w, const int64_t* quotas, const int64_t* offsets,
+                 float* out_values, int64_t* out_segments, int64_t* out_positions,
+                 hipStream_t s) {
+  segment_sort_kernel<<<segments, kSegThreads, 0, s>>>(quotas, offsets, w.run_keys, w.run_slots,
+                                                       w.refined_keys, w.refined_local,
+                                                       w.tmp_keys, w.tmp_values, w.segment_of);
+  if (int rc = check_launch("segment_sort")) return rc;
   uint32_t* keys = w.run_keys;
   uint32_t* slots = w.run_slots;
   uint32_t* alt_keys = w.tmp_keys;
@@ -692,4 +765,69 @@ extern "C" int lr_select_refine(const float* raw, const float* pooled, int64_t t
                                                    position_starts, w.refined_local, count,
                                                    out_values, out_segments, out_positions);
   return check_launch("select_emit");
+}
+
+}  // namespace
+}  // namespace lr
+
+using namespace lr;
+
+extern "C" size_t lr_select_workspace_bytes(int64_t total, int64_t segments, int64_t count) {
+  if (total < 0 || segments < 0 || count < 0) return 0;
+  return carve(nullptr, total, segments, count).bytes;
+}
+
+#define LR_SELECT_CHECK_SHAPE()                                                              \
+  LR_REQUIRE(total > 0 && segments > 0, "Invalid segment bounds");                           \
+  LR_REQUIRE(count > 0 && count <= total, "Selection count must lie in [1, total]");         \
+  LR_REQUIRE(total < (int64_t{1} << 31), "Score table too large")
+
+extern "C" int lr_select_refine_sets(const float* raw, const float* pooled, int64_t total,
+                                     const int64_t* segment_ends, const int64_t* position_starts,
+                                     int64_t segments, int64_t count, void* workspace,
+                                     size_t workspace_bytes, int64_t* quotas, int64_t* offsets,
+                                     int64_t* removed_positions, int64_t* changed, void* stream) {
+  clear_error();
+  LR_SELECT_CHECK_SHAPE();
+  LR_REQUIRE(raw && pooled && segment_ends && position_starts && workspace && quotas && offsets &&
+                 removed_positions && changed,
+             "Expected contiguous CUDA tensor");
+  LR_REQUIRE((reinterpret_cast<uintptr_t>(raw) & 15) == 0, "Score table must be 16-byte aligned");
+  const SelectWorkspace w = carve(workspace, total, segments, count);
+  LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
+  return launch_sets(raw, pooled, total, segment_ends, position_starts, segments, count, w, quotas,
+                     offsets, removed_positions, changed, as_stream(stream));
+}
+
+extern "C" int lr_select_refine_queue(const int64_t* position_starts, int64_t total,
+                                      int64_t segments, int64_t count, void* workspace,
+                                      size_t workspace_bytes, const int64_t* quotas,
+                                      const int64_t* offsets, float* out_values,
+                                      int64_t* out_segments, int64_t* out_positions,
+                                      void* stream) {
+  clear_error();
+  LR_SELECT_CHECK_SHAPE();
+  LR_REQUIRE(position_starts && workspace && quotas && offsets && out_values && out_segments &&
+                 out_positions,
+             "Expected contiguous CUDA tensor");
+  const SelectWorkspace w = carve(workspace, total, segments, count);
+  LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
+  return launch_queue(position_starts, segments, count, w, quotas, offsets, out_values,
+                      out_segments, out_positions, as_stream(stream));
+}
+
+extern "C" int lr_select_refine(const float* raw, const float* pooled, int64_t total,
+                                const int64_t* segment_ends, const int64_t* position_starts,
+                                int64_t segments, int64_t count, void* workspace,
+                                size_t workspace_bytes, float* out_values,
+                                int64_t* out_segments, int64_t* out_positions, int64_t* quotas,
+                                int64_t* offsets, int64_t* removed_positions, int64_t* changed,
+                                void* stream) {
+  if (int rc = lr_select_refine_sets(raw, pooled, total, segment_ends, position_starts, segments,
+                                     count, workspace, workspace_bytes, quotas, offsets,
+                                     removed_positions, changed, stream))
+    return rc;
+  return lr_select_refine_queue(position_starts, total, segments, count, workspace,
+                                workspace_bytes, quotas, offsets, out_values, out_segments,
+                                out_positions, stream);
 }

@@ -14,7 +14,7 @@ from __future__ import annotations
 
 from collections.abc import Sequence
 from dataclasses import dataclass
-from typing import List, Sequence as Seq
+from typing import List, Optional, Sequence as Seq
 
 import numpy as np
 import torch
@@ -59,17 +59,28 @@ class ArrayReferences(Sequence):
 
 @dataclass
 class DeviceSelection:
-    """Result of lr_select_refine, resident on the device."""
-    values: torch.Tensor             # f32 [count] ascending raw scores
-    segments: torch.Tensor           # i64 [count]
-    positions: torch.Tensor          # i64 [count] transplanted refined positions
+    """Result of lr_select_refine, resident on the device. When the queue half ran on a side
+    stream, ``queue_ready`` is the event that ends it: ``wait_queue()`` orders the current
+    stream after it (``references()`` does so itself)."""
+    values: Optional[torch.Tensor]   # f32 [count] ascending raw scores (None: queue not ordered)
+    segments: Optional[torch.Tensor]  # i64 [count]
+    positions: Optional[torch.Tensor]  # i64 [count] transplanted refined positions
     quotas: torch.Tensor             # i64 [S] picks per segment
     offsets: torch.Tensor            # i64 [S + 1] exclusive prefix of quotas
     removed_positions: torch.Tensor  # i64 [count] per-segment ascending positions
     changed: torch.Tensor            # i64 [S] refined picks absent from the raw picks
     coordinates: List[tuple]
+    queue_ready: Optional[torch.cuda.Event] = None
+
+    def wait_queue(self) -> None:
+        if self.queue_ready is not None:
+            torch.cuda.current_stream(self.quotas.device).wait_event(self.queue_ready)
+            self.queue_ready = None
 
     def references(self) -> ArrayReferences:
+        if self.values is None:
+            raise RuntimeError("the queue order was not computed (select_refine(queue=False))")
+        self.wait_queue()
         return ArrayReferences(self.values.cpu().numpy(), self.segments.cpu().numpy(),
                                self.positions.cpu().numpy(), self.coordinates)
 
@@ -79,12 +90,17 @@ class DeviceSelection:
 
 
 class SelectWorkspace:
-    """Grow-only device workspace reused across calls on one stream."""
+    """Grow-only device workspace reused across calls. A queue half still running on a side
+    stream is waited for (by the current stream) before the buffer is handed out again."""
 
     def __init__(self):
         self.buffer = None
+        self.pending: Optional[torch.cuda.Event] = None
 
     def get(self, nbytes: int, device) -> torch.Tensor:
+        if self.pending is not None:
+            torch.cuda.current_stream(device).wait_event(self.pending)
+            self.pending = None
         if self.buffer is None or self.buffer.numel() < nbytes or self.buffer.device != device:
             self.buffer = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=device)
         return self.buffer
@@ -98,10 +114,17 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
                   ends_device: torch.Tensor | None = None,
                   starts_device: torch.Tensor | None = None,
                   workspace: SelectWorkspace | None = None,
-                  quotas_out: torch.Tensor | None = None) -> DeviceSelection | None:
+                  quotas_out: torch.Tensor | None = None,
+                  queue: bool = True,
+                  queue_stream: torch.cuda.Stream | None = None) -> DeviceSelection | None:
     """Launch the device selection; returns None when nothing is selected. ``ends_device`` /
     ``starts_device`` may be passed pre-uploaded (i64 device tensors); ``quotas_out`` (i64
-    device [segments]) receives the quotas when given."""
+    device [segments]) receives the quotas when given. With ``queue_stream`` the queue order
+    (values, segments, positions) is computed there, after the removal sets, concurrently with
+    whatever the caller enqueues next on the current stream; the workspace must not be reused
+    before ``queue_ready`` (``wait_queue()``). With ``queue=False`` only the removal sets
+    (quotas, offsets, removed_positions, changed) are computed: they are all that removing
+    every selected slot needs (controller.py:154 groups the removed references per head)."""
     total = raw.numel()
     segments = len(cumulative_ends)
     count = min(max(0, int(count)), total)
@@ -125,13 +148,41 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
     quotas = out[3 * count:3 * count + segments] if quotas_out is None else quotas_out
     offsets_changed = torch.empty((2 * segments + 1,), dtype=torch.int64, device=device)
     offsets, changed = offsets_changed[:segments + 1], offsets_changed[segments + 1:]
-    _lib.call("lr_select_refine", raw.data_ptr(), pooled.data_ptr(), total,
+    if not queue:
+        _lib.call("lr_select_refine_sets", raw.data_ptr(), pooled.data_ptr(), total,
+                  ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
+                  buffer.data_ptr(), buffer.numel(), quotas.data_ptr(), offsets.data_ptr(),
+                  removed.data_ptr(), changed.data_ptr(), _lib.stream_of(raw))
+        return DeviceSelection(None, None, None, quotas, offsets, removed, changed,
+                               list(coordinates))
+    if queue_stream is None:
+        _lib.call("lr_select_refine", raw.data_ptr(), pooled.data_ptr(), total,
+                  ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
+                  buffer.data_ptr(), buffer.numel(), values.data_ptr(), seg_ids.data_ptr(),
+                  positions.data_ptr(), quotas.data_ptr(), offsets.data_ptr(), removed.data_ptr(),
+                  changed.data_ptr(), _lib.stream_of(raw))
+        return DeviceSelection(values, seg_ids, positions, quotas, offsets, removed, changed,
+                               list(coordinates))
+    current = torch.cuda.current_stream(device)
+    _lib.call("lr_select_refine_sets", raw.data_ptr(), pooled.data_ptr(), total,
               ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
-              buffer.data_ptr(), buffer.numel(), values.data_ptr(), seg_ids.data_ptr(),
-              positions.data_ptr(), quotas.data_ptr(), offsets.data_ptr(), removed.data_ptr(),
-              changed.data_ptr(), _lib.stream_of(raw))
+              buffer.data_ptr(), buffer.numel(), quotas.data_ptr(), offsets.data_ptr(),
+              removed.data_ptr(), changed.data_ptr(), current.cuda_stream)
+    sets_done = torch.cuda.Event()
+    sets_done.record(current)
+    queue_stream.wait_event(sets_done)
+    _lib.call("lr_select_refine_queue", starts_device.data_ptr(), total, segments, count,
+              buffer.data_ptr(), buffer.numel(), quotas.data_ptr(), offsets.data_ptr(),
+              values.data_ptr(), seg_ids.data_ptr(), positions.data_ptr(),
+              queue_stream.cuda_stream)
+    queue_ready = torch.cuda.Event()
+    queue_ready.record(queue_stream)
+    # memory the side stream uses stays reserved until that stream's work is done
+    for tensor in (buffer, values, out, offsets_changed, quotas, starts_device):
+        tensor.record_stream(queue_stream)
+    workspace.pending = queue_ready
     return DeviceSelection(values, seg_ids, positions, quotas, offsets, removed, changed,
-                           list(coordinates))
+                           list(coordinates), queue_ready)
 
 
 def refine_arrays(allocation, refinement, count):

@@ -207,6 +207,23 @@ int lr_select_refine(const float* raw, const float* pooled, int64_t total,
                      int64_t* quotas, int64_t* offsets, int64_t* removed_positions,
                      int64_t* changed, void* stream);
 
+/* lr_select_refine in two halves, so that a caller can overlap the queue order with the
+ * compaction that needs only the removal sets (src/lazy_recall/controller.py:148-158 removes
+ * the first `immediate` queue entries; with immediate == count the sets are all it uses).
+ * _sets: quotas, offsets, removed_positions and changed, as lr_select_refine.
+ * _queue: out_values, out_segments, out_positions, as lr_select_refine; it reads what _sets
+ * left in `workspace`, `quotas` and `offsets`, so it must be ordered after _sets (same stream,
+ * or an event) with the same arguments, and before the workspace is reused. */
+int lr_select_refine_sets(const float* raw, const float* pooled, int64_t total,
+                          const int64_t* segment_ends, const int64_t* position_starts,
+                          int64_t segments, int64_t count, void* workspace,
+                          size_t workspace_bytes, int64_t* quotas, int64_t* offsets,
+                          int64_t* removed_positions, int64_t* changed, void* stream);
+int lr_select_refine_queue(const int64_t* position_starts, int64_t total, int64_t segments,
+                           int64_t count, void* workspace, size_t workspace_bytes,
+                           const int64_t* quotas, const int64_t* offsets, float* out_values,
+                           int64_t* out_segments, int64_t* out_positions, void* stream);
+
 /* One head slot per (layer, KV head), LR_HEAD_WORDS i64 each (device):
  *   [0] keys ptr, [1] values ptr, [2] positions ptr (this head's first row),
  *   [3] length, [4] score-segment index or -1, [5] unused (0). */

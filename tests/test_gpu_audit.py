@@ -71,6 +71,27 @@ def test_select_matches_oracle(device, ties, fraction):
         np.testing.assert_array_equal(result.quotas.cpu().numpy(), reference.quotas)
 
 
+def test_select_many_segments_and_side_stream(device):
+    """More segments than one plan workgroup covers (1024), runs of 0..60 candidates, and the
+    queue half on a side stream: identical to the one-stream call and to the oracle."""
+    rng = np.random.default_rng(11)
+    lengths = rng.integers(1, 60, 1500)
+    raw, pooled, ends = tables(rng, lengths, ties=True)
+    starts = rng.integers(0, 40, len(lengths))
+    count = raw.size // 3
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+    coords = [(i // 8, i % 8) for i in range(len(ends))]
+    one = run_select(device, raw, pooled, ends, starts, count)
+    compare(one, expect, ends)
+    side = torch.cuda.Stream(device)
+    two = selection.select_refine(torch.from_numpy(raw).to(device),
+                                  torch.from_numpy(pooled).to(device), list(ends), list(starts),
+                                  coords, count, queue_stream=side)
+    two.wait_queue()
+    torch.cuda.synchronize()
+    compare(two, expect, ends)
+
+
 def test_select_all_equal_scores(device):
     lengths = [50, 60, 70]
     raw = np.full(180, 0.25, np.float32)
@@ -106,13 +127,15 @@ def test_refine_arrays_signature(device):
         k: list(v) for k, v in expect.groups([(0, 0), (0, 1), (0, 2)]).items()}
 
 
-@pytest.mark.parametrize("dim,groups", [(128, 4), (64, 4)])
-def test_audit_step_matches_oracle_chain(device, dim, groups):
+@pytest.mark.parametrize("dim,groups,queue_order", [(128, 4, False), (64, 4, False), (128, 4, True)])
+def test_audit_step_matches_oracle_chain(device, dim, groups, queue_order):
     head_lengths = [[400, 380, 35, 410], [390, 10, 400, 402], [333, 401, 399, 64]]
     layers, qpos = workloads.make_layers(head_lengths, groups, dim, 80, device, seed=11)
     margin = torch.tensor([2.0], device=device)
     count = 600
-    outcome = audit.AuditStep().run(layers, qpos, margin, count)
+    step = audit.AuditStep()
+    for _ in range(2):  # the second call reuses the step's workspaces (and side stream)
+        outcome = step.run(layers, qpos, margin, count, queue_order=queue_order)
     torch.cuda.synchronize()
     raw = outcome.scores.cpu().numpy()
     ends = np.asarray(outcome.cumulative_ends)
@@ -120,6 +143,13 @@ def test_audit_step_matches_oracle_chain(device, dim, groups):
     np.testing.assert_array_equal(outcome.pooled.cpu().numpy(), pooled)
     starts = [s.position_start for s in outcome.segments]
     expect = oselection.refine_arrays(raw, pooled, ends, starts, count)
+    if queue_order:
+        queue = outcome.selection.references()
+        np.testing.assert_array_equal(queue.scores, expect.values)
+        np.testing.assert_array_equal(queue.segments, expect.segments)
+        np.testing.assert_array_equal(queue.positions, expect.positions)
+    else:
+        assert outcome.selection.values is None
     coords = [(s.layer, s.head) for s in outcome.segments]
     groups_ = expect.groups(coords)
     for layer_index, layer in enumerate(layers):
