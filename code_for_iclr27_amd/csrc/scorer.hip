@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
   // Stage loaders: all threads share the two Q tiles; lanes 0..63 of wave 0 carry the row
   // statistics and query positions of the two units (lane / 32 = unit slot, lane % 32 = row).
   TileStager<D> stager_a, stager_b;
-  float4 st_reg = make_float4(0.0f, 1.0f, 1.0f, 0.0f);
+  float4 st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);  // padded rows: harmless, fast form
   float qp_reg = INFINITY;
   int bad_reg = 0;
   auto fetch = [&](int u) {
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
       const int uu = u + (threadIdx.x >> 5);
       const int qt = uu / groups, gg = uu - qt * groups;
       const int query = qt * 32 + (threadIdx.x & 31);
-      st_reg = make_float4(0.0f, 1.0f, 1.0f, 0.0f);
+      st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);
       qp_reg = INFINITY;
       if (uu < units && query < window) {
         st_reg = stats_seg[static_cast<int64_t>(gg) * window + query];
@@ -484,32 +484,37 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     const float4 st = st_lds[buf][slot][col];
     const float query_position = qp_lds[buf][slot][col];
     const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
-    auto epilogue = [&](auto masked) {
-      constexpr bool kMask = decltype(masked)::value;
+    // kGeneral: causal mask and denominator clamp. The fast form drops both, which is exact
+    // when no key of this wave lies after any query of the unit and every row has S >= 2 and
+    // eps*S <= 1/2: then e <= 1 gives S - e >= 1 > eps*S, so max(S - e, eps*S) == S - e.
+    auto epilogue = [&](auto general) {
+      constexpr bool kGeneral = decltype(general)::value;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
         f32x4 kp;
-        if constexpr (kMask) kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
+        if constexpr (kGeneral) kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * c + j;
           float z = logit_fast(acc[r], scale);
-          if constexpr (kMask) z = kp[j] <= query_position ? z : -INFINITY;
+          if constexpr (kGeneral) z = kp[j] <= query_position ? z : -INFINITY;
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
-          const float ratio = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
+          const float denominator = kGeneral ? fmaxf(st.y - e, st.z) : st.y - e;
+          const float ratio = e * __builtin_amdgcn_rcpf(denominator);
           drop[r] = __builtin_fmaf(ratio, w[j] - st.w, drop[r]);
         }
       }
     };
-    if (__any(kmax > query_position)) epilogue(std::true_type{});
+    const bool general = __any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f));
+    if (general) epilogue(std::true_type{});
     else epilogue(std::false_type{});
     if (g == groups - 1) {
       if (qt * 32 + col < window) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          lo[r] = fminf(lo[r], drop[r]);
-          hi[r] = fmaxf(hi[r], drop[r]);
+        for (int r = 0; r < 16; ++r) {  // NaN-propagating, as torch's amin / amax
+          lo[r] = __builtin_elementwise_minimum(lo[r], drop[r]);
+          hi[r] = __builtin_elementwise_maximum(hi[r], drop[r]);
         }
       }
 #pragma unroll
@@ -545,38 +550,51 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
     __syncthreads();
   }
   if (bad_reg) rowbad_lds = 1;
-  __syncthreads();
+  __syncthreads();  // every wave is past its last use of q_lds, which the reduction reuses
   const bool any_row_bad = rowbad_lds != 0;
-  // Reduce over the 32 query lanes of each half (same keys, different queries).
+  // Min / max over the 32 query lanes of each half through LDS, one phase each for lo and hi.
+  // Writer lane (half, col) stores its 16 values; reducer lane (pair = (half, r), part) takes
+  // 16 of the 32 queries, and lane ^ 1 holds the other 16.
+  constexpr int kRowFloats = 16;  // 16 values per writer lane
+  float* red = reinterpret_cast<float*>(&q_lds[0][0][0]) + wave * 64 * kRowFloats;
+  static_assert(sizeof(q_lds) >= 4 * 64 * kRowFloats * sizeof(float), "reduction scratch");
+  const int part = lane & 1, r_red = (lane >> 1) & 15, half_red = lane >> 5;
+  auto reduce = [&](const float* values, auto is_min) {
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<f32x4*>(red + lane * kRowFloats + 4 * c) =
+          f32x4{values[4 * c], values[4 * c + 1], values[4 * c + 2], values[4 * c + 3]};
+    __syncthreads();
+    const float* column = red + (half_red * 32 + part * 16) * kRowFloats + r_red;
+    float v = column[0];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      lo[r] = fminf(lo[r], __shfl_xor(lo[r], o, 64));
-      hi[r] = fmaxf(hi[r], __shfl_xor(hi[r], o, 64));
+    for (int q = 1; q < 16; ++q) {
+      const float x = column[q * kRowFloats];
+      v = decltype(is_min)::value ? __builtin_elementwise_minimum(v, x)
+                                  : __builtin_elementwise_maximum(v, x);
     }
-  }
-  if (col >= 16) return;
-  float mn = lo[0], mx = hi[0];
-#pragma unroll
-  for (int r = 1; r < 16; ++r) {
-    if (col == r) {
-      mn = lo[r];
-      mx = hi[r];
-    }
-  }
-  const int key_local = wave * 32 + acc_key(col, half);
+    const float other = __shfl_xor(v, 1, 64);
+    v = decltype(is_min)::value ? __builtin_elementwise_minimum(v, other)
+                                : __builtin_elementwise_maximum(v, other);
+    __syncthreads();
+    return v;
+  };
+  const float mn = reduce(lo, std::true_type{});
+  const float mx = reduce(hi, std::false_type{});
+  // Lane part 0 takes the risk of the minimum, part 1 of the maximum (f64, every lane busy).
+  const int key_local = wave * 32 + acc_key(r_red, half_red);
   const int key = key0 + key_local;
-  if (key >= seg.last) return;
-  float score;
-  if (any_row_bad || keybad_lds[key_local] || !isfinite(mn) || !isfinite(mx)) {
-    score = NAN;
-  } else {
+  const bool bad = any_row_bad || keybad_lds[key_local] || !isfinite(mn) || !isfinite(mx);
+  double risk = 0.0;
+  if (!bad) {
     const double m = static_cast<double>(margin[0]);
     const double p = 1.0 / (1.0 + exp(-m));
     const double base = softplus64(m);
-    score = static_cast<float>(fmax(risk64(m, p, base, mn), risk64(m, p, base, mx)));
+    risk = risk64(m, p, base, part ? mx : mn);
   }
+  const double other_risk = __shfl_xor(risk, 1, 64);
+  if (part != 0 || key >= seg.last) return;
+  const float score = bad ? NAN : static_cast<float>(fmax(risk, other_risk));
   scores[seg.out_offset + (key - seg.first)] = score;
   if (nonfinite != nullptr && !isfinite(score)) atomicAdd(nonfinite, 1);
 }
