@@ -52,9 +52,16 @@ class AuditOutcome:
     scores: torch.Tensor              # raw temporal scores [S]
     pooled: torch.Tensor              # Pool7 scores [S]
     selection: Optional[DeviceSelection]
-    segments: List[ScoreSegment]
-    cumulative_ends: List[int]
+    plan: SegmentPlan
     removed: int
+
+    @property
+    def segments(self) -> List[ScoreSegment]:
+        return self.plan.segments
+
+    @property
+    def cumulative_ends(self) -> List[int]:
+        return self.plan.cumulative_ends
 
 
 class _Workspace:
@@ -100,43 +107,23 @@ class AuditStep:
         mark = timer.mark if timer is not None else (lambda name: None)
         if pool_kernel <= 0 or pool_kernel % 2 == 0:
             raise ValueError("pool kernel must be a positive odd integer")
-        plan = plan_segments(layers, protect_prompt=True, protect_recent=protect_recent)
+        plan = plan_segments(layers, protect_prompt=True, protect_recent=protect_recent,
+                             pinned=True)
         device = layers[0].keys.device
         stream = torch.cuda.current_stream(device).cuda_stream
-        segments = len(plan.segments)
-        lengths = plan.head_lengths                                   # [L, H]
-        layer_count, head_count = lengths.shape
-        heads = layer_count * head_count
+        segments = plan.segment_count
+        heads = plan.head_slots
         dim = plan.dim
         elem = 2
 
-        # --- one int64 metadata block, uploaded once -----------------------------------
-        ends = np.asarray(plan.cumulative_ends, dtype=np.int64)
-        starts = plan.table[:, 6].copy()
-        segment_index = np.full(heads, -1, dtype=np.int64)
-        segment_index[plan.layer_of * head_count + plan.head_of] = np.arange(segments)
-        bases = (np.cumsum(lengths, axis=1) - lengths).reshape(-1)
-        layer_of_slot = np.repeat(np.arange(layer_count), head_count)
-        head_table = np.zeros((heads, _lib.LR_HEAD_WORDS), dtype=np.int64)
-        head_table[:, 0] = plan.pointers[layer_of_slot, 0] + bases * dim * elem
-        head_table[:, 1] = plan.pointers[layer_of_slot, 1] + bases * dim * elem
-        head_table[:, 2] = plan.pointers[layer_of_slot, 2] + bases * 4
-        head_table[:, 3] = lengths.reshape(-1)
-        head_table[:, 4] = segment_index
-        max_length = int(lengths.max())
-        pool_bounds = np.concatenate(([0], ends))
-        block = np.concatenate((plan.table.reshape(-1), pool_bounds, ends, starts,
-                                head_table.reshape(-1)))
-        device_block = _C.upload_int64(block, device)
-        cursor = plan.table.size
-        table_d = device_block[:cursor]
-        bounds_d = device_block[cursor:cursor + segments + 1]
-        cursor += segments + 1
-        ends_d = device_block[cursor:cursor + segments]
-        cursor += segments
-        starts_d = device_block[cursor:cursor + segments]
-        cursor += segments
-        heads_d = device_block[cursor:cursor + head_table.size]
+        # --- one int64 metadata block (pinned), uploaded once ------------------------------
+        device_block = plan.block.to(device, non_blocking=True)
+        table_d = plan.part("table", device_block)
+        bounds_d = plan.part("bounds", device_block)
+        ends_d = plan.part("ends", device_block)
+        starts_d = plan.part("starts", device_block)
+        heads_d = plan.part("heads", device_block)
+        max_length = plan.max_head_length
         # quotas and the non-finite score count come back in one small copy at the end
         info = torch.zeros((segments + 1,), dtype=torch.int64, device=device)
         nonfinite = info[segments:].view(torch.int32)[:1]
@@ -167,8 +154,7 @@ class AuditStep:
 
         # --- selection ---------------------------------------------------------------------
         count = min(max(0, int(count)), total)
-        coordinates = [(s.layer, s.head) for s in plan.segments]
-        selection = select_refine(raw, pooled, plan.cumulative_ends, starts, coordinates, count,
+        selection = select_refine(raw, pooled, None, None, plan.segment_info[:2].T, count,
                                   ends_device=ends_d, starts_device=starts_d,
                                   workspace=self.select_workspace, quotas_out=info[:segments],
                                   queue=queue_order,
@@ -176,8 +162,7 @@ class AuditStep:
         mark("select")
 
         # --- compaction of every layer -----------------------------------------------------
-        total_rows = sum(layer.keys.size(0) for layer in layers)
-        out_rows = total_rows - count
+        out_rows = plan.rows_total - count
         out_keys = torch.empty((out_rows, dim), dtype=layers[0].keys.dtype, device=device)
         out_values = torch.empty_like(out_keys)
         out_positions = torch.empty((out_rows,), dtype=torch.float32, device=device)
@@ -201,8 +186,9 @@ class AuditStep:
             raise RuntimeError("LazyRecall produced non-finite scores; refusing to construct a deletion queue")
 
         # --- new ragged layout (host metadata, views into the packed buffers) ----------------
+        segment_index, lengths = plan.head_info
         removed_per_slot = np.where(segment_index >= 0, quotas[np.maximum(segment_index, 0)], 0)
-        kept = (head_table[:, 3] - removed_per_slot).reshape(layer_count, head_count)
+        kept = (lengths - removed_per_slot).reshape(-1, plan.heads)
         layer_rows = kept.sum(axis=1).tolist()
         new_lens = kept.tolist()
         key_views = torch.split(out_keys, layer_rows)
@@ -211,5 +197,4 @@ class AuditStep:
         new_layers = [LayerState(k, v, p, lens, layer.prompt_lens, layer.queries, layer.gradient)
                       for k, v, p, lens, layer in zip(key_views, value_views, position_views,
                                                       new_lens, layers)]
-        return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan.segments,
-                            plan.cumulative_ends, count)
+        return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, count)

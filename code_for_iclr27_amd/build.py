@@ -1,7 +1,9 @@
-"""Build liblazyrecall_hip.so (gfx950) from csrc/*.hip with hipcc.
+"""Build liblazyrecall_hip.so (gfx950) from csrc/*.hip with hipcc, and the host planner
+module _plan from csrc/host_plan.cpp with g++ against torch's headers.
 
 Run as ``python -m code_for_iclr27_amd.build``. Each translation unit is compiled in parallel,
-then linked into ``code_for_iclr27_amd/liblazyrecall_hip.so`` next to this file.
+then linked into ``code_for_iclr27_amd/liblazyrecall_hip.so`` next to this file; the planner
+becomes ``code_for_iclr27_amd/_plan<EXT_SUFFIX>``.
 """
 
 from __future__ import annotations
@@ -55,6 +57,33 @@ def _run(command: list[str]) -> None:
         sys.stderr.write(stderr + "\n")
 
 
+def build_host_plan(verbose: bool = False) -> Path:
+    """The CPU-side planner (a CPython extension; no GPU code)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    target = PACKAGE_DIR / ("_plan" + sysconfig.get_config_var("EXT_SUFFIX"))
+    temporary = target.with_name(target.name + ".tmp")
+    includes = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"],
+                str(PACKAGE_DIR.parent / "include")]
+    library_dirs = cpp_extension.library_paths()
+    command = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function",
+               f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+               "-DTORCH_EXTENSION_NAME=_plan", str(SOURCE_DIR / "host_plan.cpp"),
+               "-o", str(temporary)]
+    command += [f"-I{path}" for path in includes]
+    command += [f"-L{path}" for path in library_dirs]
+    command += [f"-Wl,-rpath,{path}" for path in library_dirs]
+    command += ["-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    if verbose:
+        print(" ".join(command), flush=True)
+    _run(command)
+    os.replace(temporary, target)
+    return target
+
+
 def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     sources = sorted(SOURCE_DIR.glob("*.hip"))
@@ -71,9 +100,11 @@ def build(verbose: bool = False) -> Path:
         _run(command)
         return obj
 
-    workers = min(len(sources), max(1, (os.cpu_count() or 4)))
+    workers = min(len(sources) + 1, max(1, (os.cpu_count() or 4)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        planner = pool.submit(build_host_plan, verbose)
         list(pool.map(compile_one, zip(sources, objects)))
+        planner.result()
     temporary = LIBRARY.with_suffix(".so.tmp")
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(temporary),
             *map(str, objects)]

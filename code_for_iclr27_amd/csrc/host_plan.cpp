@@ -1,0 +1,186 @@
+// Host-side planning of an audit step (CPU code, built as the Python module
+// code_for_iclr27_amd._plan). It validates every layer's tensors and fills the int64 metadata
+// block that the HIP entry points read, in one pass over the layers:
+//   [segment table: segments x LR_SEG_WORDS] [pool bounds: segments + 1] [segment ends]
+//   [segment position starts] [head table: layers * heads x LR_HEAD_WORDS]
+// This is the planning part of compute_score_table (src/lazy_recall/scoring.py:218-287: the
+// per-(layer, KV head) candidate range [prompt_len, len - protect_recent), the head row
+// offsets and the mapped query heads) and of remove_positions (src/lazy_recall/cache.py:
+// 113-147: absolute rows of every head). Done from Python it costs ~27 tensor attribute
+// reads per layer at ~0.2 us each; here the whole 32-layer plan takes a few microseconds.
+#include <torch/extension.h>
+
+#include <optional>
+#include <stdexcept>
+#include <vector>
+
+#include "lazyrecall.h"
+
+namespace {
+
+void require(bool ok, const char* message) {
+  if (!ok) throw std::runtime_error(message);
+}
+
+// The same checks, in the same order and with the same messages, as the Python layer checks.
+void validate_layer(const torch::Tensor& k, const torch::Tensor& v, const torch::Tensor& p,
+                    const torch::Tensor& q, const torch::Tensor& g, const torch::Device& device,
+                    int64_t hq, int64_t window, int64_t dim) {
+  for (const torch::Tensor* t : {&k, &v, &p, &q, &g})
+    require(t->is_cuda() && t->is_contiguous() && t->device() == device,
+            "Expected contiguous CUDA tensor");
+  require(k.scalar_type() == torch::kBFloat16 && v.scalar_type() == torch::kBFloat16 &&
+              q.scalar_type() == torch::kBFloat16,
+          "The fused scorer takes bf16 keys, values and queries");
+  require(k.dim() == 2 && k.sizes() == v.sizes() && k.size(1) == dim, "Invalid KV layout");
+  require(p.scalar_type() == torch::kFloat32 && p.numel() == k.size(0), "Invalid positions");
+  require(q.dim() == 3 && q.size(0) == hq && q.size(1) == window && q.size(2) == dim,
+          "Historical query-head count changed");
+  require(g.scalar_type() == torch::kFloat32 && g.dim() == 2 && g.size(0) == hq &&
+              g.size(1) == dim,
+          "Invalid margin gradient");
+  for (const torch::Tensor* t : {&k, &v, &q})
+    require(reinterpret_cast<uintptr_t>(t->data_ptr()) % 16 == 0,
+            "bf16 operands must be 16-byte aligned");
+}
+
+inline int64_t ptr(const torch::Tensor& t) { return reinterpret_cast<int64_t>(t.data_ptr()); }
+
+// Returns (block, meta, per-segment [layer, head, first candidate, count] int64 [4, S],
+//          per-head [segment index or -1, length] int64 [2, L*H]).
+// meta = (segments, groups, window, dim, max segment length, max candidates, total candidates,
+//         projected floats, head slots, total rows, max head length).
+py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<torch::Tensor>& values,
+                     const std::vector<torch::Tensor>& positions,
+                     const std::vector<torch::Tensor>& queries,
+                     const std::vector<torch::Tensor>& gradients,
+                     const std::vector<std::vector<int64_t>>& head_lens,
+                     const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
+                     bool protect_prompt, int64_t protect_recent, bool pinned) {
+  const size_t layers = keys.size();
+  require(layers > 0, "No layers to score");
+  require(values.size() == layers && positions.size() == layers && queries.size() == layers &&
+              gradients.size() == layers && head_lens.size() == layers &&
+              prompt_lens.size() == layers,
+          "Layer lists differ in length");
+  require(queries[0].dim() == 3, "Historical query-head count changed");
+  const int64_t hq = queries[0].size(0), window = queries[0].size(1), dim = queries[0].size(2);
+  const torch::Device device = keys[0].device();
+  const int64_t heads = static_cast<int64_t>(head_lens[0].size());
+  require(heads > 0 && hq % heads == 0, "Query heads must be a multiple of KV heads");
+  const int64_t groups = hq / heads;
+  require(protect_recent >= 0, "protect_recent must be non-negative");
+
+  // pass 1: validate, count segments
+  int64_t segments = 0;
+  for (size_t l = 0; l < layers; ++l) {
+    validate_layer(keys[l], values[l], positions[l], queries[l], gradients[l], device, hq, window,
+                   dim);
+    require(static_cast<int64_t>(head_lens[l].size()) == heads,
+            "Every layer must have the same number of KV heads");
+    int64_t rows = 0;
+    for (int64_t n : head_lens[l]) {
+      require(n >= 0, "Position/KV lengths differ");
+      rows += n;
+    }
+    require(rows == keys[l].size(0), "Position/KV lengths differ");
+    const bool has_prompt = protect_prompt && prompt_lens[l].has_value();
+    if (has_prompt) require(static_cast<int64_t>(prompt_lens[l]->size()) == heads, "Invalid prompt lengths");
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t n = head_lens[l][h];
+      const int64_t first = has_prompt ? (*prompt_lens[l])[h] : 0;
+      require(first >= 0, "Invalid prompt lengths");
+      const int64_t last = std::max(first, n - protect_recent);
+      segments += last > first;
+    }
+  }
+  require(segments > 0, "No eligible KV remains after prompt/recent protection");
+
+  const int64_t slots = static_cast<int64_t>(layers) * heads;
+  const int64_t seg_words = segments * LR_SEG_WORDS;
+  const int64_t total_words = seg_words + (segments + 1) + segments + segments + slots * LR_HEAD_WORDS;
+  auto options = torch::TensorOptions().dtype(torch::kInt64).pinned_memory(pinned);
+  torch::Tensor block = torch::zeros({total_words}, options);
+  torch::Tensor segment_info = torch::empty({4, segments}, torch::dtype(torch::kInt64));
+  torch::Tensor head_info = torch::empty({2, slots}, torch::dtype(torch::kInt64));
+  int64_t* table = block.data_ptr<int64_t>();
+  int64_t* bounds = table + seg_words;
+  int64_t* ends = bounds + segments + 1;
+  int64_t* starts = ends + segments;
+  int64_t* head_table = starts + segments;
+  int64_t* seg_layer = segment_info.data_ptr<int64_t>();
+  int64_t* seg_head = seg_layer + segments;
+  int64_t* seg_first = seg_head + segments;
+  int64_t* seg_count = seg_first + segments;
+  int64_t* slot_segment = head_info.data_ptr<int64_t>();
+  int64_t* slot_length = slot_segment + slots;
+
+  // pass 2: fill
+  int64_t s = 0, total = 0, projected = 0, max_seg_length = 0, max_candidates = 0;
+  int64_t rows_total = 0, max_head_length = 0;
+  bounds[0] = 0;
+  for (size_t l = 0; l < layers; ++l) {
+    const int64_t kp = ptr(keys[l]), vp = ptr(values[l]), pp = ptr(positions[l]);
+    const int64_t qp = ptr(queries[l]), gp = ptr(gradients[l]);
+    const bool has_prompt = protect_prompt && prompt_lens[l].has_value();
+    int64_t base = 0;
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t n = head_lens[l][h];
+      const int64_t first = has_prompt ? (*prompt_lens[l])[h] : 0;
+      const int64_t last = std::max(first, n - protect_recent);
+      const int64_t slot = static_cast<int64_t>(l) * heads + h;
+      int64_t* hrow = head_table + slot * LR_HEAD_WORDS;
+      hrow[0] = kp + base * dim * 2;
+      hrow[1] = vp + base * dim * 2;
+      hrow[2] = pp + base * 4;
+      hrow[3] = n;
+      hrow[4] = -1;
+      slot_segment[slot] = -1;
+      slot_length[slot] = n;
+      if (last > first) {
+        const int64_t count = last - first;
+        int64_t* row = table + s * LR_SEG_WORDS;
+        row[0] = kp + base * dim * 2;
+        row[1] = vp + base * dim * 2;
+        row[2] = pp + base * 4;
+        row[3] = qp + h * groups * window * dim * 2;
+        row[4] = gp + h * groups * dim * 4;
+        row[5] = n;
+        row[6] = first;
+        row[7] = last;
+        row[8] = total;
+        row[9] = s * groups * window;
+        row[10] = projected;
+        row[11] = 0;
+        total += count;
+        projected += groups * n;
+        bounds[s + 1] = total;
+        ends[s] = total;
+        starts[s] = first;
+        seg_layer[s] = static_cast<int64_t>(l);
+        seg_head[s] = h;
+        seg_first[s] = first;
+        seg_count[s] = count;
+        hrow[4] = s;
+        slot_segment[slot] = s;
+        max_seg_length = std::max(max_seg_length, n);
+        max_candidates = std::max(max_candidates, count);
+        ++s;
+      }
+      base += n;
+      max_head_length = std::max(max_head_length, n);
+    }
+    rows_total += base;
+  }
+  py::tuple meta = py::make_tuple(segments, groups, window, dim, max_seg_length, max_candidates,
+                                  total, projected, slots, rows_total, max_head_length);
+  return py::make_tuple(block, meta, segment_info, head_info);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_plan, module) {
+  module.def("plan_audit", &plan_audit, "Validate layers and build the audit metadata block");
+  module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;
+  module.attr("LR_HEAD_WORDS") = LR_HEAD_WORDS;
+}

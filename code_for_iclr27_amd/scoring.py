@@ -93,26 +93,77 @@ def temporal_head_scores(queries, query_positions, keys, key_positions, values, 
     return result
 
 
-@dataclass
+def _planner():
+    try:
+        from . import _plan
+    except ImportError as error:
+        raise _lib.LazyRecallLibraryError(
+            "the host planner module _plan is not built; run `python -m code_for_iclr27_amd.build`"
+        ) from error
+    return _plan
+
+
 class SegmentPlan:
-    table: np.ndarray            # int64 [segments, LR_SEG_WORDS]
-    segments: List[ScoreSegment]
-    cumulative_ends: List[int]
-    head_starts: List[int]       # row offset of each segment's head inside its layer
-    groups: int
-    window: int
-    dim: int
-    max_length: int
-    max_candidates: int
-    projected_floats: int
-    layer_of: Optional[np.ndarray] = None   # segment -> layer
-    head_of: Optional[np.ndarray] = None    # segment -> KV head
-    head_lengths: Optional[np.ndarray] = None  # [layers, heads] lengths of every head
-    pointers: Optional[np.ndarray] = None   # [layers, 5] keys/values/positions/queries/gradient
+    """Validated layers and the int64 metadata block of one audit (host side, no GPU work),
+    built by the C++ planner in one pass (csrc/host_plan.cpp). Block layout:
+    [segment table S x LR_SEG_WORDS | pool bounds S+1 | segment ends S | position starts S |
+    head table (L*H) x LR_HEAD_WORDS]."""
+
+    def __init__(self, block: torch.Tensor, meta, segment_info: torch.Tensor,
+                 head_info: torch.Tensor, heads: int):
+        self.block = block
+        (self.segment_count, self.groups, self.window, self.dim, self.max_length,
+         self.max_candidates, self.total, self.projected_floats, self.head_slots,
+         self.rows_total, self.max_head_length) = meta
+        self.heads = heads
+        self.segment_info = segment_info.numpy()     # [4, S]: layer, head, first, count
+        self.head_info = head_info.numpy()           # [2, L*H]: segment or -1, length
+        self._segments = None
+        words = self.segment_count * _lib.LR_SEG_WORDS
+        s = self.segment_count
+        # (offset, length) of each part of the block, in words
+        self.parts = {"table": (0, words), "bounds": (words, s + 1), "ends": (words + s + 1, s),
+                      "starts": (words + 2 * s + 1, s),
+                      "heads": (words + 3 * s + 1, self.head_slots * _lib.LR_HEAD_WORDS)}
+
+    def part(self, name: str, source=None):
+        offset, length = self.parts[name]
+        return (self.block if source is None else source)[offset:offset + length]
 
     @property
-    def total(self) -> int:
-        return self.cumulative_ends[-1] if self.cumulative_ends else 0
+    def table(self) -> np.ndarray:
+        return self.part("table").numpy().reshape(self.segment_count, _lib.LR_SEG_WORDS)
+
+    @property
+    def cumulative_ends(self) -> List[int]:
+        return self.part("ends").tolist()
+
+    @property
+    def layer_of(self) -> np.ndarray:
+        return self.segment_info[0]
+
+    @property
+    def head_of(self) -> np.ndarray:
+        return self.segment_info[1]
+
+    @property
+    def head_lengths(self) -> np.ndarray:
+        return self.head_info[1].reshape(-1, self.heads)
+
+    @property
+    def head_starts(self) -> List[int]:
+        """Row offset of each segment's head inside its layer."""
+        lengths = self.head_lengths
+        bases = np.cumsum(lengths, axis=1) - lengths
+        return bases[self.layer_of, self.head_of].tolist()
+
+    @property
+    def segments(self) -> List[ScoreSegment]:
+        if self._segments is None:
+            info = self.segment_info
+            self._segments = list(map(ScoreSegment, info[0].tolist(), info[1].tolist(),
+                                      info[2].tolist(), info[3].tolist()))
+        return self._segments
 
 
 def _require(condition: bool, message: str) -> None:
@@ -120,106 +171,19 @@ def _require(condition: bool, message: str) -> None:
         raise RuntimeError(message)
 
 
-def _validate_layer(layer: LayerState, hq: int, window: int, dim: int, device) -> None:
-    """Detailed checks with the error messages; only run when the fast check fails."""
-    keys, values, positions = layer.keys, layer.values, layer.positions
-    for tensor in (keys, values, positions, layer.queries, layer.gradient):
-        _require(tensor.is_cuda and tensor.is_contiguous() and tensor.device == device,
-                 "Expected contiguous CUDA tensor")
-    _require(keys.dtype == torch.bfloat16 and values.dtype == torch.bfloat16
-             and layer.queries.dtype == torch.bfloat16,
-             "The fused scorer takes bf16 keys, values and queries")
-    _require(keys.dim() == 2 and keys.shape == values.shape and keys.size(1) == dim,
-             "Invalid KV layout")
-    _require(positions.dtype == torch.float32 and positions.numel() == keys.size(0),
-             "Invalid positions")
-    _require(tuple(layer.queries.shape) == (hq, window, dim), "Historical query-head count changed")
-    _require(layer.gradient.dtype == torch.float32 and tuple(layer.gradient.shape) == (hq, dim),
-             "Invalid margin gradient")
-    for tensor in (keys, values, layer.queries):
-        _require(tensor.data_ptr() % 16 == 0, "bf16 operands must be 16-byte aligned")
-    heads = len(layer.head_lens)
-    _require(heads > 0 and hq % heads == 0, "Query heads must be a multiple of KV heads")
-    _require(int(np.sum(layer.head_lens)) == keys.size(0), "Position/KV lengths differ")
-    raise RuntimeError("Inconsistent layer state")
-
-
 def plan_segments(layers: Sequence[LayerState], protect_prompt: bool = True,
-                  protect_recent: int = 32) -> SegmentPlan:
-    """Validate the layers and build the device segment table (host side, no GPU work).
-    Every head of every layer is planned in one vectorised pass."""
+                  protect_recent: int = 32, pinned: bool = False) -> SegmentPlan:
+    """Validate the layers and build the metadata block for every (layer, KV head) segment.
+    Candidates of a head are [prompt_len, len - protect_recent) as in scoring.py:259-265; heads
+    with none are skipped. Raises RuntimeError with the reference's messages on bad input."""
     _require(len(layers) > 0, "No layers to score")
-    first_layer = layers[0]
-    hq, window, dim = first_layer.queries.shape
-    device = first_layer.keys.device
-    bf16, f32 = torch.bfloat16, torch.float32
-    count = len(layers)
-    pointers = np.empty((count, 5), dtype=np.int64)
-    rows = np.empty(count, dtype=np.int64)
-    heads = len(first_layer.head_lens)
-    lengths_list, prompts_list = [], []
-    any_prompt = False
-    qshape, gshape = (hq, window, dim), (hq, dim)
-    for index, layer in enumerate(layers):
-        k, v, p, q, g = layer.keys, layer.values, layer.positions, layer.queries, layer.gradient
-        kp, vp, qp = k.data_ptr(), v.data_ptr(), q.data_ptr()
-        ok = (k.dtype == bf16 and v.dtype == bf16 and q.dtype == bf16 and p.dtype == f32
-              and g.dtype == f32 and k.device == device and v.device == device
-              and p.device == device and q.device == device and g.device == device
-              and k.dim() == 2 and k.shape == v.shape and k.shape[1] == dim
-              and p.numel() == k.shape[0] and q.shape == qshape and g.shape == gshape
-              and k.is_contiguous() and v.is_contiguous() and p.is_contiguous()
-              and q.is_contiguous() and g.is_contiguous() and (kp | vp | qp) % 16 == 0
-              and len(layer.head_lens) == heads and k.is_cuda)
-        if not ok:
-            _require(len(layer.head_lens) == heads, "Every layer must have the same number of KV heads")
-            _validate_layer(layer, hq, window, dim, device)
-        pointers[index] = (kp, vp, p.data_ptr(), qp, g.data_ptr())
-        rows[index] = k.shape[0]
-        lengths_list.append(layer.head_lens)
-        if protect_prompt and layer.prompt_lens is not None:
-            any_prompt = True
-        prompts_list.append(layer.prompt_lens)
-    _require(heads > 0 and hq % heads == 0, "Query heads must be a multiple of KV heads")
-    groups = hq // heads
-    lengths = np.asarray(lengths_list, dtype=np.int64)                      # [L, H]
-    if not np.array_equal(lengths.sum(axis=1), rows):
-        for layer in layers:
-            _validate_layer(layer, hq, window, dim, device)
-    bases = np.cumsum(lengths, axis=1) - lengths                            # row of each head
-    starts = np.zeros_like(lengths)
-    if any_prompt:
-        for index, prompt in enumerate(prompts_list):
-            if prompt is not None:
-                starts[index] = np.asarray(prompt, dtype=np.int64)
-    ends = np.maximum(starts, lengths - protect_recent)
-    layer_of, head_of = np.nonzero(ends > starts)                            # row-major order
-    if not layer_of.size:
-        raise RuntimeError("No eligible KV remains after prompt/recent protection")
-    base = bases[layer_of, head_of]
-    seg_lengths = lengths[layer_of, head_of]
-    seg_starts = starts[layer_of, head_of]
-    seg_ends = ends[layer_of, head_of]
-    counts = seg_ends - seg_starts
-    table = np.zeros((layer_of.size, _lib.LR_SEG_WORDS), dtype=np.int64)
-    table[:, 0] = pointers[layer_of, 0] + base * dim * 2
-    table[:, 1] = pointers[layer_of, 1] + base * dim * 2
-    table[:, 2] = pointers[layer_of, 2] + base * 4
-    table[:, 3] = pointers[layer_of, 3] + head_of * groups * window * dim * 2
-    table[:, 4] = pointers[layer_of, 4] + head_of * groups * dim * 4
-    table[:, 5] = seg_lengths
-    table[:, 6] = seg_starts
-    table[:, 7] = seg_ends
-    cumulative = np.cumsum(counts)
-    table[:, 8] = cumulative - counts
-    table[:, 9] = np.arange(layer_of.size, dtype=np.int64) * groups * window
-    projected = np.cumsum(groups * seg_lengths)
-    table[:, 10] = projected - groups * seg_lengths
-    segments = list(map(ScoreSegment, layer_of.tolist(), head_of.tolist(), seg_starts.tolist(),
-                        counts.tolist()))
-    return SegmentPlan(table, segments, cumulative.tolist(), base.tolist(), groups, window, dim,
-                       int(seg_lengths.max()), int(counts.max()), int(projected[-1]),
-                       layer_of, head_of, lengths, pointers)
+    block, meta, segment_info, head_info = _planner().plan_audit(
+        [layer.keys for layer in layers], [layer.values for layer in layers],
+        [layer.positions for layer in layers], [layer.queries for layer in layers],
+        [layer.gradient for layer in layers], [list(layer.head_lens) for layer in layers],
+        [None if layer.prompt_lens is None else list(layer.prompt_lens) for layer in layers],
+        bool(protect_prompt), int(protect_recent), bool(pinned))
+    return SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
 
 
 def score_plan(plan: SegmentPlan, query_positions: torch.Tensor, margin: torch.Tensor,
@@ -230,11 +194,11 @@ def score_plan(plan: SegmentPlan, query_positions: torch.Tensor, margin: torch.T
              and query_positions.numel() == plan.window, "Query positions do not match the window")
     margin = margin.to(device=device, dtype=torch.float32).reshape(1).contiguous()
     query_positions = query_positions.contiguous()
-    segments = len(plan.segments)
+    segments = plan.segment_count
     workspace_bytes = _lib.load().lr_score_workspace_bytes(
         segments, plan.groups, plan.window, segments * plan.groups * plan.max_length)
     with torch.cuda.device(device):
-        table = _C.upload_int64(plan.table, device)
+        table = plan.part("table").to(device)
         workspace = torch.empty((workspace_bytes,), dtype=torch.uint8, device=device)
         scores = torch.empty((plan.total,), dtype=torch.float32, device=device)
         _lib.call("lr_score_segments", table.data_ptr(), segments, plan.groups, plan.window,
@@ -265,7 +229,7 @@ def debug_segment_logits(plan: SegmentPlan, segment: int, device) -> torch.Tenso
     scorer (test hook for the parity suite)."""
     length = int(plan.table[segment, 5])
     with torch.cuda.device(device):
-        table = _C.upload_int64(plan.table, device)
+        table = plan.part("table").to(device)
         out = torch.empty((plan.groups, plan.window, length), dtype=torch.bfloat16, device=device)
         _lib.call("lr_debug_segment_logits", table.data_ptr(), segment, plan.groups, plan.window,
                   plan.dim, length, plan.window, out.data_ptr(), _lib.stream_of(out))

@@ -69,7 +69,7 @@ class DeviceSelection:
     offsets: torch.Tensor            # i64 [S + 1] exclusive prefix of quotas
     removed_positions: torch.Tensor  # i64 [count] per-segment ascending positions
     changed: torch.Tensor            # i64 [S] refined picks absent from the raw picks
-    coordinates: List[tuple]
+    coordinates: Seq  # (layer, head) per segment: list of pairs or an int array [S, 2]
     queue_ready: Optional[torch.cuda.Event] = None
 
     def wait_queue(self) -> None:
@@ -118,7 +118,8 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
                   queue: bool = True,
                   queue_stream: torch.cuda.Stream | None = None) -> DeviceSelection | None:
     """Launch the device selection; returns None when nothing is selected. ``ends_device`` /
-    ``starts_device`` may be passed pre-uploaded (i64 device tensors); ``quotas_out`` (i64
+    ``starts_device`` may be passed pre-uploaded (i64 device tensors), and then
+    ``cumulative_ends`` / ``position_starts`` may be None; ``quotas_out`` (i64
     device [segments]) receives the quotas when given. With ``queue_stream`` the queue order
     (values, segments, positions) is computed there, after the removal sets, concurrently with
     whatever the caller enqueues next on the current stream; the workspace must not be reused
@@ -126,7 +127,7 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
     (quotas, offsets, removed_positions, changed) are computed: they are all that removing
     every selected slot needs (controller.py:154 groups the removed references per head)."""
     total = raw.numel()
-    segments = len(cumulative_ends)
+    segments = len(cumulative_ends) if cumulative_ends is not None else ends_device.numel()
     count = min(max(0, int(count)), total)
     if not count:
         return None
@@ -153,8 +154,7 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
                   ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
                   buffer.data_ptr(), buffer.numel(), quotas.data_ptr(), offsets.data_ptr(),
                   removed.data_ptr(), changed.data_ptr(), _lib.stream_of(raw))
-        return DeviceSelection(None, None, None, quotas, offsets, removed, changed,
-                               list(coordinates))
+        return DeviceSelection(None, None, None, quotas, offsets, removed, changed, coordinates)
     if queue_stream is None:
         _lib.call("lr_select_refine", raw.data_ptr(), pooled.data_ptr(), total,
                   ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
@@ -162,7 +162,7 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
                   positions.data_ptr(), quotas.data_ptr(), offsets.data_ptr(), removed.data_ptr(),
                   changed.data_ptr(), _lib.stream_of(raw))
         return DeviceSelection(values, seg_ids, positions, quotas, offsets, removed, changed,
-                               list(coordinates))
+                               coordinates)
     current = torch.cuda.current_stream(device)
     _lib.call("lr_select_refine_sets", raw.data_ptr(), pooled.data_ptr(), total,
               ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
@@ -182,7 +182,7 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
         tensor.record_stream(queue_stream)
     workspace.pending = queue_ready
     return DeviceSelection(values, seg_ids, positions, quotas, offsets, removed, changed,
-                           list(coordinates), queue_ready)
+                           coordinates, queue_ready)
 
 
 def refine_arrays(allocation, refinement, count):

@@ -72,3 +72,24 @@ def test_cpu_tensors_rejected_like_reference():
 def test_register_host_failure_raises():
     with pytest.raises(RuntimeError):
         _host.register_host(0, 0)
+
+
+def test_host_planner_validates_like_the_reference():
+    """The C++ planner (module _plan) is built and rejects bad layers on the host."""
+    from code_for_iclr27_amd import scoring
+
+    def layer(**over):
+        fields = dict(keys=torch.zeros(8, 64, dtype=torch.bfloat16),
+                      values=torch.zeros(8, 64, dtype=torch.bfloat16),
+                      positions=torch.arange(8, dtype=torch.float32), head_lens=[4, 4],
+                      prompt_lens=None, queries=torch.zeros(4, 3, 64, dtype=torch.bfloat16),
+                      gradient=torch.zeros(4, 64))
+        fields.update(over)
+        return scoring.LayerState(**fields)
+
+    with pytest.raises(RuntimeError, match="Expected contiguous CUDA tensor"):
+        scoring.plan_segments([layer()])
+    with pytest.raises(RuntimeError, match="No layers to score"):
+        scoring.plan_segments([])
+    with pytest.raises(RuntimeError, match="Query heads must be a multiple of KV heads"):
+        scoring.plan_segments([layer(head_lens=[3, 3, 2])])
