@@ -183,6 +183,43 @@ struct TileStager {
   }
 };
 
+// Direct global -> LDS copies (global_load_lds_dword / _dwordx4): lane L of a wave writes its
+// granule at LDS `wave_base` + L * granule; `wave_base` must be the same for the whole wave.
+// Nothing passes through VGPRs. Completion is awaited with dma_wait() before the barrier that
+// publishes the data.
+__device__ __forceinline__ void dma16(const void* src, void* wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* src, void* wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)wave_base, 4, 0, 0);
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Swizzled LDS rows: D bf16 per row, no padding; 16-byte chunk c of row r is stored in chunk
+// slot c ^ (r & 7), so the 32 lanes that read chunk c of 32 consecutive rows (an MFMA operand)
+// touch eight different 16-byte bank groups per eight rows.
+__device__ __forceinline__ int swizzled_chunk(int row, int chunk) { return chunk ^ (row & 7); }
+
+// DMA of `rows` consecutive rows (row0..) of a [*, D] bf16 matrix into swizzled LDS rows; rows
+// at or past `last_row` re-read row `last_row` (callers mask them). All 256 threads call it.
+template <int D, int ROWS>
+__device__ __forceinline__ void dma_rows(const __bf16* matrix, int row0, int last_row,
+                                         __bf16* lds) {
+  constexpr int CH = D / 8, CHUNKS = ROWS * CH;
+  static_assert(CHUNKS % 256 == 0, "whole waves per copy");
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < CHUNKS / 256; ++i) {
+    const int slot = 256 * i + threadIdx.x;
+    const int row = slot / CH, chunk = slot % CH;
+    const int source = min(row0 + row, last_row);
+    dma16(matrix + static_cast<int64_t>(source) * D + 8 * swizzled_chunk(row, chunk),
+          lds + (256 * i + 64 * wave) * 8);
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // 2. Row statistics. One wave per (group, 32-query tile) task, four tasks per workgroup; the
 // workgroup streams all key tiles of its segment through LDS (double buffered).
@@ -195,8 +232,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     const int64_t* __restrict__ query_positions, float scale, float epsilon,
     int64_t wg_per_segment, const float* __restrict__ pv, float4* __restrict__ stats) {
   constexpr int KS = D / 16;
-  constexpr int ROW = D + 8;
-  __shared__ __bf16 k_lds[2][64 * ROW];
+  __shared__ __bf16 k_lds[2][64 * D];  // swizzled rows
   __shared__ float pv_lds[2][kMaxGroups * 64];
   __shared__ float kpos_lds[2][64];
   __shared__ float kmax_lds[2];
@@ -238,31 +274,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   const int ktiles = (length + 63) / 64;  // 64-key stages: two 32-key MFMA tiles each
   const float* pv_seg = pv + seg.pv_offset;
 
-  TileStager<D> stager_a, stager_b;
-  float pv_reg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float kpos_reg = INFINITY;
-  auto fetch = [&](int kt) {
+  // Key stage kt -> LDS buffer `buf`: K rows and projected values by DMA (rows past the end
+  // re-read the last row; their key position +inf masks them), key positions via VGPRs.
+  auto fetch = [&](int kt, int buf) {
     const int t0 = kt * 64;
-    stager_a.load(seg.keys + static_cast<int64_t>(t0) * D, length - t0);
-    stager_b.load(seg.keys + static_cast<int64_t>(t0 + 32) * D, length - t0 - 32);
+    dma_rows<D, 64>(seg.keys, t0, length - 1, k_lds[buf]);
+    const int wave_slot = 64 * (threadIdx.x >> 6), lane_slot = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      const int gg = idx >> 6, k = idx & 63;
-      pv_reg[i] = (gg < groups && t0 + k < length) ? gload<float>(pv_seg + static_cast<int64_t>(gg) * length + t0 + k) : 0.0f;
+    for (int i = 0; i < kMaxGroups / 4; ++i) {
+      const int gg = 4 * i + (threadIdx.x >> 6);  // uniform per wave
+      if (gg < groups)
+        dma4(pv_seg + static_cast<int64_t>(gg) * length + min(t0 + lane_slot, length - 1),
+             &pv_lds[buf][256 * i + wave_slot]);
     }
     kpos_reg = (threadIdx.x < 64 && t0 + static_cast<int>(threadIdx.x) < length)
                    ? gload<float>(seg.key_positions + t0 + threadIdx.x)
                    : INFINITY;
   };
   auto commit = [&](int buf) {
-    stager_a.store(k_lds[buf]);
-    stager_b.store(k_lds[buf] + 32 * ROW);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = threadIdx.x + 256 * i;
-      if (idx < kMaxGroups * 64) pv_lds[buf][idx] = pv_reg[i];
-    }
     if (threadIdx.x < 64) {
       kpos_lds[buf][threadIdx.x] = kpos_reg;
       float m = kpos_reg;
@@ -280,9 +310,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       bf16x8 a[KS];
-      const __bf16* arow = k_lds[buf] + (32 * t + col) * ROW + half * (D / 2);
+      const __bf16* arow = k_lds[buf] + (32 * t + col) * D;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) a[ks] = *reinterpret_cast<const bf16x8*>(arow + 8 * ks);
+      for (int ks = 0; ks < KS; ++ks)
+        a[ks] = *reinterpret_cast<const bf16x8*>(arow + 8 * swizzled_chunk(col, half * KS + ks));
       f32x16 acc = mfma_tile_zero();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
@@ -320,18 +351,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     m_run = m_new;
   };
 
-  fetch(0);
+  fetch(0, 0);
+  dma_wait();
   commit(0);
   __syncthreads();
   for (int kt = 0; kt < ktiles; ++kt) {
     const int buf = kt & 1;
     const bool more = kt + 1 < ktiles;
-    if (more) fetch(kt + 1);
+    if (more) fetch(kt + 1, buf ^ 1);  // buf ^ 1 was last read before the previous barrier
     if (active) {
       if (uniform(kmax_lds[buf] > qmin ? 1 : 0)) stage(buf, std::true_type{});
       else stage(buf, std::false_type{});
     }
-    if (more) commit(buf ^ 1);
+    if (more) {
+      dma_wait();
+      commit(buf ^ 1);
+    }
     __syncthreads();
   }
   // Merge the two half-waves (same query, disjoint keys).
