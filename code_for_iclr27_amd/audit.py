@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import math
 import time
+from collections import abc
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -45,9 +46,43 @@ def pool_score_table(table: ScoreTable, kernel_size: int = 7) -> ScoreTable:
                       table.score_ms + (time.perf_counter() - started) * 1000.0)
 
 
+class PackedLayers(abc.Sequence):
+    """The compacted layers of an audit: every layer's rows live in one packed K, V and
+    positions buffer (layer-major, heads in order). Layer i's LayerState, with views into those
+    buffers, is created when first indexed."""
+
+    def __init__(self, keys, values, positions, kept: np.ndarray, sources: Sequence[LayerState]):
+        self.keys, self.values, self.positions = keys, values, positions
+        self.kept = kept                                   # [L, H] rows kept per head
+        rows = kept.sum(axis=1)
+        self.offsets = np.concatenate(([0], np.cumsum(rows))).tolist()
+        self.sources = sources
+        self._cache = {}
+
+    def __len__(self) -> int:
+        return len(self.sources)
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            return [self[i] for i in range(*index.indices(len(self)))]
+        if index < 0:
+            index += len(self)
+        if not 0 <= index < len(self):
+            raise IndexError(index)
+        layer = self._cache.get(index)
+        if layer is None:
+            start, end = self.offsets[index], self.offsets[index + 1]
+            source = self.sources[index]
+            layer = LayerState(self.keys[start:end], self.values[start:end],
+                               self.positions[start:end], self.kept[index].tolist(),
+                               source.prompt_lens, source.queries, source.gradient)
+            self._cache[index] = layer
+        return layer
+
+
 @dataclass
 class AuditOutcome:
-    layers: List[LayerState]          # compacted layers (views into one packed K/V/pos buffer)
+    layers: PackedLayers              # compacted layers (views into one packed K/V/pos buffer)
     head_lens: List[List[int]]
     scores: torch.Tensor              # raw temporal scores [S]
     pooled: torch.Tensor              # Pool7 scores [S]
@@ -118,11 +153,12 @@ class AuditStep:
 
         # --- one int64 metadata block (pinned), uploaded once ------------------------------
         device_block = plan.block.to(device, non_blocking=True)
-        table_d = plan.part("table", device_block)
-        bounds_d = plan.part("bounds", device_block)
+        base = device_block.data_ptr()
+        table_ptr = base + 8 * plan.parts["table"][0]
+        bounds_ptr = base + 8 * plan.parts["bounds"][0]
+        heads_ptr = base + 8 * plan.parts["heads"][0]
         ends_d = plan.part("ends", device_block)
         starts_d = plan.part("starts", device_block)
-        heads_d = plan.part("heads", device_block)
         max_length = plan.max_head_length
         # quotas and the non-finite score count come back in one small copy at the end
         info = torch.zeros((segments + 1,), dtype=torch.int64, device=device)
@@ -140,7 +176,7 @@ class AuditStep:
         stage_masks = (1, 2, 4) if timer is not None else (7,)
         mark("start")
         for index, stages in enumerate(stage_masks):
-            _lib.call("lr_score_segments", table_d.data_ptr(), segments, plan.groups,
+            _lib.call("lr_score_segments", table_ptr, segments, plan.groups,
                       plan.window, dim, plan.max_length, plan.max_candidates, plan.window,
                       query_positions.data_ptr(), margin.data_ptr(), float(1.0 / math.sqrt(dim)),
                       float(denominator_epsilon), score_ws.data_ptr(), score_bytes,
@@ -148,7 +184,7 @@ class AuditStep:
             mark(stage_names[index] if timer is not None else "score")
 
         # --- Pool7 -------------------------------------------------------------------------
-        _lib.call("lr_pool", raw.data_ptr(), total, bounds_d.data_ptr(), segments,
+        _lib.call("lr_pool", raw.data_ptr(), total, bounds_ptr, segments,
                   plan.max_candidates, pool_kernel, pooled.data_ptr(), stream)
         mark("pool")
 
@@ -167,7 +203,7 @@ class AuditStep:
         out_values = torch.empty_like(out_keys)
         out_positions = torch.empty((out_rows,), dtype=torch.float32, device=device)
         if selection is not None:
-            _lib.call("lr_compact_heads", heads_d.data_ptr(), heads, selection.quotas.data_ptr(),
+            _lib.call("lr_compact_heads", heads_ptr, heads, selection.quotas.data_ptr(),
                       selection.offsets.data_ptr(), selection.removed_positions.data_ptr(), dim,
                       elem, max_length, out_rows, out_keys.data_ptr(), out_values.data_ptr(),
                       out_positions.data_ptr(), stream)
@@ -189,12 +225,6 @@ class AuditStep:
         segment_index, lengths = plan.head_info
         removed_per_slot = np.where(segment_index >= 0, quotas[np.maximum(segment_index, 0)], 0)
         kept = (lengths - removed_per_slot).reshape(-1, plan.heads)
-        layer_rows = kept.sum(axis=1).tolist()
         new_lens = kept.tolist()
-        key_views = torch.split(out_keys, layer_rows)
-        value_views = torch.split(out_values, layer_rows)
-        position_views = torch.split(out_positions, layer_rows)
-        new_layers = [LayerState(k, v, p, lens, layer.prompt_lens, layer.queries, layer.gradient)
-                      for k, v, p, lens, layer in zip(key_views, value_views, position_views,
-                                                      new_lens, layers)]
+        new_layers = PackedLayers(out_keys, out_values, out_positions, kept, layers)
         return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, count)

@@ -42,7 +42,7 @@ class ScoreTable:
     score_ms: float
 
 
-@dataclass
+@dataclass(slots=True)
 class LayerState:
     """What the scorer reads from one layer of a LazyRecallCache plus its query history:
     keys/values [rows, d] bf16 in the flat per-head layout (_core/cache.py:104-105), positions
