@@ -390,23 +390,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 
 // ---------------------------------------------------------------------------------------
 // 3. Column scores. Workgroup = 128 candidate keys (4 waves x 32, K operand resident in
-// registers); streams the G * ceil(W/32) Q tiles through LDS in (query tile, group) order,
-// two tiles per stage, together with each tile's 32 row statistics and query positions, so
-// the inner loop never waits on global memory.
+// registers). It streams the G * ceil(W/32) (query tile, group) units in query-tile-major order
+// through LDS, one unit per double-buffered stage: the 32 query rows by direct copy into
+// swizzled rows, with each row's statistics and query position. After a query tile's last
+// group every lane holds 16 drops (its query x 16 keys); a transpose through LDS reduces them
+// over the tile's queries, so a lane keeps one running (min, max) pair and the kernel fits
+// three waves per SIMD.
 template <int D>
-__global__ __launch_bounds__(256) void column_scores_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 3 : 1))) void column_scores_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, const float* __restrict__ margin, float scale,
     int64_t tiles_per_segment, const float* __restrict__ pv, const float4* __restrict__ stats,
     float* __restrict__ scores, int* __restrict__ nonfinite) {
   constexpr int KS = D / 16;
-  constexpr int ROW = D + 8;
-  __shared__ __bf16 q_lds[2][2][32 * ROW];
-  __shared__ float4 st_lds[2][2][32];
-  __shared__ float qp_lds[2][2][32];
+  __shared__ __bf16 q_lds[3][32 * D];  // swizzled rows, triple buffered
+  __shared__ float4 st_lds[3][32];
+  __shared__ float qp_lds[3][32];
   __shared__ float pv_lds[kMaxGroups * kTileKeys];
   __shared__ float kpos_lds[kTileKeys];
   __shared__ int keybad_lds[kTileKeys];
+  __shared__ float red_lds[4][64 * 16];  // per-wave transpose scratch
   __shared__ int rowbad_lds;
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
@@ -451,47 +454,57 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
   }
   if (threadIdx.x == 0) rowbad_lds = 0;
 
-  // Stage loaders: all threads share the two Q tiles; lanes 0..63 of wave 0 carry the row
-  // statistics and query positions of the two units (lane / 32 = unit slot, lane % 32 = row).
-  TileStager<D> stager_a, stager_b;
-  float4 st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);  // padded rows: harmless, fast form
-  float qp_reg = INFINITY;
+  // Stage loader for unit u into buffer buf: the query rows by direct copy (rows past the
+  // window re-read the last query; their results are never used), and on lanes 0..31 of wave 0
+  // the rows' statistics and query positions (padded rows: harmless values that take the fast
+  // epilogue).
+  // The loads are only issued here; their values are first used in commit(), after the wait
+  // that also covers the row copies, so no wave stalls on them mid-stage.
+  float4 st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);
+  int64_t qp_raw = 0;
+  bool row_loaded = false;
   int bad_reg = 0;
-  auto fetch = [&](int u) {
-    {
-      const int qt = u / groups, gg = u - qt * groups;
-      stager_a.load(seg.queries + (static_cast<int64_t>(gg) * query_stride + qt * 32) * D,
-                    window - qt * 32);
-    }
-    if (u + 1 < units) {
-      const int qt = (u + 1) / groups, gg = (u + 1) - qt * groups;
-      stager_b.load(seg.queries + (static_cast<int64_t>(gg) * query_stride + qt * 32) * D,
-                    window - qt * 32);
-    }
-    if (threadIdx.x < 64) {
-      const int uu = u + (threadIdx.x >> 5);
-      const int qt = uu / groups, gg = uu - qt * groups;
-      const int query = qt * 32 + (threadIdx.x & 31);
-      st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);
-      qp_reg = INFINITY;
-      if (uu < units && query < window) {
-        st_reg = stats_seg[static_cast<int64_t>(gg) * window + query];
-        qp_reg = static_cast<float>(query_positions[query]);
-        bad_reg |= !(isfinite(st_reg.x) && isfinite(st_reg.y) && isfinite(st_reg.w));
+  int fetch_qt = 0, fetch_g = 0;  // unit of the next fetch, (query tile, group)
+  auto fetch = [&](int buf) {
+    dma_rows<D, 32>(seg.queries + static_cast<int64_t>(fetch_g) * query_stride * D,
+                    fetch_qt * 32, window - 1, q_lds[buf]);
+    if (threadIdx.x < 32) {
+      const int query = fetch_qt * 32 + threadIdx.x;
+      row_loaded = query < window;
+      if (row_loaded) {
+        st_reg = stats_seg[static_cast<int64_t>(fetch_g) * window + query];
+        qp_raw = query_positions[query];
       }
+    }
+    if (++fetch_g == groups) {
+      fetch_g = 0;
+      ++fetch_qt;
     }
   };
   auto commit = [&](int buf) {
-    stager_a.store(q_lds[buf][0]);
-    stager_b.store(q_lds[buf][1]);
-    if (threadIdx.x < 64) {
-      st_lds[buf][threadIdx.x >> 5][threadIdx.x & 31] = st_reg;
-      qp_lds[buf][threadIdx.x >> 5][threadIdx.x & 31] = qp_reg;
+    if (threadIdx.x < 32) {
+      float4 st = make_float4(0.0f, 2.0f, 0.0f, 0.0f);  // padded rows take the fast epilogue
+      float qp = INFINITY;
+      if (row_loaded) {
+        st = st_reg;
+        qp = static_cast<float>(qp_raw);
+        bad_reg |= !(isfinite(st.x) && isfinite(st.y) && isfinite(st.w));
+      }
+      st_lds[buf][threadIdx.x] = st;
+      qp_lds[buf][threadIdx.x] = qp;
     }
   };
+  // Unit u lives in buffer u % 3: while unit u's epilogue runs, unit u + 1's MFMAs are in
+  // flight (issued from its buffer) and unit u + 2 is being copied in.
   fetch(0);
   __syncthreads();  // rowbad_lds cleared before any loader may set it
+  dma_wait();
   commit(0);
+  if (units > 1) {
+    fetch(1);
+    dma_wait();
+    commit(1);
+  }
   __syncthreads();
   if (threadIdx.x < kTileKeys) {
     int bad = 0;
@@ -503,21 +516,38 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
 
-  float lo[16], hi[16], drop[16];
+  float drop[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    lo[r] = INFINITY;
-    hi[r] = -INFINITY;
-    drop[r] = 0.0f;
-  }
+  for (int r = 0; r < 16; ++r) drop[r] = 0.0f;
+  // Reducer role in the tile transpose: lane = (half, r, part); it owns key acc_key(r, half)
+  // and queries part*16 .. part*16+15 of each tile; lane ^ 1 owns the other 16.
+  const int part = lane & 1, r_red = (lane >> 1) & 15, half_red = lane >> 5;
+  float lo = INFINITY, hi = -INFINITY;
+  float* red = red_lds[wave];
   const float* kpos_wave = kpos_lds + wave * 32;
 
-  // Epilogue of one unit: logits -> p -> ratio -> drop accumulation (and the min/max over
-  // queries after a query tile's last group).
-  auto finish_unit = [&](int u, int buf, int slot, const f32x16& acc) {
-    const int qt = u / groups, g = u - qt * groups;
-    const float4 st = st_lds[buf][slot][col];
-    const float query_position = qp_lds[buf][slot][col];
+  auto logits = [&](int buf) {
+    bf16x8 b[KS];
+    const __bf16* brow = q_lds[buf] + col * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      b[ks] = *reinterpret_cast<const bf16x8*>(brow + 8 * swizzled_chunk(col, half * KS + ks));
+    f32x16 acc = mfma_tile_zero();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], b[ks], acc, 0, 0, 0);
+    return acc;
+  };
+  f32x16 acc_next = logits(0);
+  int qt = 0, g = 0;  // unit u = (query tile, group)
+  for (int u = 0, buf = 0; u < units; ++u, buf = buf == 2 ? 0 : buf + 1) {
+    const int buf1 = buf == 2 ? 0 : buf + 1, buf2 = buf1 == 2 ? 0 : buf1 + 1;
+    // unit u + 2 goes to the buffer unit u - 1 used; its last readers passed the previous barrier
+    if (u + 2 < units) fetch(buf2);
+    const f32x16 acc = acc_next;
+    if (u + 1 < units) acc_next = logits(buf1);
+    const float4 st = st_lds[buf][col];
+    const float query_position = qp_lds[buf][col];
     const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
     // kGeneral: causal mask and denominator clamp. The fast form drops both, which is exact
     // when no key of this wave lies after any query of the unit and every row has S >= 2 and
@@ -541,82 +571,53 @@ __global__ __launch_bounds__(256) void column_scores_kernel(
         }
       }
     };
-    const bool general = __any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f));
-    if (general) epilogue(std::true_type{});
+    if (__any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f))) epilogue(std::true_type{});
     else epilogue(std::false_type{});
     if (g == groups - 1) {
-      if (qt * 32 + col < window) {
+      // Min / max of the tile's drops over its queries, through this wave's LDS scratch. LDS
+      // accesses of one wave complete in order, so the reads see this wave's writes.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {  // NaN-propagating, as torch's amin / amax
-          lo[r] = __builtin_elementwise_minimum(lo[r], drop[r]);
-          hi[r] = __builtin_elementwise_maximum(hi[r], drop[r]);
-        }
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<f32x4*>(red + lane * 16 + 4 * c) =
+            f32x4{drop[4 * c], drop[4 * c + 1], drop[4 * c + 2], drop[4 * c + 3]};
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int valid = min(max(window - qt * 32 - part * 16, 0), 16);
+      const float* column = red + (half_red * 32 + part * 16) * 16 + r_red;
+      float tile_lo = INFINITY, tile_hi = -INFINITY;
+      // NaN-propagating, as torch's amin / amax; padded queries of the last tile are skipped
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const float x = column[q * 16];
+        tile_lo = __builtin_elementwise_minimum(tile_lo, q < valid ? x : INFINITY);
+        tile_hi = __builtin_elementwise_maximum(tile_hi, q < valid ? x : -INFINITY);
       }
+      lo = __builtin_elementwise_minimum(lo, tile_lo);
+      hi = __builtin_elementwise_maximum(hi, tile_hi);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int r = 0; r < 16; ++r) drop[r] = 0.0f;
     }
-  };
-
-  for (int u = 0, stage = 0; u < units; u += 2, ++stage) {
-    const int buf = stage & 1;
-    const bool has_b = u + 1 < units;
-    const bool more = u + 2 < units;
-    if (more) fetch(u + 2);
-    bf16x8 ba[KS], bb[KS];
-    const __bf16* rowa = q_lds[buf][0] + col * ROW + half * (D / 2);
-    const __bf16* rowb = q_lds[buf][1] + col * ROW + half * (D / 2);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) ba[ks] = *reinterpret_cast<const bf16x8*>(rowa + 8 * ks);
-    f32x16 acc_a = mfma_tile_zero();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      acc_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], ba[ks], acc_a, 0, 0, 0);
-    f32x16 acc_b = mfma_tile_zero();
-    if (has_b) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) bb[ks] = *reinterpret_cast<const bf16x8*>(rowb + 8 * ks);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        acc_b = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], bb[ks], acc_b, 0, 0, 0);
+    if (u + 2 < units) {
+      dma_wait();
+      commit(buf2);
     }
-    finish_unit(u, buf, 0, acc_a);
-    if (has_b) finish_unit(u + 1, buf, 1, acc_b);
-    if (more) commit(buf ^ 1);
     __syncthreads();
+    if (++g == groups) {
+      g = 0;
+      ++qt;
+    }
   }
   if (bad_reg) rowbad_lds = 1;
-  __syncthreads();  // every wave is past its last use of q_lds, which the reduction reuses
+  __syncthreads();
   const bool any_row_bad = rowbad_lds != 0;
-  // Min / max over the 32 query lanes of each half through LDS, one phase each for lo and hi.
-  // Writer lane (half, col) stores its 16 values; reducer lane (pair = (half, r), part) takes
-  // 16 of the 32 queries, and lane ^ 1 holds the other 16.
-  constexpr int kRowFloats = 16;  // 16 values per writer lane
-  float* red = reinterpret_cast<float*>(&q_lds[0][0][0]) + wave * 64 * kRowFloats;
-  static_assert(sizeof(q_lds) >= 4 * 64 * kRowFloats * sizeof(float), "reduction scratch");
-  const int part = lane & 1, r_red = (lane >> 1) & 15, half_red = lane >> 5;
-  auto reduce = [&](const float* values, auto is_min) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<f32x4*>(red + lane * kRowFloats + 4 * c) =
-          f32x4{values[4 * c], values[4 * c + 1], values[4 * c + 2], values[4 * c + 3]};
-    __syncthreads();
-    const float* column = red + (half_red * 32 + part * 16) * kRowFloats + r_red;
-    float v = column[0];
-#pragma unroll
-    for (int q = 1; q < 16; ++q) {
-      const float x = column[q * kRowFloats];
-      v = decltype(is_min)::value ? __builtin_elementwise_minimum(v, x)
-                                  : __builtin_elementwise_maximum(v, x);
-    }
-    const float other = __shfl_xor(v, 1, 64);
-    v = decltype(is_min)::value ? __builtin_elementwise_minimum(v, other)
-                                : __builtin_elementwise_maximum(v, other);
-    __syncthreads();
-    return v;
-  };
-  const float mn = reduce(lo, std::true_type{});
-  const float mx = reduce(hi, std::false_type{});
-  // Lane part 0 takes the risk of the minimum, part 1 of the maximum (f64, every lane busy).
+  // Combine the two reducer lanes of each key, then part 0 takes the risk of the minimum and
+  // part 1 of the maximum (f64, every lane busy).
+  const float mn = __builtin_elementwise_minimum(lo, __shfl_xor(lo, 1, 64));
+  const float mx = __builtin_elementwise_maximum(hi, __shfl_xor(hi, 1, 64));
   const int key_local = wave * 32 + acc_key(r_red, half_red);
   const int key = key0 + key_local;
   const bool bad = any_row_bad || keybad_lds[key_local] || !isfinite(mn) || !isfinite(mx);
