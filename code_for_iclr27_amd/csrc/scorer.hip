@@ -538,14 +538,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], b[ks], acc, 0, 0, 0);
     return acc;
   };
-  f32x16 acc_next = logits(0);
   int qt = 0, g = 0;  // unit u = (query tile, group)
-  for (int u = 0, buf = 0; u < units; ++u, buf = buf == 2 ? 0 : buf + 1) {
+  // One unit: copy unit u + 2 in, start unit u + 1's MFMAs (into acc_out), run unit u's
+  // epilogue on acc. The loop below alternates two accumulators, so none is copied.
+  auto step = [&](int u, int buf, const f32x16& acc, f32x16& acc_out) {
     const int buf1 = buf == 2 ? 0 : buf + 1, buf2 = buf1 == 2 ? 0 : buf1 + 1;
     // unit u + 2 goes to the buffer unit u - 1 used; its last readers passed the previous barrier
     if (u + 2 < units) fetch(buf2);
-    const f32x16 acc = acc_next;
-    if (u + 1 < units) acc_next = logits(buf1);
+    if (u + 1 < units) acc_out = logits(buf1);
     const float4 st = st_lds[buf][col];
     const float query_position = qp_lds[buf][col];
     const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
@@ -583,15 +583,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int valid = min(max(window - qt * 32 - part * 16, 0), 16);
       const float* column = red + (half_red * 32 + part * 16) * 16 + r_red;
       float tile_lo = INFINITY, tile_hi = -INFINITY;
-      // NaN-propagating, as torch's amin / amax; padded queries of the last tile are skipped
+      // NaN-propagating, as torch's amin / amax; padded queries of a partial last tile skipped
+      if (qt * 32 + 32 <= window) {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const float x = column[q * 16];
-        tile_lo = __builtin_elementwise_minimum(tile_lo, q < valid ? x : INFINITY);
-        tile_hi = __builtin_elementwise_maximum(tile_hi, q < valid ? x : -INFINITY);
+        for (int q = 0; q < 16; ++q) {
+          const float x = column[q * 16];
+          tile_lo = __builtin_elementwise_minimum(tile_lo, x);
+          tile_hi = __builtin_elementwise_maximum(tile_hi, x);
+        }
+      } else {
+        const int valid = min(max(window - qt * 32 - part * 16, 0), 16);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const float x = column[q * 16];
+          tile_lo = __builtin_elementwise_minimum(tile_lo, q < valid ? x : INFINITY);
+          tile_hi = __builtin_elementwise_maximum(tile_hi, q < valid ? x : -INFINITY);
+        }
       }
       lo = __builtin_elementwise_minimum(lo, tile_lo);
       hi = __builtin_elementwise_maximum(hi, tile_hi);
@@ -610,6 +619,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       g = 0;
       ++qt;
     }
+  };
+  f32x16 acc_a = logits(0), acc_b = mfma_tile_zero();
+  for (int u = 0, buf = 0; u < units; u += 2) {
+    step(u, buf, acc_a, acc_b);
+    buf = buf == 2 ? 0 : buf + 1;
+    if (u + 1 < units) step(u + 1, buf, acc_b, acc_a);
+    buf = buf == 2 ? 0 : buf + 1;
   }
   if (bad_reg) rowbad_lds = 1;
   __syncthreads();
