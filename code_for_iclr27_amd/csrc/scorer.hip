@@ -47,6 +47,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxGroups = 16;
 constexpr int kMaxQueryTiles = 256;  // window <= 8192
 constexpr int kTileKeys = 128;       // candidate keys per column-pass workgroup
+constexpr int kProjectedRowsPerLane = 4;  // V rows each projected-values lane loads at once
 
 struct Segment {
   const __bf16* keys;
@@ -119,36 +120,61 @@ __device__ __forceinline__ double risk64(double margin, double probability, doub
 // ---------------------------------------------------------------------------------------
 // 1. Projected values pv[g, t] = grad[g] . V[t] for every key of every segment. A lane group
 // of D/8 lanes reads one V row with 16-byte loads (fully coalesced); each lane forms its
-// 8-column partial dot product per group and the group reduces across its lanes.
+// 8-column partial dot product per group and the group reduces across its lanes. A workgroup
+// covers kRows * RPB consecutive rows and every lane issues its kRows row loads before any
+// arithmetic, so several loads per lane are in flight.
 template <int D>
 __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __restrict__ table,
-                                                               int64_t groups,
+                                                               int64_t groups64,
                                                                float* __restrict__ pv,
                                                                int* __restrict__ nonfinite) {
   constexpr int LPR = D / 8;         // lanes per row
   constexpr int RPB = 256 / LPR;     // rows per block step
+  constexpr int kRows = kProjectedRowsPerLane;
   __shared__ float grad[kMaxGroups * D];
   const Segment seg = load_segment(table, blockIdx.y);
+  const int groups = static_cast<int>(groups64);
   if (nonfinite != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *nonfinite = 0;
-  for (int64_t i = threadIdx.x; i < groups * D; i += 256) grad[i] = seg.gradient[i];
-  __syncthreads();
+  for (int i = threadIdx.x; i < groups * D; i += 256) grad[i] = seg.gradient[i];
   const int lane = threadIdx.x % LPR;
-  const int64_t row_slot = threadIdx.x / LPR;
+  const int length = static_cast<int>(seg.length);
+  const int base = static_cast<int>(blockIdx.x) * (kRows * RPB) + static_cast<int>(threadIdx.x / LPR);
+  float x[kRows][8];
+#pragma unroll
+  for (int k = 0; k < kRows; ++k) {
+    const int t = base + k * RPB;
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = static_cast<__bf16>(0.0f);
+    if (t < length) v = gload<bf16x8>(seg.values + static_cast<int64_t>(t) * D + 8 * lane);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[k][e] = static_cast<float>(v[e]);
+  }
+  __syncthreads();
   float* out = pv + seg.pv_offset;
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * RPB + row_slot; t < seg.length;
-       t += static_cast<int64_t>(gridDim.x) * RPB) {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(seg.values + t * D + 8 * lane);
-    float x[8];
+  for (int g = 0; g < groups; ++g) {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(grad + g * D + 8 * lane);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(grad + g * D + 8 * lane + 4);
+    float acc[kRows];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = static_cast<float>(v[e]);
-    for (int64_t g = 0; g < groups; ++g) {
-      const float* w = grad + g * D + 8 * lane;
-      float acc = 0.0f;
+    for (int k = 0; k < kRows; ++k) {
+      float a = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(w[e], x[e], acc);
+      for (int e = 0; e < 4; ++e) a = __builtin_fmaf(w0[e], x[k][e], a);
 #pragma unroll
-      for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, LPR);
-      if (lane == 0) out[g * seg.length + t] = acc;
+      for (int e = 0; e < 4; ++e) a = __builtin_fmaf(w1[e], x[k][4 + e], a);
+      acc[k] = a;
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1)
+#pragma unroll
+      for (int k = 0; k < kRows; ++k) acc[k] += __shfl_xor(acc[k], o, LPR);
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < kRows; ++k) {
+        const int t = base + k * RPB;
+        if (t < length) out[static_cast<int64_t>(g) * length + t] = acc[k];
+      }
     }
   }
 }
@@ -700,7 +726,7 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
                  hipStream_t stream) {
   if (stages & 1) {
     constexpr int rows_per_block = 256 / (D / 8);
-    dim3 pv_grid(static_cast<unsigned>(ceil_div(max_length, 4 * rows_per_block)),
+    dim3 pv_grid(static_cast<unsigned>(ceil_div(max_length, kProjectedRowsPerLane * rows_per_block)),
                  static_cast<unsigned>(segments));
     projected_values_kernel<D><<<pv_grid, 256, 0, stream>>>(table, groups, pv, nonfinite);
     if (int rc = check_launch("projected_values")) return rc;
