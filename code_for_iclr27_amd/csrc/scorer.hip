@@ -261,7 +261,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   __shared__ __bf16 k_lds[2][64 * D];  // swizzled rows
   __shared__ float pv_lds[2][kMaxGroups * 64];
   __shared__ float kpos_lds[2][64];
-  __shared__ float kmax_lds[2];
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
   const int per = static_cast<int>(wg_per_segment);
@@ -319,13 +318,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
                    : INFINITY;
   };
   auto commit = [&](int buf) {
-    if (threadIdx.x < 64) {
-      kpos_lds[buf][threadIdx.x] = kpos_reg;
-      float m = kpos_reg;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      if (threadIdx.x == 0) kmax_lds[buf] = m;
-    }
+    if (threadIdx.x < 64) kpos_lds[buf][threadIdx.x] = kpos_reg;
   };
 
   float m_run = -INFINITY, S = 0.0f, A = 0.0f;
@@ -386,7 +379,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     const bool more = kt + 1 < ktiles;
     if (more) fetch(kt + 1, buf ^ 1);  // buf ^ 1 was last read before the previous barrier
     if (active) {
-      if (uniform(kmax_lds[buf] > qmin ? 1 : 0)) stage(buf, std::true_type{});
+      // masked form only if some key of the stage lies after some query of this wave
+      if (__any(kpos_lds[buf][lane] > qmin)) stage(buf, std::true_type{});
       else stage(buf, std::false_type{});
     }
     if (more) {
