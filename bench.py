@@ -17,6 +17,10 @@ Also reported on the same line:
                 oracle/cpu_path.py) on a bounded sample of the same workload, host cores
   reinsert      cfg3 recall reinsertion: pinned-host -> HBM copy of 512 recalled K/V rows per
                 (layer, head) (link GB/s) and the merge of all 32 layers (HBM GB/s)
+  ops           the other data-movement entry points on their own shapes (append, the legacy
+                flat-cache ops, per-layer compact, pack, cfg2 batch_append): device time per
+                call from a held stream, GB/s against the HBM peak, host-inclusive step time
+  audit_configs the audit step on cfg0 (Llama-3.2-1B) and cfg4 (Qwen3.5-style, d256, G6)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg1]
 """
@@ -51,6 +55,10 @@ def parse_args():
                         help="target CPU work for the bounded CPU-baseline sample")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--no-reinsert", action="store_true", help="skip the cfg3 reinsertion")
+    parser.add_argument("--no-ops", action="store_true",
+                        help="skip the append / legacy / pack / cfg2 batch-append measurements")
+    parser.add_argument("--other-configs", default="cfg0,cfg4",
+                        help="comma-separated further audit configurations to time ('' for none)")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="first run one plain elementwise copy (negation) of MIB MiB f32, "
                              "the reference dispatch for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -213,6 +221,222 @@ def reinsert_bench(torch, seed, reps=5):
     }
 
 
+class HeldStream:
+    """Device time of a run of calls without the host's enqueue gaps: a bounded spin kernel
+    (torch.cuda._sleep) holds the current stream while the host enqueues the calls and an event
+    after each, so consecutive events bracket the calls back to back on the device."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        cycles = 1 << 22
+        a, b = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+        torch.cuda.synchronize()
+        a.record()
+        torch.cuda._sleep(cycles)
+        b.record()
+        torch.cuda.synchronize()
+        self.cycles_per_ms = cycles / max(a.elapsed_time(b), 1e-3)
+
+    def run(self, calls, hold_ms=20.0):
+        """Returns (per-call device microseconds, host enqueue milliseconds); the hold is
+        lengthened and the run repeated while the enqueue outlasts it."""
+        torch = self.torch
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
+        while True:
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(self.cycles_per_ms * hold_ms))
+            started = time.perf_counter()
+            events[0].record()
+            for call, event in zip(calls, events[1:]):
+                call()
+                event.record()
+            enqueue_ms = (time.perf_counter() - started) * 1e3
+            torch.cuda.synchronize()
+            if enqueue_ms < 0.8 * hold_ms or hold_ms > 2000:
+                break
+            hold_ms *= 4
+        return [a.elapsed_time(b) * 1e3 for a, b in zip(events, events[1:])], enqueue_ms
+
+
+def _op_line(workload, calls, device_us, nbytes, wall_ms):
+    """One `ops` entry: median device time per call, bytes per call, HBM roofline fraction."""
+    import numpy as np
+
+    us = float(np.median(device_us))
+    gbps = nbytes / (us / 1e6) / 1e9
+    return {"workload": workload, "calls_per_step": calls, "device_us_per_call": round(us, 2),
+            "bytes_per_call": int(nbytes), "GBps": round(gbps, 1),
+            "hbm_fraction": round(gbps / HBM_PEAK_GBPS, 4),
+            "wall_ms_per_step": round(wall_ms, 3)}
+
+
+def ops_bench(torch, seed, reps=5):
+    """The scope table's data-movement rows outside the audit step, on their own shapes:
+    decode-time appends (cfg1 layer, cfg2 static batch), the legacy flat-cache ops, the per-layer
+    compaction and the eviction archive pack. Each call's device time comes from a held stream;
+    wall_ms_per_step is the host-inclusive time of one decode/audit step's worth of calls."""
+    import numpy as np
+
+    from code_for_iclr27_amd import _C, _legacy_C
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 7)
+    rng = np.random.default_rng(seed + 7)
+    held = HeldStream(torch)
+    bf16 = torch.bfloat16
+    L, H, d, T, E = 32, 8, 128, 2250, 250  # cfg1 layer shape, 250 evicted per head
+    rows = H * T
+
+    def randn(*shape):
+        return torch.randn(shape, generator=gen, device=dev).to(bf16)
+
+    def measure(make_calls, per_step):
+        calls = make_calls()
+        for call in calls[:2]:  # warm the allocator and the library
+            call()
+        device = []
+        for _ in range(reps):
+            us, _ = held.run(calls)
+            device.extend(us)
+        torch.cuda.synchronize()
+        walls = []
+        for _ in range(reps):
+            started = time.perf_counter()
+            for call in calls[:per_step]:
+                call()
+            torch.cuda.synchronize()
+            walls.append((time.perf_counter() - started) * 1e3)
+        return device, float(np.median(walls))
+
+    out = {}
+    keys = [randn(rows, d) for _ in range(2)]
+    values = [randn(rows, d) for _ in range(2)]
+    positions = torch.arange(T, dtype=torch.float32, device=dev).repeat(H)[:, None].contiguous()
+    cumulative = torch.arange(0, rows + 1, T, dtype=torch.int32, device=dev)
+    new_k, new_v = randn(1, H, 1, d), randn(1, H, 1, d)
+
+    # a10 append: one token per head into every layer (cache.py:33-52)
+    device, wall = measure(lambda: [
+        (lambda l=l: _C.append(keys[l % 2], values[l % 2], positions, new_k, new_v, cumulative,
+                               T, T)) for l in range(L)], L)
+    nbytes = 2 * rows * d * 2 + 2 * (rows + H) * d * 2 + rows * 4 + (rows + H) * 4 + 2 * H * d * 2
+    out["append"] = _op_line("cfg1 layer: 8 heads x 2250 rows + 1 token per head, bf16 d128", L,
+                             device, nbytes, wall)
+
+    # a11 append_flattened_cache: K and V of every layer (cache_legacy.cu:145-197)
+    head_lens = torch.full((H,), T, dtype=torch.int32, device=dev)
+    device, wall = measure(lambda: [
+        (lambda l=l: _legacy_C.append_flattened_cache(keys[l % 2], new_k, head_lens, cumulative))
+        for l in range(2 * L)], 2 * L)
+    nbytes = rows * d * 2 + (rows + H) * d * 2 + H * d * 2
+    out["append_flattened_cache"] = _op_line("cfg1 layer K (or V): 8 heads x 2250 rows + 1 token",
+                                             2 * L, device, nbytes, wall)
+
+    # eviction of 250 rows per head, as an audit removes them (sorted absolute rows)
+    removed = np.sort(np.concatenate([h * T + rng.choice(T - 32, E, replace=False)
+                                      for h in range(H)])).astype(np.int64)
+    keep = np.setdiff1d(np.arange(rows), removed)
+    removed_d = torch.from_numpy(removed).to(dev)
+    keep_d = torch.from_numpy(keep).to(dev)
+    kept = keep.size
+
+    # a9 compact, per layer (scoring.cu:294-314)
+    device, wall = measure(lambda: [
+        (lambda l=l: _C.compact(keys[l % 2], values[l % 2], positions, removed_d))
+        for l in range(L)], L)
+    nbytes = 2 * kept * d * 2 * 2 + kept * 4 * 2 + removed.size * 8
+    out["compact"] = _op_line("cfg1 layer: remove 250 of 2250 rows per head", L, device, nbytes,
+                              wall)
+
+    # a12 compact_flattened_kv (cache_legacy.cu:199-242)
+    device, wall = measure(lambda: [
+        (lambda l=l: _legacy_C.compact_flattened_kv(keys[l % 2], values[l % 2], keep_d))
+        for l in range(L)], L)
+    nbytes = 2 * kept * d * 2 * 2 + kept * 8
+    out["compact_flattened_kv"] = _op_line("cfg1 layer: keep 2000 of 2250 rows per head", L,
+                                           device, nbytes, wall)
+
+    # a16 pack: archive the evicted rows of every layer (transport.py:129-177)
+    heads_d = torch.from_numpy(removed // T).to(dev)
+    payload = torch.empty((removed.size, 2, d), dtype=bf16, device=dev)
+    meta = torch.empty((removed.size, 3), dtype=torch.int64, device=dev)
+    device, wall = measure(lambda: [
+        (lambda l=l: _C.pack(keys[l % 2], values[l % 2], positions, removed_d, heads_d, l,
+                             payload, meta)) for l in range(L)], L)
+    nbytes = removed.size * (2 * d * 2 * 2 + 4 + 8 + 8 + 3 * 8)
+    out["pack"] = _op_line("cfg1 layer: 2000 evicted rows -> [2000, 2, 128] payload", L, device,
+                           nbytes, wall)
+    del keys, values, positions, payload, meta
+
+    # a14 batch_append, cfg2: 8 requests with per-head lengths U[1500, 2250], one token each
+    R = 8
+    lengths = [[int(x) for x in rng.integers(1500, 2251, H)] for _ in range(R)]
+    totals = [sum(l) for l in lengths]
+    req_k = [[randn(n, d) for n in totals] for _ in range(2)]
+    req_v = [[randn(n, d) for n in totals] for _ in range(2)]
+    req_p = [torch.cat([torch.arange(n, dtype=torch.float32, device=dev) for n in l])[:, None]
+             for l in lengths]
+    nk, nv = randn(R, H, 1, d), randn(R, H, 1, d)
+    logical = [max(l) for l in lengths]
+    device, wall = measure(lambda: [
+        (lambda l=l: _C.batch_append(req_k[l % 2], req_v[l % 2], req_p, nk, nv, lengths, logical))
+        for l in range(L)], L)
+    n = sum(totals)
+    nbytes = 2 * n * d * 2 + 2 * (n + R * H) * d * 2 + n * 4 + (n + R * H) * 4 + 2 * R * H * d * 2
+    out["batch_append"] = _op_line(
+        f"cfg2 layer: 8 requests x 8 heads, {n} rows (U[1500,2250] per head) + 1 token each",
+        L, device, nbytes, wall)
+    del req_k, req_v, req_p
+    torch.cuda.empty_cache()
+    return out
+
+
+def audit_config_bench(torch, name, seed, steps=10, warmup=3):
+    """A shorter audit-step measurement of another BASELINE configuration (cfg0, cfg4)."""
+    import numpy as np
+
+    from code_for_iclr27_amd import audit, workloads
+
+    cfg = workloads.CONFIGS[name]
+    dev = torch.device("cuda:0")
+    layers, qpos, margin = workloads.make_audit(cfg, dev, seed=seed, generator_device="cuda")
+    step = audit.AuditStep()
+
+    def run(timer=None):
+        return step.run(layers, qpos, margin, cfg.count, cfg.protect_recent, cfg.pool_kernel,
+                        cfg.epsilon, timer=timer)
+
+    for _ in range(warmup):
+        outcome = run()
+    torch.cuda.synchronize()
+    started = time.perf_counter()
+    for _ in range(steps):
+        outcome = run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - started) * 1e3 / steps
+    timers = [EventTimer(torch) for _ in range(3)]
+    for timer in timers:
+        run(timer)
+    torch.cuda.synchronize()
+    stages = {}
+    for timer in timers:
+        for stage, us in timer.stages().items():
+            stages[stage] = stages.get(stage, 0.0) + us / len(timers)
+    rows_total = sum(layer.keys.size(0) for layer in layers)
+    nbytes = audit_bytes(cfg, rows_total, outcome.removed, int(outcome.scores.numel()),
+                         len(outcome.segments))
+    line = {"workload": f"{cfg.name}: L{cfg.layers} H{cfg.heads} d{cfg.dim} G{cfg.groups} "
+                        f"T{cfg.length} W{cfg.window}, evict {cfg.evict_per_head} per head",
+            "ms_per_step": round(ms, 4), "GBps": round(nbytes / (ms / 1e3) / 1e9, 1),
+            "hbm_fraction": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "algorithmic_bytes": nbytes, "evicted": outcome.removed,
+            "stages_us": {k: round(v, 1) for k, v in stages.items()}}
+    del layers, outcome, step
+    torch.cuda.empty_cache()
+    return line
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -337,11 +561,17 @@ def main():
         "roofline": roofline,
     }
 
+    del outcome
+    torch.cuda.empty_cache()
     if not args.no_reinsert:
-        del outcome
-        torch.cuda.empty_cache()
         line["reinsert"] = reinsert_bench(torch, args.seed)
         torch.cuda.empty_cache()
+    if not args.no_ops:
+        line["ops"] = ops_bench(torch, args.seed)
+    others = [name for name in args.other_configs.split(",") if name and name != args.config]
+    if others:
+        line["audit_configs"] = {name: audit_config_bench(torch, name, args.seed)
+                                 for name in others}
 
     if not args.no_cpu:
         n, seconds, scaled, threads = cpu_baseline(torch, layers, qpos, margin, cfg, args.cpu_seconds)
