@@ -213,15 +213,35 @@ struct TileStager {
 // granule at LDS `wave_base` + L * granule; `wave_base` must be the same for the whole wave.
 // Nothing passes through VGPRs. Completion is awaited with dma_wait() before the barrier that
 // publishes the data.
+// The copies are issued by inline assembly, not by the compiler's builtin: for the builtin the
+// compiler makes every later LDS read that it cannot prove disjoint from the copy wait for it
+// (s_waitcnt vmcnt(0)), and a buffer picked at run time is never provably disjoint, so the
+// copy of the next stage would be waited for at the first read of the current one. Copies the
+// compiler does not see only lengthen its own vmcnt waits (counts drain in order), never
+// shorten them. M0 (the wave's LDS base for the copy) is set inside the same statement; no
+// compiler-generated code in these kernels keeps a value in M0.
+__device__ __forceinline__ uint32_t lds_base(void* wave_base) {
+  const auto lds = (__attribute__((address_space(3))) void*)wave_base;
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is a reserved register; clobbered on purpose
 __device__ __forceinline__ void dma16(const void* src, void* wave_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                   (__attribute__((address_space(3))) void*)wave_base, 16, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds_base(wave_base)) : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* src, void* wave_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                   (__attribute__((address_space(3))) void*)wave_base, 4, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(src), "s"(lds_base(wave_base)) : "memory", "m0");
 }
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+#pragma clang diagnostic pop
+// vmcnt(0) through the builtin, so that the compiler knows every vector-memory load has landed
+// here (loads issued before a loop, such as the resident MFMA operands, are then not waited for
+// again inside it); the empty statement keeps LDS accesses from moving across the wait.
+__device__ __forceinline__ void dma_wait() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+  asm volatile("" ::: "memory");
+}
 
 // Swizzled LDS rows: D bf16 per row, no padding; 16-byte chunk c of row r is stored in chunk
 // slot c ^ (r & 7), so the 32 lanes that read chunk c of 32 consecutive rows (an MFMA operand)
@@ -299,9 +319,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   const int ktiles = (length + 63) / 64;  // 64-key stages: two 32-key MFMA tiles each
   const float* pv_seg = pv + seg.pv_offset;
 
-  float kpos_reg = INFINITY;
-  // Key stage kt -> LDS buffer `buf`: K rows and projected values by DMA (rows past the end
-  // re-read the last row; their key position +inf masks them), key positions via VGPRs.
+  // Key stage kt -> LDS buffer `buf`, all by direct copy: K rows, projected values and key
+  // positions (rows past the end re-read the last row; commit() then gives their positions
+  // +inf, which masks them). No compiler-visible load is left in the loop, so no wait the
+  // compiler adds can fall between issuing the copies and the stage's LDS reads.
   auto fetch = [&](int kt, int buf) {
     const int t0 = kt * 64;
     dma_rows<D, 64>(seg.keys, t0, length - 1, k_lds[buf]);
@@ -313,12 +334,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
         dma4(pv_seg + static_cast<int64_t>(gg) * length + min(t0 + lane_slot, length - 1),
              &pv_lds[buf][256 * i + wave_slot]);
     }
-    kpos_reg = (threadIdx.x < 64 && t0 + static_cast<int>(threadIdx.x) < length)
-                   ? gload<float>(seg.key_positions + t0 + threadIdx.x)
-                   : INFINITY;
+    if (threadIdx.x < 64) dma4(seg.key_positions + min(t0 + lane_slot, length - 1), kpos_lds[buf]);
   };
-  auto commit = [&](int buf) {
-    if (threadIdx.x < 64) kpos_lds[buf][threadIdx.x] = kpos_reg;
+  // After dma_wait(): the wave that copied the key positions overwrites those of rows past the
+  // end (its own copy has landed, and LDS accesses of one wave complete in order).
+  auto commit = [&](int kt, int buf) {
+    if (threadIdx.x < 64 && kt * 64 + static_cast<int>(threadIdx.x) >= length)
+      kpos_lds[buf][threadIdx.x] = INFINITY;
   };
 
   float m_run = -INFINITY, S = 0.0f, A = 0.0f;
@@ -372,7 +394,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 
   fetch(0, 0);
   dma_wait();
-  commit(0);
+  commit(0, 0);
   __syncthreads();
   for (int kt = 0; kt < ktiles; ++kt) {
     const int buf = kt & 1;
@@ -385,7 +407,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     }
     if (more) {
       dma_wait();
-      commit(buf ^ 1);
+      commit(kt + 1, buf ^ 1);
     }
     __syncthreads();
   }
@@ -485,9 +507,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   bool row_loaded = false;
   int bad_reg = 0;
   int fetch_qt = 0, fetch_g = 0;  // unit of the next fetch, (query tile, group)
+  // The statistics loads go first: a wait the compiler adds before them (they reuse the
+  // registers of the previous unit's loads) then falls before the copies are issued.
   auto fetch = [&](int buf) {
-    dma_rows<D, 32>(seg.queries + static_cast<int64_t>(fetch_g) * query_stride * D,
-                    fetch_qt * 32, window - 1, q_lds[buf]);
     if (threadIdx.x < 32) {
       const int query = fetch_qt * 32 + threadIdx.x;
       row_loaded = query < window;
@@ -496,6 +518,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
         qp_raw = query_positions[query];
       }
     }
+    dma_rows<D, 32>(seg.queries + static_cast<int64_t>(fetch_g) * query_stride * D,
+                    fetch_qt * 32, window - 1, q_lds[buf]);
     if (++fetch_g == groups) {
       fetch_g = 0;
       ++fetch_qt;
@@ -569,40 +593,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     const float4 st = st_lds[buf][col];
     const float query_position = qp_lds[buf][col];
     const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
-    // kGeneral: causal mask and denominator clamp. The fast form drops both, which is exact
-    // when no key of this wave lies after any query of the unit and every row has S >= 2 and
-    // eps*S <= 1/2: then e <= 1 gives S - e >= 1 > eps*S, so max(S - e, eps*S) == S - e.
-    auto epilogue = [&](auto general) {
-      constexpr bool kGeneral = decltype(general)::value;
+    // ratio = p / max(1 - p, eps) = e / max(S - e, eps*S) for the lane's 16 (key, query) pairs.
+    // The general form applies the causal mask and the clamp. The fast form drops both, which
+    // is exact when no key of this wave lies after any query of the unit and every row has
+    // S >= 2 and eps*S <= 1/2: then e <= 1 gives S - e >= 1 > eps*S. It also takes the ratio
+    // as 1 / (S*u - 1) with u = 1/e = exp(m - z), one operation fewer than e / (S - e).
+    float ratio[16];
+    if (__any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f))) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
-        f32x4 kp;
-        if constexpr (kGeneral) kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
+        const f32x4 kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * c + j;
           float z = logit_fast(acc[r], scale);
-          if constexpr (kGeneral) z = kp[j] <= query_position ? z : -INFINITY;
+          z = kp[j] <= query_position ? z : -INFINITY;
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
-          const float denominator = kGeneral ? fmaxf(st.y - e, st.z) : st.y - e;
-          const float ratio = e * __builtin_amdgcn_rcpf(denominator);
-          drop[r] = __builtin_fmaf(ratio, w[j] - st.w, drop[r]);
+          ratio[r] = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
         }
       }
-    };
-    if (__any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f))) epilogue(std::true_type{});
-    else epilogue(std::false_type{});
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float u = __builtin_amdgcn_exp2f(__builtin_fmaf(logit_fast(acc[r], scale), -kLog2e, -st.x));
+        ratio[r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, u, -1.0f));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) drop[4 * c + j] = __builtin_fmaf(ratio[4 * c + j], w[j] - st.w, drop[4 * c + j]);
+    }
+    if (u + 2 < units) {
+      dma_wait();
+      commit(buf2);
+    }
     if (g == groups - 1) {
       // Min / max of the tile's drops over its queries, through this wave's LDS scratch. LDS
-      // accesses of one wave complete in order, so the reads see this wave's writes.
+      // accesses of one wave complete in order, so the reads see this wave's writes. It runs
+      // after the wait for the next units' direct copies into LDS: the compiler makes every LDS
+      // read wait for outstanding copies, which here have already landed.
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         *reinterpret_cast<f32x4*>(red + lane * 16 + 4 * c) =
             f32x4{drop[4 * c], drop[4 * c + 1], drop[4 * c + 2], drop[4 * c + 3]};
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
       const float* column = red + (half_red * 32 + part * 16) * 16 + r_red;
       float tile_lo = INFINITY, tile_hi = -INFINITY;
       // NaN-propagating, as torch's amin / amax; padded queries of a partial last tile skipped
@@ -624,15 +662,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       }
       lo = __builtin_elementwise_minimum(lo, tile_lo);
       hi = __builtin_elementwise_maximum(hi, tile_hi);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
       for (int r = 0; r < 16; ++r) drop[r] = 0.0f;
-    }
-    if (u + 2 < units) {
-      dma_wait();
-      commit(buf2);
     }
     __syncthreads();
     if (++g == groups) {
