@@ -47,7 +47,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxGroups = 16;
 constexpr int kMaxQueryTiles = 256;  // window <= 8192
 constexpr int kTileKeys = 128;       // candidate keys per column-pass workgroup
-constexpr int kProjectedRowsPerLane = 4;  // V rows each projected-values lane loads at once
+constexpr int kProjectedRowsPerLane = 8;  // V rows each projected-values lane loads at once
 
 struct Segment {
   const __bf16* keys;
@@ -119,18 +119,61 @@ __device__ __forceinline__ double risk64(double margin, double probability, doub
 
 // ---------------------------------------------------------------------------------------
 // 1. Projected values pv[g, t] = grad[g] . V[t] for every key of every segment. A lane group
-// of D/8 lanes reads one V row with 16-byte loads (fully coalesced); each lane forms its
-// 8-column partial dot product per group and the group reduces across its lanes. A workgroup
-// covers kRows * RPB consecutive rows and every lane issues its kRows row loads before any
-// arithmetic, so several loads per lane are in flight.
+// of D/8 lanes reads one V row with 16-byte loads (fully coalesced); each lane issues all its
+// kRows row loads before any arithmetic, so several loads per lane are in flight. Per chunk of
+// four groups, a lane holds 16 partial sums (4 rows x 4 groups, each over its 8 columns); a
+// reduce-scatter across the lane group (DPP exchanges within a 16-lane row, a shuffle across
+// rows) leaves every lane with whole sums, which it stores.
+constexpr int kQuadXor1 = 0xB1;       // DPP quad_perm [1,0,3,2]: partner lane ^ 1
+constexpr int kQuadXor2 = 0x4E;       // DPP quad_perm [2,3,0,1]: partner lane ^ 2
+constexpr int kRowHalfMirror = 0x141;  // DPP: lane i <-> 7 - i within each 8 lanes (differs in bit 2)
+constexpr int kRowMirror = 0x140;      // DPP: lane i <-> 15 - i within each 16 lanes (differs in bit 3)
+
+// The value of the partner lane across lane bit `bit` (partners agree on every higher bit).
+template <int BIT>
+__device__ __forceinline__ float partner(float x) {
+  if constexpr (BIT == 0) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kQuadXor1, 0xF, 0xF, false));
+  else if constexpr (BIT == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kQuadXor2, 0xF, 0xF, false));
+  else if constexpr (BIT == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kRowHalfMirror, 0xF, 0xF, false));
+  else if constexpr (BIT == 3) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kRowMirror, 0xF, 0xF, false));
+  else return __shfl_xor(x, 1 << BIT, 64);
+}
+
+// Reduce-scatter of v[0..N) over the lane bits BIT..0 of `lane`: each stage keeps the half
+// selected by the lane's bit and adds the partner's copy of it; once one value is left the
+// remaining stages add it across partners. Afterwards lane L holds the sums of indices
+// (L >> (bits left over)) * n + [0, n), n = N >> (BIT + 1) (at least 1).
+template <int BIT, int N>
+__device__ __forceinline__ void reduce_scatter(float (&v)[16], int lane) {
+  const bool upper = (lane >> BIT) & 1;
+  if constexpr (N > 1) {
+    constexpr int H = N / 2;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float keep = upper ? v[H + i] : v[i];
+      const float send = upper ? v[i] : v[H + i];
+      v[i] = keep + partner<BIT>(send);
+    }
+  } else {
+    v[0] += partner<BIT>(v[0]);
+  }
+  if constexpr (BIT > 0) reduce_scatter<BIT - 1, (N > 1 ? N / 2 : 1)>(v, lane);
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __restrict__ table,
                                                                int64_t groups64,
                                                                float* __restrict__ pv,
                                                                int* __restrict__ nonfinite) {
-  constexpr int LPR = D / 8;         // lanes per row
-  constexpr int RPB = 256 / LPR;     // rows per block step
+  constexpr int LPR = D / 8;          // lanes per row (a power of two, 8..32)
+  constexpr int LOG_LPR = LPR == 8 ? 3 : LPR == 16 ? 4 : 5;
+  static_assert(LPR == (1 << LOG_LPR), "D must be 64, 128 or 256");
+  constexpr int RPB = 256 / LPR;      // lane groups per block
   constexpr int kRows = kProjectedRowsPerLane;
+  static_assert(kRows % 4 == 0, "rows are reduced four at a time");
+  // after the reduce-scatter of 16 values: values per lane, and lanes holding the same sums
+  constexpr int kKept = LOG_LPR >= 4 ? 1 : 16 >> LOG_LPR;
+  constexpr int kCopies = LOG_LPR > 4 ? 1 << (LOG_LPR - 4) : 1;
   __shared__ float grad[kMaxGroups * D];
   const Segment seg = load_segment(table, blockIdx.y);
   const int groups = static_cast<int>(groups64);
@@ -138,44 +181,71 @@ __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __
   for (int i = threadIdx.x; i < groups * D; i += 256) grad[i] = seg.gradient[i];
   const int lane = threadIdx.x % LPR;
   const int length = static_cast<int>(seg.length);
-  const int base = static_cast<int>(blockIdx.x) * (kRows * RPB) + static_cast<int>(threadIdx.x / LPR);
-  float x[kRows][8];
-#pragma unroll
-  for (int k = 0; k < kRows; ++k) {
-    const int t = base + k * RPB;
-    bf16x8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = static_cast<__bf16>(0.0f);
-    if (t < length) v = gload<bf16x8>(seg.values + static_cast<int64_t>(t) * D + 8 * lane);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[k][e] = static_cast<float>(v[e]);
-  }
-  __syncthreads();
+  constexpr int kChunk = kRows * RPB;  // rows per block step
+  const int stride = static_cast<int>(gridDim.x) * kChunk;
   float* out = pv + seg.pv_offset;
-  for (int g = 0; g < groups; ++g) {
-    const f32x4 w0 = *reinterpret_cast<const f32x4*>(grad + g * D + 8 * lane);
-    const f32x4 w1 = *reinterpret_cast<const f32x4*>(grad + g * D + 8 * lane + 4);
-    float acc[kRows];
+  // Block steps of kChunk rows, strided over the grid; the next step's rows are loaded while
+  // the current step's are reduced.
+  auto load = [&](int first, bf16x8 (&raw)[kRows]) {
+    const int base = first + static_cast<int>(threadIdx.x / LPR);
 #pragma unroll
     for (int k = 0; k < kRows; ++k) {
-      float a = 0.0f;
+      const int t = base + k * RPB;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) a = __builtin_fmaf(w0[e], x[k][e], a);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) a = __builtin_fmaf(w1[e], x[k][4 + e], a);
-      acc[k] = a;
+      for (int e = 0; e < 8; ++e) raw[k][e] = static_cast<__bf16>(0.0f);
+      if (t < length) raw[k] = gload<bf16x8>(seg.values + static_cast<int64_t>(t) * D + 8 * lane);
     }
+  };
+  auto reduce = [&](int first, const bf16x8 (&raw)[kRows]) {
+    const int base = first + static_cast<int>(threadIdx.x / LPR);
+    for (int g0 = 0; g0 < groups; g0 += 4) {
+      f32x4 w[4][2];
 #pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1)
+      for (int gl = 0; gl < 4; ++gl) {
+        const bool live = g0 + gl < groups;
+        w[gl][0] = live ? *reinterpret_cast<const f32x4*>(grad + (g0 + gl) * D + 8 * lane) : f32x4{0, 0, 0, 0};
+        w[gl][1] = live ? *reinterpret_cast<const f32x4*>(grad + (g0 + gl) * D + 8 * lane + 4) : f32x4{0, 0, 0, 0};
+      }
 #pragma unroll
-      for (int k = 0; k < kRows; ++k) acc[k] += __shfl_xor(acc[k], o, LPR);
-    if (lane == 0) {
+      for (int k0 = 0; k0 < kRows; k0 += 4) {
+        float v[16];  // index 4 * (row k - k0) + group gl
 #pragma unroll
-      for (int k = 0; k < kRows; ++k) {
-        const int t = base + k * RPB;
-        if (t < length) out[static_cast<int64_t>(g) * length + t] = acc[k];
+        for (int kk = 0; kk < 4; ++kk) {
+          float x[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = static_cast<float>(raw[k0 + kk][e]);
+#pragma unroll
+          for (int gl = 0; gl < 4; ++gl) {
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a = __builtin_fmaf(w[gl][0][e], x[e], a);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a = __builtin_fmaf(w[gl][1][e], x[4 + e], a);
+            v[4 * kk + gl] = a;
+          }
+        }
+        reduce_scatter<LOG_LPR - 1, 16>(v, lane);
+        if (lane % kCopies == 0) {
+#pragma unroll
+          for (int j = 0; j < kKept; ++j) {
+            const int index = (lane / kCopies) * kKept + j;
+            const int t = base + (k0 + index / 4) * RPB;
+            const int g = g0 + index % 4;
+            if (t < length && g < groups) out[static_cast<int64_t>(g) * length + t] = v[j];
+          }
+        }
       }
     }
+  };
+  int first = static_cast<int>(blockIdx.x) * kChunk;
+  bf16x8 cur[kRows], next[kRows];
+  load(first, cur);
+  __syncthreads();  // gradient in LDS
+  for (; first < length; first += stride) {
+    if (first + stride < length) load(first + stride, next);
+    reduce(first, cur);
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) cur[k] = next[k];
   }
 }
 
@@ -753,9 +823,11 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
                  float4* stats, float* pv, float* scores, int* nonfinite, int stages,
                  hipStream_t stream) {
   if (stages & 1) {
+    // about six block steps per block: each block overlaps its next step's loads with the
+    // current step's arithmetic (cfg1 shape: 3 blocks per segment, one wave of resident blocks)
     constexpr int rows_per_block = 256 / (D / 8);
-    dim3 pv_grid(static_cast<unsigned>(ceil_div(max_length, kProjectedRowsPerLane * rows_per_block)),
-                 static_cast<unsigned>(segments));
+    const int64_t steps = ceil_div(max_length, kProjectedRowsPerLane * rows_per_block);
+    dim3 pv_grid(static_cast<unsigned>(ceil_div(steps, int64_t{6})), static_cast<unsigned>(segments));
     projected_values_kernel<D><<<pv_grid, 256, 0, stream>>>(table, groups, pv, nonfinite);
     if (int rc = check_launch("projected_values")) return rc;
   }
