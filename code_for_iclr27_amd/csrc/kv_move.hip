@@ -59,6 +59,24 @@ __device__ __forceinline__ void copy_row(const uint8_t* __restrict__ src, uint8_
   for (int64_t c = lane; c < chunks; c += lanes) d[c] = s[c];
 }
 
+// The same pointer in the global address space (lets the compiler emit global_* instead of
+// flat_* memory instructions for pointers read from device tables).
+template <int G> struct RawGranule;
+template <> struct RawGranule<16> { typedef unsigned type __attribute__((ext_vector_type(4))); };
+template <> struct RawGranule<8> { typedef unsigned type __attribute__((ext_vector_type(2))); };
+template <> struct RawGranule<4> { using type = unsigned; };
+template <> struct RawGranule<2> { using type = unsigned short; };
+template <> struct RawGranule<1> { using type = unsigned char; };
+
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* global_ptr(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* global_ptr(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
 // Lane-group coordinates shared by the row kernels.
 struct GroupCoord {
   int lane, lanes, group, groups_per_block;
@@ -280,62 +298,95 @@ __global__ __launch_bounds__(kThreads) void batch_append_kernel(
 // cache.py:113-178). blockIdx.y = head slot; each head keeps its rows minus the sorted
 // head-relative removal list of its score segment, and lands in one packed output at
 // sum over earlier head slots of (length - quota), derived here from the quotas.
+// Block x covers output rows [x * kCompactRows, ...) of its head. It first maps each of them to
+// its source row (gather rule of csrc/scoring.cu:164-188: output d takes input d + j,
+// j = #{i : removed[i] - i <= d}, by binary search over the removal list, staged in LDS when it
+// fits), copying the positions on the way; then every lane group copies rows with the loads of
+// several rows in flight before their stores. No per-row index work remains in the copy.
+constexpr int kCompactRows = 256;    // output rows per block
+constexpr int kCompactStaged = 4096;  // removal entries staged in LDS (larger lists: global)
+constexpr int kCompactUnroll = 4;     // rows per lane group with loads in flight together
+
 template <int G>
 __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
     const int64_t* __restrict__ head_table, const int64_t* __restrict__ quotas,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ removed_positions,
     RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
+  using V = typename RawGranule<G>::type;  // a plain vector type: stays in registers
   __shared__ int64_t partial[kThreads / 64];
-  const GroupCoord gc = group_coord(layout.lanes_log2);
+  __shared__ int32_t staged[kCompactStaged];
+  __shared__ int64_t source[kCompactRows];
   const int64_t head = blockIdx.y;
+  const int64_t* row = head_table + head * LR_HEAD_WORDS;
+  const int64_t length = row[3], segment = row[4];
+  const int64_t removed_count = segment >= 0 ? quotas[segment] : 0;
+  const int64_t rows_out = length - removed_count;
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kCompactRows;
+  if (d0 >= rows_out) return;  // uniform across the block, before any barrier
   // output start of this head slot
   int64_t before = 0;
   for (int64_t h = threadIdx.x; h < head; h += kThreads) {
-    const int64_t* row = head_table + h * LR_HEAD_WORDS;
-    before += row[3] - (row[4] >= 0 ? quotas[row[4]] : 0);
+    const int64_t* other = head_table + h * LR_HEAD_WORDS;
+    before += other[3] - (other[4] >= 0 ? quotas[other[4]] : 0);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o, 64);
   if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = before;
+  const int64_t* removed = segment >= 0 ? removed_positions + offsets[segment] : nullptr;
+  const bool in_lds = removed_count <= kCompactStaged;
+  if (in_lds)
+    for (int64_t i = threadIdx.x; i < removed_count; i += kThreads)
+      staged[i] = static_cast<int32_t>(removed[i]);
   __syncthreads();
   int64_t out_start = 0;
   for (int w = 0; w < kThreads / 64; ++w) out_start += partial[w];
-  const int64_t* row = head_table + head * LR_HEAD_WORDS;
   const uint8_t* keys = reinterpret_cast<const uint8_t*>(row[0]);
   const uint8_t* values = reinterpret_cast<const uint8_t*>(row[1]);
   const float* positions = reinterpret_cast<const float*>(row[2]);
-  const int64_t length = row[3], segment = row[4];
-  const int64_t removed_count = segment >= 0 ? quotas[segment] : 0;
-  const int64_t* removed = segment >= 0 ? removed_positions + offsets[segment] : nullptr;
-  const int64_t rows_out = length - removed_count;
-  const int64_t R = layout.rows_per_group;
-  const int64_t rb = layout.row_bytes;
-  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
-       first < rows_out;
-       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
+  const int n = static_cast<int>(rows_out - d0 < kCompactRows ? rows_out - d0 : kCompactRows);
+  if (static_cast<int>(threadIdx.x) < n) {
+    const int64_t d = d0 + threadIdx.x;
     int64_t lo = 0, hi = removed_count;
     while (lo < hi) {
       const int64_t mid = (lo + hi) >> 1;
-      if (removed[mid] - mid <= first) lo = mid + 1;
+      const int64_t r = in_lds ? staged[mid] : removed[mid];
+      if (r - mid <= d) lo = mid + 1;
       else hi = mid;
     }
-    int64_t src = first + lo;
-    int64_t next = lo;
-    const int64_t end = first + R < rows_out ? first + R : rows_out;
-    for (int64_t r = first; r < end; ++r) {
-      if (r != first) {
-        ++src;
-        while (next < removed_count && removed[next] == src) {
-          ++src;
-          ++next;
+    const int64_t src = d + lo;
+    const bool valid = src < length;  // a malformed removal list can point past the head
+    source[threadIdx.x] = valid ? src : -1;
+    if (valid) out_positions[out_start + d] = positions[src];
+  }
+  __syncthreads();
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t rb = layout.row_bytes, chunks = layout.chunks;
+  for (int r0 = gc.group; r0 < n; r0 += gc.groups_per_block * kCompactUnroll) {
+    int64_t src[kCompactUnroll], dst[kCompactUnroll];
+#pragma unroll
+    for (int u = 0; u < kCompactUnroll; ++u) {
+      const int r = r0 + u * gc.groups_per_block;
+      src[u] = r < n ? source[r] : -1;
+      dst[u] = out_start + d0 + r;
+    }
+    // Loads are unconditional (rows without a source re-read row 0 of the head, which exists
+    // since n > 0): a load under a branch would be waited for before the next one is issued.
+    for (int64_t c = gc.lane; c < chunks; c += gc.lanes) {
+      V k[kCompactUnroll], v[kCompactUnroll];
+#pragma unroll
+      for (int u = 0; u < kCompactUnroll; ++u) {
+        const int64_t from = src[u] >= 0 ? src[u] : 0;
+        k[u] = global_ptr(reinterpret_cast<const V*>(keys + from * rb))[c];
+        v[u] = global_ptr(reinterpret_cast<const V*>(values + from * rb))[c];
+      }
+#pragma unroll
+      for (int u = 0; u < kCompactUnroll; ++u) {
+        if (src[u] >= 0) {
+          global_ptr(reinterpret_cast<V*>(out_keys + dst[u] * rb))[c] = k[u];
+          global_ptr(reinterpret_cast<V*>(out_values + dst[u] * rb))[c] = v[u];
         }
       }
-      if (src < 0 || src >= length) break;
-      const int64_t dst = out_start + r;
-      copy_row<G>(keys + src * rb, out_keys + dst * rb, layout.chunks, gc.lane, gc.lanes);
-      copy_row<G>(values + src * rb, out_values + dst * rb, layout.chunks, gc.lane, gc.lanes);
-      if (gc.lane == 0) out_positions[dst] = positions[src];
     }
   }
 }
@@ -540,10 +591,11 @@ extern "C" int lr_compact_heads(const int64_t* head_table, int64_t heads, const 
   const int64_t row_bytes = dim * elem_bytes;
   // Head rows are whole rows of 256-byte aligned allocations; the outputs bound the granule.
   const int g = granule_for(row_bytes, {out_keys, out_values});
+  LR_REQUIRE(max_length < (int64_t{1} << 31), "Invalid head table");
   const RowLayout layout = make_layout(row_bytes, g, total_out_rows, 8);
-  int64_t bx = ceil_div(ceil_div(max_length, layout.rows_per_group), kThreads >> layout.lanes_log2);
-  if (bx < 1) bx = 1;
-  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads));
+  const int64_t bx = ceil_div(max_length, kCompactRows);
+  LR_REQUIRE(bx <= 65535, "Invalid head table");
+  dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(heads));
   return dispatch_granule(g, [&]<int G>() {
     compact_heads_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
         head_table, quotas, offsets, removed_positions, layout, bytes(out_keys),

@@ -59,6 +59,53 @@ def test_compact_llama8b_layer(device):
         np.testing.assert_array_equal(bits(g).reshape(e.shape), e)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dim", [128, 64, 3])
+def test_compact_heads(device, dtype, dim):
+    """lr_compact_heads over ragged head slots: several 256-row output chunks per head, a
+    removal list longer than the LDS-staged limit (4096), a head without a score segment, a
+    head losing every row, an empty head; packed in head-slot order."""
+    from code_for_iclr27_amd import _lib
+
+    rng = np.random.default_rng(dim)
+    lengths = [700, 9000, 0, 300, 257, 1]
+    segment_of = [0, 1, -1, 2, 3, -1]
+    removals = {0: np.sort(rng.choice(700, 90, replace=False)),
+                1: np.sort(rng.choice(9000, 5000, replace=False)),
+                2: np.arange(300),
+                3: np.asarray([0, 255, 256])}
+    keys = [rand((n, dim), dtype, device, 40 + h) for h, n in enumerate(lengths)]
+    values = [rand((n, dim), dtype, device, 50 + h) for h, n in enumerate(lengths)]
+    positions = [torch.from_numpy(rng.permutation(n).astype(np.float32)).to(device) for n in lengths]
+    table = np.zeros((len(lengths), 6), np.int64)
+    for h, n in enumerate(lengths):
+        table[h, :5] = [keys[h].data_ptr(), values[h].data_ptr(), positions[h].data_ptr(), n,
+                        segment_of[h]]
+    quotas = np.asarray([len(removals[s]) for s in range(4)], np.int64)
+    offsets = np.concatenate(([0], np.cumsum(quotas)[:-1])).astype(np.int64)
+    flat = np.concatenate([removals[s] for s in range(4)]).astype(np.int64)
+    out_rows = sum(lengths) - int(quotas.sum())
+    out_k = torch.empty((out_rows, dim), dtype=dtype, device=device)
+    out_v = torch.empty_like(out_k)
+    out_p = torch.empty((out_rows,), dtype=torch.float32, device=device)
+    on = lambda a: torch.from_numpy(a).to(device)
+    table_d, quotas_d, offsets_d, flat_d = on(table), on(quotas), on(offsets), on(flat)
+    _lib.call("lr_compact_heads", table_d.data_ptr(), len(lengths), quotas_d.data_ptr(),
+              offsets_d.data_ptr(), flat_d.data_ptr(), dim, out_k.element_size(), max(lengths),
+              out_rows, out_k.data_ptr(), out_v.data_ptr(), out_p.data_ptr(),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    expect_k, expect_v, expect_p = [], [], []
+    for h, n in enumerate(lengths):
+        gone = removals[segment_of[h]] if segment_of[h] >= 0 else np.zeros(0, np.int64)
+        ek, ev, ep = kv_ops.compact(bits(keys[h]), bits(values[h]), positions[h].cpu().numpy(),
+                                    gone.astype(np.int64))
+        expect_k.append(ek), expect_v.append(ev), expect_p.append(ep.reshape(-1))
+    np.testing.assert_array_equal(bits(out_k), np.concatenate(expect_k))
+    np.testing.assert_array_equal(bits(out_v), np.concatenate(expect_v))
+    np.testing.assert_array_equal(out_p.cpu().numpy(), np.concatenate(expect_p))
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("added", [1, 3])
 @pytest.mark.parametrize("dim", [128, 5])
