@@ -13,6 +13,7 @@ namespace lr {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kBatch = 4;  // rows a lane group copies with all their loads in flight together
 
 struct RowLayout {
   int64_t row_bytes;  // bytes per row (dim * element size)
@@ -35,8 +36,9 @@ inline RowLayout make_layout(int64_t row_bytes, int granule, int64_t rows, int m
   layout.lanes_log2 = log2_ceil(layout.chunks < 64 ? layout.chunks : 64);
   const int64_t lanes = int64_t{1} << layout.lanes_log2;
   const int64_t target_groups = (int64_t{256} * 2048) / lanes;  // ~full residency on 256 CUs
-  int64_t r = ceil_div(rows, target_groups);
-  if (r < 1) r = 1;
+  // whole batches of rows per lane group (the kernels copy kBatch rows at a time)
+  int64_t r = ceil_div(ceil_div(rows, target_groups), kBatch) * kBatch;
+  if (r < kBatch) r = kBatch;
   if (r > max_rows_per_group) r = max_rows_per_group;
   layout.rows_per_group = static_cast<int>(r);
   return layout;
@@ -50,24 +52,15 @@ inline int64_t blocks_for(const RowLayout& layout, int64_t rows) {
   return blocks < kMaxGridX ? blocks : kMaxGridX;
 }
 
-template <int G>
-__device__ __forceinline__ void copy_row(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
-                                         int64_t chunks, int lane, int lanes) {
-  using V = typename Granule<G>::type;
-  const V* s = reinterpret_cast<const V*>(src);
-  V* d = reinterpret_cast<V*>(dst);
-  for (int64_t c = lane; c < chunks; c += lanes) d[c] = s[c];
-}
-
-// The same pointer in the global address space (lets the compiler emit global_* instead of
-// flat_* memory instructions for pointers read from device tables).
-template <int G> struct RawGranule;
+template <int G> struct RawGranule;  // plain vector types: arrays of them stay in registers
 template <> struct RawGranule<16> { typedef unsigned type __attribute__((ext_vector_type(4))); };
 template <> struct RawGranule<8> { typedef unsigned type __attribute__((ext_vector_type(2))); };
 template <> struct RawGranule<4> { using type = unsigned; };
 template <> struct RawGranule<2> { using type = unsigned short; };
 template <> struct RawGranule<1> { using type = unsigned char; };
 
+// The same pointer in the global address space (lets the compiler emit global_* instead of
+// flat_* memory instructions for pointers read from device tables).
 template <typename T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* global_ptr(const T* p) {
   return (const __attribute__((address_space(1))) T*)p;
@@ -91,47 +84,113 @@ __device__ __forceinline__ GroupCoord group_coord(int lanes_log2) {
   return g;
 }
 
+// A lane group's batch of up to kBatch rows of one or two tensors (K and V). Every lane issues
+// all its loads of the batch before any store: a load issued under a per-row branch would be
+// waited for before the next one. Rows that are not copied read `src` = a readable fallback
+// row and store nothing.
+
+template <bool kTwo>
+struct RowBatch {
+  const uint8_t* src[kBatch];
+  uint8_t* dst[kBatch];
+  const uint8_t* src2[kBatch];
+  uint8_t* dst2[kBatch];
+  bool ok[kBatch];
+};
+
+template <int G, bool kTwo>
+__device__ __forceinline__ void copy_batch(const RowBatch<kTwo>& b, int64_t chunks, int lane,
+                                           int lanes) {
+  using V = typename RawGranule<G>::type;
+  for (int64_t c = lane; c < chunks; c += lanes) {
+    V x[kBatch], y[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      x[u] = global_ptr(reinterpret_cast<const V*>(b.src[u]))[c];
+      if constexpr (kTwo) y[u] = global_ptr(reinterpret_cast<const V*>(b.src2[u]))[c];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (b.ok[u]) {
+        global_ptr(reinterpret_cast<V*>(b.dst[u]))[c] = x[u];
+        if constexpr (kTwo) global_ptr(reinterpret_cast<V*>(b.dst2[u]))[c] = y[u];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
-// compact: output row r takes input row r + j, j = #{i : removed[i] - i <= r}
-// (the gather rule of csrc/scoring.cu:164-188). One binary search per lane group start, then
-// an incremental walk over the sorted removal list for the following rows.
+// Compaction of one row range: output rows [d0, d0 + n) of a head of `length` rows minus the
+// sorted removal list `removed` land at out_start + d0... Output d takes input d + j,
+// j = #{i : removed[i] - i <= d} (the gather rule of csrc/scoring.cu:164-188). The block first
+// maps each of its n <= kCompactRows output rows to its source by binary search over the
+// removal list (staged in LDS when it fits), copying the positions on the way; then its lane
+// groups copy the rows in batches. Called by every thread of the block (it has barriers).
+constexpr int kCompactRows = 256;     // most output rows per block
+constexpr int kCompactStaged = 4096;  // removal entries staged in LDS (larger lists: global)
+
+template <int G>
+__device__ __forceinline__ void compact_block(const uint8_t* keys, const uint8_t* values,
+                                              const float* positions, int64_t length,
+                                              const int64_t* removed, int64_t removed_count,
+                                              int64_t d0, int n, int64_t out_start,
+                                              const RowLayout& layout, uint8_t* out_keys,
+                                              uint8_t* out_values, float* out_positions) {
+  __shared__ int32_t staged[kCompactStaged];
+  __shared__ int64_t source[kCompactRows];
+  const bool in_lds = removed_count <= kCompactStaged;
+  if (in_lds)
+    for (int64_t i = threadIdx.x; i < removed_count; i += kThreads)
+      staged[i] = static_cast<int32_t>(removed[i]);
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < n) {
+    const int64_t d = d0 + threadIdx.x;
+    int64_t lo = 0, hi = removed_count;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      const int64_t r = in_lds ? staged[mid] : removed[mid];
+      if (r - mid <= d) lo = mid + 1;
+      else hi = mid;
+    }
+    const int64_t src = d + lo;
+    const bool valid = src < length;  // a malformed removal list can point past the head
+    source[threadIdx.x] = valid ? src : -1;
+    if (valid) out_positions[out_start + d] = positions[src];
+  }
+  __syncthreads();
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t rb = layout.row_bytes;
+  for (int r0 = gc.group; r0 < n; r0 += gc.groups_per_block * kBatch) {
+    RowBatch<true> b;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int r = r0 + u * gc.groups_per_block;
+      const int64_t src = r < n ? source[r] : -1;
+      const int64_t from = src >= 0 ? src : 0;  // n > 0, so row 0 of the head exists
+      b.ok[u] = src >= 0;
+      b.src[u] = keys + from * rb;
+      b.src2[u] = values + from * rb;
+      b.dst[u] = out_keys + (out_start + d0 + r) * rb;
+      b.dst2[u] = out_values + (out_start + d0 + r) * rb;
+    }
+    copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+  }
+}
+
+// compact (csrc/scoring.cu:294-314): one flat [rows_in, dim] cache, block x = output rows
+// [x * rows_per_block, ...), rows_per_block <= kCompactRows.
 template <int G>
 __global__ __launch_bounds__(kThreads) void compact_kernel(
     const uint8_t* __restrict__ keys, const uint8_t* __restrict__ values,
     const float* __restrict__ positions, const int64_t* __restrict__ removed,
-    int64_t removed_count, int64_t rows_in, int64_t rows_out, RowLayout layout,
-    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    int64_t removed_count, int64_t rows_in, int64_t rows_out, int rows_per_block,
+    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
-  const GroupCoord gc = group_coord(layout.lanes_log2);
-  const int64_t R = layout.rows_per_group;
-  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
-       first < rows_out;
-       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
-    int64_t lo = 0, hi = removed_count;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if (removed[mid] - mid <= first) lo = mid + 1;
-      else hi = mid;
-    }
-    int64_t src = first + lo;
-    int64_t next = lo;  // removed[next] > src for a well-formed list
-    const int64_t end = first + R < rows_out ? first + R : rows_out;
-    for (int64_t row = first; row < end; ++row) {
-      if (row != first) {
-        ++src;
-        while (next < removed_count && removed[next] == src) {
-          ++src;
-          ++next;
-        }
-      }
-      if (src < 0 || src >= rows_in) break;
-      copy_row<G>(keys + src * layout.row_bytes, out_keys + row * layout.row_bytes,
-                  layout.chunks, gc.lane, gc.lanes);
-      copy_row<G>(values + src * layout.row_bytes, out_values + row * layout.row_bytes,
-                  layout.chunks, gc.lane, gc.lanes);
-      if (gc.lane == 0) out_positions[row] = positions[src];
-    }
-  }
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+  if (d0 >= rows_out) return;  // uniform across the block
+  const int n = static_cast<int>(rows_out - d0 < rows_per_block ? rows_out - d0 : rows_per_block);
+  compact_block<G>(keys, values, positions, rows_in, removed, removed_count, d0, n, 0, layout,
+                   out_keys, out_values, out_positions);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -148,6 +207,7 @@ __global__ __launch_bounds__(kThreads) void head_append_kernel(
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
     int32_t* __restrict__ out_lengths) {
+  constexpr bool kTwo = kWithPositions;  // the legacy single-tensor form has no values
   const GroupCoord gc = group_coord(layout.lanes_log2);
   const int64_t head = blockIdx.y;
   const int64_t old_start = starts[head];
@@ -164,31 +224,47 @@ __global__ __launch_bounds__(kThreads) void head_append_kernel(
   if (total > covered_rows) total = covered_rows;
   const int64_t rows_out = rows_in + heads * added;
   const int64_t R = layout.rows_per_group;
+  const int64_t rb = layout.row_bytes;
   for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
        first < total;
        first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
     const int64_t end = first + R < total ? first + R : total;
-    for (int64_t p = first; p < end; ++p) {
-      const int64_t dst = new_start + p;
-      if (dst < 0 || dst >= rows_out) break;
-      if (p < old_length) {
-        const int64_t src = old_start + p;
-        if (src < 0 || src >= rows_in) break;
-        copy_row<G>(cache_keys + src * layout.row_bytes, out_keys + dst * layout.row_bytes,
-                    layout.chunks, gc.lane, gc.lanes);
-        if (cache_values != nullptr)
-          copy_row<G>(cache_values + src * layout.row_bytes, out_values + dst * layout.row_bytes,
-                      layout.chunks, gc.lane, gc.lanes);
-        if (kWithPositions && gc.lane == 0) out_positions[dst] = positions[src];
-      } else {
-        const int64_t src = head * added + (p - old_length);
-        copy_row<G>(new_keys + src * layout.row_bytes, out_keys + dst * layout.row_bytes,
-                    layout.chunks, gc.lane, gc.lanes);
-        if (new_values != nullptr)
-          copy_row<G>(new_values + src * layout.row_bytes, out_values + dst * layout.row_bytes,
-                      layout.chunks, gc.lane, gc.lanes);
-        if (kWithPositions && gc.lane == 0)
-          out_positions[dst] = static_cast<float>(logical_start + (p - old_length));
+    // skipped copies read the first new row, or with no new rows the first cache row (the
+    // host returns early when there are neither)
+    const uint8_t* fallback = added > 0 ? new_keys : cache_keys;
+    const uint8_t* fallback2 = added > 0 ? new_values : cache_values;
+    for (int64_t p0 = first; p0 < end; p0 += kBatch) {
+      RowBatch<kTwo> b;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t p = p0 + u, dst = new_start + p;
+        const bool old = p < old_length;
+        const int64_t src = old ? old_start + p : head * added + (p - old_length);
+        const bool ok = p < end && dst >= 0 && dst < rows_out && (!old || (src >= 0 && src < rows_in));
+        b.ok[u] = ok;
+        b.src[u] = !ok ? fallback : old ? cache_keys + src * rb : new_keys + src * rb;
+        b.dst[u] = out_keys + dst * rb;
+        if constexpr (kTwo) {
+          b.src2[u] = !ok ? fallback2 : old ? cache_values + src * rb : new_values + src * rb;
+          b.dst2[u] = out_values + dst * rb;
+        }
+      }
+      float position[kBatch];
+      if constexpr (kWithPositions) {
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int64_t p = p0 + u;
+          const bool old = b.ok[u] && p < old_length;
+          // rows without an old position read the first one (only when the cache has rows)
+          const float loaded = rows_in > 0 ? positions[old ? old_start + p : 0] : 0.0f;
+          position[u] = old ? loaded : static_cast<float>(logical_start + (p - old_length));
+        }
+      }
+      copy_batch<G, kTwo>(b, layout.chunks, gc.lane, gc.lanes);
+      if (kWithPositions && gc.lane == 0) {
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          if (b.ok[u]) out_positions[new_start + p0 + u] = position[u];
       }
     }
   }
@@ -213,37 +289,67 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
   const GroupCoord gc = group_coord(layout.lanes_log2);
   const int64_t R = layout.rows_per_group;
   const int64_t rb = layout.row_bytes;
+  // a readable row for copies that are skipped; with none, no index can be valid
+  const uint8_t* fallback = rows_in > 0 ? keys : recalled_rows > 0 ? recalled : nullptr;
+  if (fallback == nullptr) return;
+  const float* fallback_position = rows_in > 0 ? positions : recalled_positions;
   for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
        first < rows_out;
        first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
     const int64_t end = first + R < rows_out ? first + R : rows_out;
-    for (int64_t r = first; r < end; ++r) {
-      const int64_t source = index[r];
-      if (kMode == kMerge && source < 0) {
-        const int64_t restored = -source - 1;
-        if (restored >= recalled_rows) continue;
-        copy_row<G>(recalled + (2 * restored) * rb, out_keys + r * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        copy_row<G>(recalled + (2 * restored + 1) * rb, out_values + r * rb, layout.chunks,
-                    gc.lane, gc.lanes);
-        if (gc.lane == 0) out_positions[r] = recalled_positions[restored];
-        continue;
-      }
-      if (source < 0 || source >= rows_in) continue;
-      if (kMode == kPack) {
-        copy_row<G>(keys + source * rb, out_keys + (2 * r) * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        copy_row<G>(values + source * rb, out_keys + (2 * r + 1) * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        if (gc.lane == 0) {
-          metadata[3 * r] = layer;
-          metadata[3 * r + 1] = heads[r];
-          metadata[3 * r + 2] = static_cast<int64_t>(positions[source]);
+    for (int64_t r0 = first; r0 < end; r0 += kBatch) {
+      // every load of the batch is unconditional (clamped indices, fallback rows), so none is
+      // waited for before the next is issued
+      int64_t source[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) source[u] = index[r0 + u < end ? r0 + u : end - 1];
+      RowBatch<true> b;
+      const float* from_position[kBatch];
+      int64_t head_of[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t r = r0 + u, src = source[u];
+        const bool from_recalled = kMode == kMerge && src < 0 && src != INT64_MIN;
+        const int64_t restored = from_recalled ? -src - 1 : 0;
+        bool ok;
+        if (from_recalled) {
+          ok = restored < recalled_rows;
+          b.src[u] = ok ? recalled + (2 * restored) * rb : fallback;
+          b.src2[u] = ok ? recalled + (2 * restored + 1) * rb : fallback;
+          from_position[u] = ok ? recalled_positions + restored : fallback_position;
+        } else {
+          ok = src >= 0 && src < rows_in;
+          b.src[u] = ok ? keys + src * rb : fallback;
+          b.src2[u] = ok ? values + src * rb : fallback;
+          from_position[u] = ok ? positions + src : fallback_position;
         }
-      } else {
-        copy_row<G>(keys + source * rb, out_keys + r * rb, layout.chunks, gc.lane, gc.lanes);
-        copy_row<G>(values + source * rb, out_values + r * rb, layout.chunks, gc.lane, gc.lanes);
-        if (kMode == kMerge && gc.lane == 0) out_positions[r] = positions[source];
+        b.ok[u] = ok && r < end;
+        if (kMode == kPack) {
+          b.dst[u] = out_keys + (2 * r) * rb;
+          b.dst2[u] = out_keys + (2 * r + 1) * rb;
+          head_of[u] = heads[r < end ? r : end - 1];
+        } else {
+          b.dst[u] = out_keys + r * rb;
+          b.dst2[u] = out_values + r * rb;
+        }
+      }
+      float position[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) position[u] = kMode == kKeep ? 0.0f : *from_position[u];
+      copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+      if (gc.lane == 0) {
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (!b.ok[u]) continue;
+          const int64_t r = r0 + u;
+          if (kMode == kPack) {
+            metadata[3 * r] = layer;
+            metadata[3 * r + 1] = head_of[u];
+            metadata[3 * r + 2] = static_cast<int64_t>(position[u]);
+          } else if (kMode == kMerge) {
+            out_positions[r] = position[u];
+          }
+        }
       }
     }
   }
@@ -274,20 +380,34 @@ __global__ __launch_bounds__(kThreads) void batch_append_kernel(
        first < total;
        first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
     const int64_t end = first + R < total ? first + R : total;
-    for (int64_t p = first; p < end; ++p) {
-      const int64_t dst = destination + p;
-      if (p < old_length) {
-        copy_row<G>(keys + (source + p) * rb, out_keys + dst * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        copy_row<G>(values + (source + p) * rb, out_values + dst * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        if (gc.lane == 0) out_positions[dst] = positions[source + p];
-      } else {
-        copy_row<G>(new_keys + segment * rb, out_keys + dst * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        copy_row<G>(new_values + segment * rb, out_values + dst * rb, layout.chunks, gc.lane,
-                    gc.lanes);
-        if (gc.lane == 0) out_positions[dst] = static_cast<float>(logical);
+    for (int64_t p0 = first; p0 < end; p0 += kBatch) {
+      RowBatch<true> b;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t p = p0 + u, dst = destination + p;
+        const bool ok = p < end;
+        const bool old = ok && p < old_length;
+        b.ok[u] = ok;
+        // rows past the end (and the new row) read the segment's new row
+        b.src[u] = old ? keys + (source + p) * rb : new_keys + segment * rb;
+        b.src2[u] = old ? values + (source + p) * rb : new_values + segment * rb;
+        b.dst[u] = out_keys + dst * rb;
+        b.dst2[u] = out_values + dst * rb;
+      }
+      float position[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t p = p0 + u;
+        const bool old = p < end && p < old_length;
+        // rows without an old position read the first one (only when the segment has old rows)
+        const float loaded = old_length > 0 ? positions[source + (old ? p : 0)] : 0.0f;
+        position[u] = old ? loaded : static_cast<float>(logical);
+      }
+      copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+      if (gc.lane == 0) {
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          if (b.ok[u]) out_positions[destination + p0 + u] = position[u];
       }
     }
   }
@@ -297,26 +417,15 @@ __global__ __launch_bounds__(kThreads) void batch_append_kernel(
 // Audit-step compaction of every (layer, KV head) in one launch (the per-layer loop of
 // cache.py:113-178). blockIdx.y = head slot; each head keeps its rows minus the sorted
 // head-relative removal list of its score segment, and lands in one packed output at
-// sum over earlier head slots of (length - quota), derived here from the quotas.
-// Block x covers output rows [x * kCompactRows, ...) of its head. It first maps each of them to
-// its source row (gather rule of csrc/scoring.cu:164-188: output d takes input d + j,
-// j = #{i : removed[i] - i <= d}, by binary search over the removal list, staged in LDS when it
-// fits), copying the positions on the way; then every lane group copies rows with the loads of
-// several rows in flight before their stores. No per-row index work remains in the copy.
-constexpr int kCompactRows = 256;    // output rows per block
-constexpr int kCompactStaged = 4096;  // removal entries staged in LDS (larger lists: global)
-constexpr int kCompactUnroll = 4;     // rows per lane group with loads in flight together
-
+// sum over earlier head slots of (length - quota), derived here from the quotas. Block x
+// covers output rows [x * kCompactRows, ...) of its head.
 template <int G>
 __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
     const int64_t* __restrict__ head_table, const int64_t* __restrict__ quotas,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ removed_positions,
     RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
-  using V = typename RawGranule<G>::type;  // a plain vector type: stays in registers
   __shared__ int64_t partial[kThreads / 64];
-  __shared__ int32_t staged[kCompactStaged];
-  __shared__ int64_t source[kCompactRows];
   const int64_t head = blockIdx.y;
   const int64_t* row = head_table + head * LR_HEAD_WORDS;
   const int64_t length = row[3], segment = row[4];
@@ -333,62 +442,14 @@ __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o, 64);
   if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = before;
-  const int64_t* removed = segment >= 0 ? removed_positions + offsets[segment] : nullptr;
-  const bool in_lds = removed_count <= kCompactStaged;
-  if (in_lds)
-    for (int64_t i = threadIdx.x; i < removed_count; i += kThreads)
-      staged[i] = static_cast<int32_t>(removed[i]);
   __syncthreads();
   int64_t out_start = 0;
   for (int w = 0; w < kThreads / 64; ++w) out_start += partial[w];
-  const uint8_t* keys = reinterpret_cast<const uint8_t*>(row[0]);
-  const uint8_t* values = reinterpret_cast<const uint8_t*>(row[1]);
-  const float* positions = reinterpret_cast<const float*>(row[2]);
   const int n = static_cast<int>(rows_out - d0 < kCompactRows ? rows_out - d0 : kCompactRows);
-  if (static_cast<int>(threadIdx.x) < n) {
-    const int64_t d = d0 + threadIdx.x;
-    int64_t lo = 0, hi = removed_count;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      const int64_t r = in_lds ? staged[mid] : removed[mid];
-      if (r - mid <= d) lo = mid + 1;
-      else hi = mid;
-    }
-    const int64_t src = d + lo;
-    const bool valid = src < length;  // a malformed removal list can point past the head
-    source[threadIdx.x] = valid ? src : -1;
-    if (valid) out_positions[out_start + d] = positions[src];
-  }
-  __syncthreads();
-  const GroupCoord gc = group_coord(layout.lanes_log2);
-  const int64_t rb = layout.row_bytes, chunks = layout.chunks;
-  for (int r0 = gc.group; r0 < n; r0 += gc.groups_per_block * kCompactUnroll) {
-    int64_t src[kCompactUnroll], dst[kCompactUnroll];
-#pragma unroll
-    for (int u = 0; u < kCompactUnroll; ++u) {
-      const int r = r0 + u * gc.groups_per_block;
-      src[u] = r < n ? source[r] : -1;
-      dst[u] = out_start + d0 + r;
-    }
-    // Loads are unconditional (rows without a source re-read row 0 of the head, which exists
-    // since n > 0): a load under a branch would be waited for before the next one is issued.
-    for (int64_t c = gc.lane; c < chunks; c += gc.lanes) {
-      V k[kCompactUnroll], v[kCompactUnroll];
-#pragma unroll
-      for (int u = 0; u < kCompactUnroll; ++u) {
-        const int64_t from = src[u] >= 0 ? src[u] : 0;
-        k[u] = global_ptr(reinterpret_cast<const V*>(keys + from * rb))[c];
-        v[u] = global_ptr(reinterpret_cast<const V*>(values + from * rb))[c];
-      }
-#pragma unroll
-      for (int u = 0; u < kCompactUnroll; ++u) {
-        if (src[u] >= 0) {
-          global_ptr(reinterpret_cast<V*>(out_keys + dst[u] * rb))[c] = k[u];
-          global_ptr(reinterpret_cast<V*>(out_values + dst[u] * rb))[c] = v[u];
-        }
-      }
-    }
-  }
+  compact_block<G>(reinterpret_cast<const uint8_t*>(row[0]), reinterpret_cast<const uint8_t*>(row[1]),
+                   reinterpret_cast<const float*>(row[2]), length,
+                   segment >= 0 ? removed_positions + offsets[segment] : nullptr, removed_count,
+                   d0, n, out_start, layout, out_keys, out_values, out_positions);
 }
 
 inline const uint8_t* bytes(const void* p) { return static_cast<const uint8_t*>(p); }
@@ -414,11 +475,17 @@ extern "C" int lr_compact(const void* keys, const void* values, const float* pos
   LR_REQUIRE(removed_count == 0 || removed != nullptr, "Invalid removals");
   const int64_t row_bytes = dim * elem_bytes;
   const int g = granule_for(row_bytes, {keys, values, out_keys, out_values});
+  LR_REQUIRE(rows < (int64_t{1} << 31), "Invalid KV layout");
   const RowLayout layout = make_layout(row_bytes, g, rows_out, 8);
-  const int64_t blocks = blocks_for(layout, rows_out);
+  // enough blocks to spread one layer over the CUs: 32..kCompactRows rows per block
+  int64_t per_block = ceil_div(ceil_div(rows_out, 1024), 32) * 32;
+  if (per_block > kCompactRows) per_block = kCompactRows;
+  const int64_t blocks = ceil_div(rows_out, per_block);
+  LR_REQUIRE(blocks < kMaxGridX, "Invalid KV layout");
   return dispatch_granule(g, [&]<int G>() {
     compact_kernel<G><<<blocks, kThreads, 0, as_stream(stream)>>>(
-        bytes(keys), bytes(values), positions, removed, removed_count, rows, rows_out, layout,
+        bytes(keys), bytes(values), positions, removed, removed_count, rows, rows_out,
+        static_cast<int>(per_block), layout,
         bytes(out_keys), bytes(out_values), out_positions);
     return check_launch("compact");
   });
