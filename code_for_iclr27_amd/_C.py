@@ -217,51 +217,6 @@ def pack(keys, values, positions, indices, heads, layer, payload, metadata):
     return None
 
 
-def batch_descriptors(keys: Sequence[torch.Tensor], values: Sequence[torch.Tensor],
-                      positions: Sequence[torch.Tensor], heads: int, dimension: int,
-                      dtype: torch.dtype, device: torch.device,
-                      lengths: Sequence[Sequence[int]], logical_positions: Sequence[int]):
-    """Validate a batch and build the reference's 7-word segment descriptors on the host
-    (csrc/batch_append.cu:49-80). Returns (int64 numpy [R*H, 7], total rows, max rows)."""
-    requests = len(keys)
-    descriptors = np.empty((requests * heads, 7), dtype=np.int64)
-    destination, maximum = 0, 0
-    row_bytes = dimension * torch.empty((), dtype=dtype).element_size()
-    granule = 16
-    while granule > 1 and row_bytes % granule:
-        granule //= 2
-    for request in range(requests):
-        k, v, p = keys[request], values[request], positions[request]
-        _check(k.is_cuda and k.is_contiguous() and v.is_contiguous() and p.is_contiguous(),
-               "Contiguous CUDA cache required")
-        _check(k.device == device and v.device == device and p.device == device,
-               "Cache devices differ")
-        _check(k.dim() == 2 and k.size(1) == dimension and k.shape == v.shape and k.dtype == dtype
-               and v.dtype == dtype, "Cache K/V mismatch")
-        logical = int(logical_positions[request])
-        _check(p.dtype == torch.float32 and p.numel() == k.size(0)
-               and len(lengths[request]) == heads and 0 <= logical < (1 << 24),
-               "Invalid positions or head metadata")
-        _check(k.data_ptr() % granule == 0 and v.data_ptr() % granule == 0,
-               "Cache rows must be aligned to the row granule")
-        head_lengths = np.asarray(lengths[request], dtype=np.int64)
-        _check(bool((head_lengths >= 0).all()), "Invalid head length")
-        sources = np.concatenate(([0], np.cumsum(head_lengths)[:-1]))
-        _check(bool((sources + head_lengths <= k.size(0)).all()), "Invalid head length")
-        _check(int(head_lengths.sum()) == k.size(0), "Head lengths do not cover cache rows")
-        block = descriptors[request * heads:(request + 1) * heads]
-        block[:, 0] = k.data_ptr()
-        block[:, 1] = v.data_ptr()
-        block[:, 2] = p.data_ptr()
-        block[:, 3] = sources
-        block[:, 4] = head_lengths
-        block[:, 5] = destination + np.concatenate(([0], np.cumsum(head_lengths + 1)[:-1]))
-        block[:, 6] = logical
-        destination += int((head_lengths + 1).sum())
-        maximum = max(maximum, int(head_lengths.max()) + 1)
-    return descriptors, destination, maximum
-
-
 def upload_int64(host: np.ndarray, device: torch.device) -> torch.Tensor:
     """Stage an int64 table in pinned memory and copy it to the device without blocking the
     host (the reference's descriptor copy, csrc/batch_append.cu:81, is synchronous)."""
@@ -285,11 +240,14 @@ def batch_append(keys: List[torch.Tensor], values: List[torch.Tensor],
            and len(positions) == requests and len(lengths) == requests
            and len(logical_positions) == requests, "Request metadata mismatch")
     elem = _elem_bytes(new_keys, "batch_append")
-    descriptors, rows, maximum = batch_descriptors(keys, values, positions, heads, dimension,
-                                                   new_keys.dtype, new_keys.device, lengths,
-                                                   logical_positions)
+    from .scoring import _planner
     with torch.cuda.device(new_keys.device):
-        device_descriptors = upload_int64(descriptors, new_keys.device)
+        # csrc/host_plan.cpp: the reference's descriptor loop (csrc/batch_append.cu:49-80) and
+        # its checks, then a non-blocking upload from pinned memory (the reference's copy,
+        # csrc/batch_append.cu:81, blocks the host)
+        device_descriptors, rows, maximum = _planner().plan_batch_append(
+            keys, values, positions, heads, dimension, new_keys.dtype, new_keys.device,
+            lengths, logical_positions)
         output_keys = torch.empty((rows, dimension), dtype=new_keys.dtype, device=new_keys.device)
         output_values = torch.empty_like(output_keys)
         output_positions = torch.empty((rows, 1), dtype=torch.float32, device=new_keys.device)

@@ -177,10 +177,70 @@ py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<t
   return py::make_tuple(block, meta, segment_info, head_info);
 }
 
+// The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,
+// head): [keys ptr, values ptr, positions ptr, first source row, old length, destination row,
+// logical position]; same checks, order and messages as the reference's host loop. Returns
+// (descriptors int64 [R*H, 7] already copied to `device` on the current stream (from pinned
+// memory, without blocking the host), total output rows, rows of the longest head + 1).
+py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
+                            const std::vector<torch::Tensor>& values,
+                            const std::vector<torch::Tensor>& positions, int64_t heads,
+                            int64_t dim, torch::ScalarType dtype, const torch::Device& device,
+                            const std::vector<std::vector<int64_t>>& lengths,
+                            const std::vector<int64_t>& logical_positions) {
+  const size_t requests = keys.size();
+  const int64_t row_bytes = dim * c10::elementSize(dtype);
+  int64_t granule = 16;
+  while (granule > 1 && row_bytes % granule) granule /= 2;
+  torch::Tensor host = torch::empty({static_cast<int64_t>(requests) * heads, 7},
+                                    torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
+  int64_t* out = host.data_ptr<int64_t>();
+  int64_t destination = 0, maximum = 0;
+  for (size_t r = 0; r < requests; ++r) {
+    const torch::Tensor &k = keys[r], &v = values[r], &p = positions[r];
+    require(k.is_cuda() && k.is_contiguous() && v.is_contiguous() && p.is_contiguous(),
+            "Contiguous CUDA cache required");
+    require(k.device() == device && v.device() == device && p.device() == device,
+            "Cache devices differ");
+    require(k.dim() == 2 && k.size(1) == dim && k.sizes() == v.sizes() && k.scalar_type() == dtype &&
+                v.scalar_type() == dtype,
+            "Cache K/V mismatch");
+    const int64_t logical = logical_positions[r];
+    require(p.scalar_type() == torch::kFloat32 && p.numel() == k.size(0) &&
+                static_cast<int64_t>(lengths[r].size()) == heads && logical >= 0 &&
+                logical < (int64_t{1} << 24),
+            "Invalid positions or head metadata");
+    require(reinterpret_cast<uintptr_t>(k.data_ptr()) % granule == 0 &&
+                reinterpret_cast<uintptr_t>(v.data_ptr()) % granule == 0,
+            "Cache rows must be aligned to the row granule");
+    int64_t source = 0;
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t n = lengths[r][h];
+      require(n >= 0, "Invalid head length");
+      require(source + n <= k.size(0), "Invalid head length");
+      int64_t* row = out + (static_cast<int64_t>(r) * heads + h) * 7;
+      row[0] = ptr(k);
+      row[1] = ptr(v);
+      row[2] = ptr(p);
+      row[3] = source;
+      row[4] = n;
+      row[5] = destination;
+      row[6] = logical;
+      source += n;
+      destination += n + 1;
+      maximum = std::max(maximum, n + 1);
+    }
+    require(source == k.size(0), "Head lengths do not cover cache rows");
+  }
+  return py::make_tuple(host.to(device, /*non_blocking=*/true), destination, maximum);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_plan, module) {
   module.def("plan_audit", &plan_audit, "Validate layers and build the audit metadata block");
+  module.def("plan_batch_append", &plan_batch_append,
+             "Validate a batch and upload its batch_append descriptors");
   module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;
   module.attr("LR_HEAD_WORDS") = LR_HEAD_WORDS;
 }

@@ -198,6 +198,44 @@ def test_pack_into_staging_view(device, dtype):
     assert int((archive_meta[0] != -1).sum()) == 0 and int((archive_meta[1, :10] != -1).sum()) == 0
 
 
+@pytest.mark.parametrize("case,message", [
+    ("short", "Head lengths do not cover cache rows"),
+    ("negative", "Invalid head length"),
+    ("overrun", "Invalid head length"),
+    ("logical", "Invalid positions or head metadata"),
+    ("heads", "Invalid positions or head metadata"),
+    ("dtype", "Cache K/V mismatch"),
+    ("cpu", "Contiguous CUDA cache required"),
+])
+def test_batch_append_rejects_bad_metadata(device, case, message):
+    """The descriptor checks of csrc/batch_append.cu:49-80 (the host planner raises them
+    before anything is launched)."""
+    heads, dim = 2, 64
+    lengths = [[3, 4], [5, 0]]
+    keys = [rand((sum(l), dim), torch.bfloat16, device, 60 + r) for r, l in enumerate(lengths)]
+    values = [rand((sum(l), dim), torch.bfloat16, device, 70 + r) for r, l in enumerate(lengths)]
+    positions = [torch.zeros((sum(l), 1), device=device) for l in lengths]
+    logical = [10, 11]
+    if case == "short":
+        lengths = [[3, 3], [5, 0]]
+    elif case == "negative":
+        lengths = [[3, 4], [6, -1]]
+    elif case == "overrun":
+        lengths = [[3, 5], [5, 0]]
+    elif case == "logical":
+        logical = [10, 1 << 24]
+    elif case == "heads":
+        lengths = [[3, 4], [5]]
+    elif case == "dtype":
+        values[1] = values[1].float()
+    elif case == "cpu":
+        keys[0] = keys[0].cpu()
+    nk = rand((2, heads, 1, dim), torch.bfloat16, device, 80)
+    nv = rand((2, heads, 1, dim), torch.bfloat16, device, 81)
+    with pytest.raises(RuntimeError, match=message):
+        _C.batch_append(keys, values, positions, nk, nv, lengths, logical)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_batch_append_over_packed_views(device, dtype):
     """Requests' caches are views into the previous packed output, as append_packed leaves
