@@ -46,7 +46,7 @@ __device__ __forceinline__ T gload(const void* p) {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxGroups = 16;
 constexpr int kMaxQueryTiles = 256;  // window <= 8192
-constexpr int kTileKeys = 128;       // candidate keys per column-pass workgroup
+constexpr int kTileKeys = 128;       // fewest candidate keys per column-pass workgroup
 constexpr int kProjectedRowsPerLane = 8;  // V rows each projected-values lane loads at once
 
 struct Segment {
@@ -501,27 +501,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 }
 
 // ---------------------------------------------------------------------------------------
-// 3. Column scores. Workgroup = 128 candidate keys (4 waves x 32, K operand resident in
-// registers). It streams the G * ceil(W/32) (query tile, group) units in query-tile-major order
-// through LDS, one unit per double-buffered stage: the 32 query rows by direct copy into
-// swizzled rows, with each row's statistics and query position. After a query tile's last
-// group every lane holds 16 drops (its query x 16 keys); a transpose through LDS reduces them
-// over the tile's queries, so a lane keeps one running (min, max) pair and the kernel fits
-// three waves per SIMD.
+// 3. Column scores. Workgroup = 4 waves x KT tiles of 32 candidate keys; each wave keeps the
+// K operand of its KT tiles in registers. It streams the G * ceil(W/32) (query tile, group)
+// units in query-tile-major order through LDS, one unit per double-buffered stage: the 32
+// query rows by direct copy into swizzled rows, with each row's statistics and query
+// position. A unit's B operand (its 32 query rows) is read from LDS once and multiplied into
+// all KT key tiles. After a query tile's last group every lane holds 16 drops per key tile
+// (its query x 16 keys); a transpose through LDS reduces them over the tile's queries, so a
+// lane keeps one running (min, max) pair per key tile.
+// On gfx950 MFMA and VALU work of a SIMD's waves do not overlap; the kernel is bound by their
+// sum; KT = 2 halves the per-unit overhead (copies, statistics, branches, barrier, B reads)
+// per key, at two waves per SIMD.
+// Key tiles per wave: two for d = 128 (measured faster there), one for d = 64 (three waves per
+// SIMD fit) and d = 256 (the K operand alone takes 64 registers per tile).
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 3 : 1))) void column_scores_kernel(
+constexpr int column_key_tiles() { return D == 128 ? 2 : 1; }
+
+template <int D>
+constexpr int column_waves_per_simd() { return column_key_tiles<D>() == 2 ? 2 : D <= 128 ? 3 : 1; }
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_waves_per_simd<D>()))) void column_scores_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, const float* __restrict__ margin, float scale,
     int64_t tiles_per_segment, const float* __restrict__ pv, const float4* __restrict__ stats,
     float* __restrict__ scores, int* __restrict__ nonfinite) {
   constexpr int KS = D / 16;
-  __shared__ __bf16 q_lds[3][32 * D];  // swizzled rows, triple buffered
-  __shared__ float4 st_lds[3][32];
-  __shared__ float qp_lds[3][32];
-  __shared__ float pv_lds[kMaxGroups * kTileKeys];
-  __shared__ float kpos_lds[kTileKeys];
-  __shared__ int keybad_lds[kTileKeys];
-  __shared__ float red_lds[4][64 * 16];  // per-wave transpose scratch
+  constexpr int KT = column_key_tiles<D>();
+  constexpr int kKeys = 4 * 32 * KT;  // candidate keys per workgroup
+  __shared__ __bf16 q_lds[2][32 * D];  // swizzled rows, double buffered
+  __shared__ float4 st_lds[2][32];
+  __shared__ float qp_lds[2][32];
+  __shared__ float pv_lds[kMaxGroups * kKeys];
+  __shared__ float kpos_lds[kKeys];
+  __shared__ int keybad_lds[kKeys];
+  __shared__ float red_lds[4][64 * 16];  // per-wave transpose scratch (one key tile at a time)
   __shared__ int rowbad_lds;
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
@@ -531,21 +545,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   const int tile = block - s * per;
   const Segment seg = load_segment(table, s);
   const int count = static_cast<int>(seg.last - seg.first);
-  if (tile * kTileKeys >= count) return;  // uniform across the workgroup, before any barrier
+  if (tile * kKeys >= count) return;  // uniform across the workgroup, before any barrier
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int half = lane >> 5, col = lane & 31;
   const int length = static_cast<int>(seg.length);
-  const int key0 = static_cast<int>(seg.first) + tile * kTileKeys;
-  const int wave_key0 = key0 + wave * 32;
+  const int key0 = static_cast<int>(seg.first) + tile * kKeys;
+  const int wave_key0 = key0 + wave * 32 * KT;  // key tile t: wave_key0 + 32 t + [0, 32)
   const int qtiles = (window + 31) / 32;
   const int units = qtiles * groups;
   const float* pv_seg = pv + seg.pv_offset;
   const float4* stats_seg = stats + seg.stats_offset;
 
-  // K operand of this wave's 32 keys.
-  bf16x8 kop[KS];
-  {
-    const int key = wave_key0 + col;
+  // K operand of this wave's KT x 32 keys.
+  bf16x8 kop[KT][KS];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const int key = wave_key0 + 32 * t + col;
     const __bf16* krow = seg.keys + static_cast<int64_t>(key) * D + half * (D / 2);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -553,32 +568,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = static_cast<__bf16>(0.0f);
       if (key < length) v = gload<bf16x8>(krow + 8 * ks);
-      kop[ks] = v;
+      kop[t][ks] = v;
     }
   }
-  for (int i = threadIdx.x; i < groups * kTileKeys; i += 256) {
-    const int gg = i / kTileKeys, key = key0 + (i - gg * kTileKeys);
+  for (int i = threadIdx.x; i < groups * kKeys; i += 256) {
+    const int gg = i / kKeys, key = key0 + (i - gg * kKeys);
     pv_lds[i] = key < length ? gload<float>(pv_seg + static_cast<int64_t>(gg) * length + key) : 0.0f;
   }
-  if (threadIdx.x < kTileKeys) {
-    const int key = key0 + threadIdx.x;
-    kpos_lds[threadIdx.x] = key < length ? gload<float>(seg.key_positions + key) : INFINITY;
+  for (int i = threadIdx.x; i < kKeys; i += 256) {
+    const int key = key0 + i;
+    kpos_lds[i] = key < length ? gload<float>(seg.key_positions + key) : INFINITY;
   }
   if (threadIdx.x == 0) rowbad_lds = 0;
 
   // Stage loader for unit u into buffer buf: the query rows by direct copy (rows past the
   // window re-read the last query; their results are never used), and on lanes 0..31 of wave 0
   // the rows' statistics and query positions (padded rows: harmless values that take the fast
-  // epilogue).
-  // The loads are only issued here; their values are first used in commit(), after the wait
-  // that also covers the row copies, so no wave stalls on them mid-stage.
+  // epilogue). The statistics loads go first: a wait the compiler adds before them (they reuse
+  // the registers of the previous unit's loads) then falls before the copies are issued. Their
+  // values are first used in commit(), after the wait that also covers the row copies.
   float4 st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);
   int64_t qp_raw = 0;
   bool row_loaded = false;
   int bad_reg = 0;
   int fetch_qt = 0, fetch_g = 0;  // unit of the next fetch, (query tile, group)
-  // The statistics loads go first: a wait the compiler adds before them (they reuse the
-  // registers of the previous unit's loads) then falls before the copies are issued.
   auto fetch = [&](int buf) {
     if (threadIdx.x < 32) {
       const int query = fetch_qt * 32 + threadIdx.x;
@@ -608,171 +621,175 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       qp_lds[buf][threadIdx.x] = qp;
     }
   };
-  // Unit u lives in buffer u % 3: while unit u's epilogue runs, unit u + 1's MFMAs are in
-  // flight (issued from its buffer) and unit u + 2 is being copied in.
   fetch(0);
   __syncthreads();  // rowbad_lds cleared before any loader may set it
   dma_wait();
   commit(0);
-  if (units > 1) {
-    fetch(1);
-    dma_wait();
-    commit(1);
-  }
   __syncthreads();
-  if (threadIdx.x < kTileKeys) {
+  for (int i = threadIdx.x; i < kKeys; i += 256) {
     int bad = 0;
-    for (int gg = 0; gg < groups; ++gg) bad |= !isfinite(pv_lds[gg * kTileKeys + threadIdx.x]);
-    keybad_lds[threadIdx.x] = bad;
+    for (int gg = 0; gg < groups; ++gg) bad |= !isfinite(pv_lds[gg * kKeys + i]);
+    keybad_lds[i] = bad;
   }
   // Largest candidate key position of this wave (keys at or past `last` never matter).
-  float kmax = (wave_key0 + col < seg.last) ? kpos_lds[wave * 32 + col] : -INFINITY;
+  float kmax = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
+    if (wave_key0 + 32 * t + col < seg.last) kmax = fmaxf(kmax, kpos_lds[wave * 32 * KT + 32 * t + col]);
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
 
-  float drop[16];
+  float drop[KT][16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) drop[r] = 0.0f;
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) drop[t][r] = 0.0f;
   // Reducer role in the tile transpose: lane = (half, r, part); it owns key acc_key(r, half)
-  // and queries part*16 .. part*16+15 of each tile; lane ^ 1 owns the other 16.
+  // of each key tile and queries part*16 .. part*16+15 of each query tile; lane ^ 1 owns the
+  // other 16.
   const int part = lane & 1, r_red = (lane >> 1) & 15, half_red = lane >> 5;
-  float lo = INFINITY, hi = -INFINITY;
+  float lo[KT], hi[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) lo[t] = INFINITY, hi[t] = -INFINITY;
   float* red = red_lds[wave];
-  const float* kpos_wave = kpos_lds + wave * 32;
+  const float* kpos_wave = kpos_lds + wave * 32 * KT;
 
-  auto logits = [&](int buf) {
-    bf16x8 b[KS];
-    const __bf16* brow = q_lds[buf] + col * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      b[ks] = *reinterpret_cast<const bf16x8*>(brow + 8 * swizzled_chunk(col, half * KS + ks));
-    f32x16 acc = mfma_tile_zero();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[ks], b[ks], acc, 0, 0, 0);
-    return acc;
-  };
   int qt = 0, g = 0;  // unit u = (query tile, group)
-  // One unit: copy unit u + 2 in, start unit u + 1's MFMAs (into acc_out), run unit u's
-  // epilogue on acc. The loop below alternates two accumulators, so none is copied.
-  auto step = [&](int u, int buf, const f32x16& acc, f32x16& acc_out) {
-    const int buf1 = buf == 2 ? 0 : buf + 1, buf2 = buf1 == 2 ? 0 : buf1 + 1;
-    // unit u + 2 goes to the buffer unit u - 1 used; its last readers passed the previous barrier
-    if (u + 2 < units) fetch(buf2);
-    if (u + 1 < units) acc_out = logits(buf1);
+  for (int u = 0; u < units; ++u) {
+    const int buf = u & 1;
+    // unit u + 1 goes to the other buffer; its last readers passed the previous barrier
+    if (u + 1 < units) fetch(buf ^ 1);
+    f32x16 acc[KT];
+    {
+      bf16x8 b[KS];
+      const __bf16* brow = q_lds[buf] + col * D;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        b[ks] = *reinterpret_cast<const bf16x8*>(brow + 8 * swizzled_chunk(col, half * KS + ks));
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        acc[t] = mfma_tile_zero();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[t][ks], b[ks], acc[t], 0, 0, 0);
+      }
+    }
     const float4 st = st_lds[buf][col];
     const float query_position = qp_lds[buf][col];
-    const float* pv_row = pv_lds + g * kTileKeys + wave * 32;
-    // ratio = p / max(1 - p, eps) = e / max(S - e, eps*S) for the lane's 16 (key, query) pairs.
+    // ratio = p / max(1 - p, eps) = e / max(S - e, eps*S) for the lane's (key, query) pairs.
     // The general form applies the causal mask and the clamp. The fast form drops both, which
     // is exact when no key of this wave lies after any query of the unit and every row has
     // S >= 2 and eps*S <= 1/2: then e <= 1 gives S - e >= 1 > eps*S. It also takes the ratio
     // as 1 / (S*u - 1) with u = 1/e = exp(m - z), one operation fewer than e / (S - e).
-    float ratio[16];
+    float ratio[KT][16];
     if (__any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f))) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f32x4 kp = *reinterpret_cast<const f32x4*>(kpos_wave + 8 * c + 4 * half);
+      for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * c + j;
-          float z = logit_fast(acc[r], scale);
-          z = kp[j] <= query_position ? z : -INFINITY;
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
-          ratio[r] = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 kp = *reinterpret_cast<const f32x4*>(kpos_wave + 32 * t + 8 * c + 4 * half);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * c + j;
+            float z = logit_fast(acc[t][r], scale);
+            z = kp[j] <= query_position ? z : -INFINITY;
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
+            ratio[t][r] = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
+          }
         }
-      }
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float u = __builtin_amdgcn_exp2f(__builtin_fmaf(logit_fast(acc[r], scale), -kLog2e, -st.x));
-        ratio[r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, u, -1.0f));
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(logit_fast(acc[t][r], scale), -kLog2e, -st.x));
+          ratio[t][r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
+        }
+    }
+    const float* pv_row = pv_lds + g * kKeys + wave * 32 * KT;
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 32 * t + 8 * c + 4 * half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          drop[t][4 * c + j] = __builtin_fmaf(ratio[t][4 * c + j], w[j] - st.w, drop[t][4 * c + j]);
       }
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) drop[4 * c + j] = __builtin_fmaf(ratio[4 * c + j], w[j] - st.w, drop[4 * c + j]);
-    }
-    if (u + 2 < units) {
+    if (u + 1 < units) {
       dma_wait();
-      commit(buf2);
+      commit(buf ^ 1);
     }
     if (g == groups - 1) {
-      // Min / max of the tile's drops over its queries, through this wave's LDS scratch. LDS
-      // accesses of one wave complete in order, so the reads see this wave's writes. It runs
-      // after the wait for the next units' direct copies into LDS: the compiler makes every LDS
-      // read wait for outstanding copies, which here have already landed.
+      // Min / max of each key tile's drops over the query tile's queries, through this wave's
+      // LDS scratch. LDS accesses of one wave complete in order, so the reads see this wave's
+      // writes (and the next tile's writes follow this tile's reads).
+      const int valid = min(max(window - qt * 32 - part * 16, 0), 16);  // padded queries skipped
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<f32x4*>(red + lane * 16 + 4 * c) =
-            f32x4{drop[4 * c], drop[4 * c + 1], drop[4 * c + 2], drop[4 * c + 3]};
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-      const float* column = red + (half_red * 32 + part * 16) * 16 + r_red;
-      float tile_lo = INFINITY, tile_hi = -INFINITY;
-      // NaN-propagating, as torch's amin / amax; padded queries of a partial last tile skipped
-      if (qt * 32 + 32 <= window) {
+      for (int t = 0; t < KT; ++t) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const float x = column[q * 16];
-          tile_lo = __builtin_elementwise_minimum(tile_lo, x);
-          tile_hi = __builtin_elementwise_maximum(tile_hi, x);
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<f32x4*>(red + lane * 16 + 4 * c) =
+              f32x4{drop[t][4 * c], drop[t][4 * c + 1], drop[t][4 * c + 2], drop[t][4 * c + 3]};
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        const float* column = red + (half_red * 32 + part * 16) * 16 + r_red;
+        float tile_lo = INFINITY, tile_hi = -INFINITY;
+        // NaN-propagating, as torch's amin / amax
+        if (valid == 16) {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const float x = column[q * 16];
+            tile_lo = __builtin_elementwise_minimum(tile_lo, x);
+            tile_hi = __builtin_elementwise_maximum(tile_hi, x);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            const float x = column[q * 16];
+            tile_lo = __builtin_elementwise_minimum(tile_lo, q < valid ? x : INFINITY);
+            tile_hi = __builtin_elementwise_maximum(tile_hi, q < valid ? x : -INFINITY);
+          }
         }
-      } else {
-        const int valid = min(max(window - qt * 32 - part * 16, 0), 16);
+        lo[t] = __builtin_elementwise_minimum(lo[t], tile_lo);
+        hi[t] = __builtin_elementwise_maximum(hi[t], tile_hi);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const float x = column[q * 16];
-          tile_lo = __builtin_elementwise_minimum(tile_lo, q < valid ? x : INFINITY);
-          tile_hi = __builtin_elementwise_maximum(tile_hi, q < valid ? x : -INFINITY);
-        }
+        for (int r = 0; r < 16; ++r) drop[t][r] = 0.0f;
       }
-      lo = __builtin_elementwise_minimum(lo, tile_lo);
-      hi = __builtin_elementwise_maximum(hi, tile_hi);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-#pragma unroll
-      for (int r = 0; r < 16; ++r) drop[r] = 0.0f;
     }
     __syncthreads();
     if (++g == groups) {
       g = 0;
       ++qt;
     }
-  };
-  f32x16 acc_a = logits(0), acc_b = mfma_tile_zero();
-  for (int u = 0, buf = 0; u < units; u += 2) {
-    step(u, buf, acc_a, acc_b);
-    buf = buf == 2 ? 0 : buf + 1;
-    if (u + 1 < units) step(u + 1, buf, acc_b, acc_a);
-    buf = buf == 2 ? 0 : buf + 1;
   }
   if (bad_reg) rowbad_lds = 1;
   __syncthreads();
   const bool any_row_bad = rowbad_lds != 0;
-  // Combine the two reducer lanes of each key, then part 0 takes the risk of the minimum and
-  // part 1 of the maximum (f64, every lane busy).
-  const float mn = __builtin_elementwise_minimum(lo, __shfl_xor(lo, 1, 64));
-  const float mx = __builtin_elementwise_maximum(hi, __shfl_xor(hi, 1, 64));
-  const int key_local = wave * 32 + acc_key(r_red, half_red);
-  const int key = key0 + key_local;
-  const bool bad = any_row_bad || keybad_lds[key_local] || !isfinite(mn) || !isfinite(mx);
-  double risk = 0.0;
-  if (!bad) {
-    const double m = static_cast<double>(margin[0]);
-    const double p = 1.0 / (1.0 + exp(-m));
-    const double base = softplus64(m);
-    risk = risk64(m, p, base, part ? mx : mn);
+  const double m = static_cast<double>(margin[0]);
+  const double p = 1.0 / (1.0 + exp(-m));
+  const double base = softplus64(m);
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    // Combine the two reducer lanes of each key, then part 0 takes the risk of the minimum and
+    // part 1 of the maximum (f64, every lane busy).
+    const float mn = __builtin_elementwise_minimum(lo[t], __shfl_xor(lo[t], 1, 64));
+    const float mx = __builtin_elementwise_maximum(hi[t], __shfl_xor(hi[t], 1, 64));
+    const int key_local = wave * 32 * KT + 32 * t + acc_key(r_red, half_red);
+    const int key = key0 + key_local;
+    const bool bad = any_row_bad || keybad_lds[key_local] || !isfinite(mn) || !isfinite(mx);
+    const double risk = bad ? 0.0 : risk64(m, p, base, part ? mx : mn);
+    const double other_risk = __shfl_xor(risk, 1, 64);
+    if (part == 0 && key < seg.last) {
+      const float score = bad ? NAN : static_cast<float>(fmax(risk, other_risk));
+      scores[seg.out_offset + (key - seg.first)] = score;
+      if (nonfinite != nullptr && !isfinite(score)) atomicAdd(nonfinite, 1);
+    }
   }
-  const double other_risk = __shfl_xor(risk, 1, 64);
-  if (part != 0 || key >= seg.last) return;
-  const float score = bad ? NAN : static_cast<float>(fmax(risk, other_risk));
-  scores[seg.out_offset + (key - seg.first)] = score;
-  if (nonfinite != nullptr && !isfinite(score)) atomicAdd(nonfinite, 1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -840,7 +857,7 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
     if (int rc = check_launch("row_stats")) return rc;
   }
   if (stages & 4) {
-    const int64_t tiles = ceil_div(max_candidates, kTileKeys);
+    const int64_t tiles = ceil_div(max_candidates, 4 * 32 * column_key_tiles<D>());
     column_scores_kernel<D><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
         table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
         scores, nonfinite);
