@@ -29,8 +29,27 @@ import numpy as np
 import torch
 
 from . import _C, _lib
-from .scoring import LayerState, ScoreSegment, ScoreTable, SegmentPlan, plan_segments
+from .scoring import LayerState, ScoreSegment, ScoreTable, SegmentPlan, _planner, plan_segments
 from .selection import DeviceSelection, SelectWorkspace, select_refine
+
+_bound = False
+
+
+def _native_planner():
+    """The C++ host module, with the library entry points it launches bound once."""
+    global _bound
+    planner = _planner()
+    if not _bound:
+        import ctypes
+
+        library = _lib.load()
+        address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
+        planner.bind_library(address("lr_score_workspace_bytes"), address("lr_score_segments"),
+                             address("lr_pool"), address("lr_select_workspace_bytes"),
+                             address("lr_select_refine_sets"), address("lr_compact_heads"),
+                             address("lr_last_error"))
+        _bound = True
+    return planner
 
 
 def pool_score_table(table: ScoreTable, kernel_size: int = 7) -> ScoreTable:
@@ -139,9 +158,12 @@ class AuditStep:
         ``queue_order=True``, on a side stream, overlapping the compaction.
         ``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
         stage, on the current stream, for per-stage event timing."""
-        mark = timer.mark if timer is not None else (lambda name: None)
         if pool_kernel <= 0 or pool_kernel % 2 == 0:
             raise ValueError("pool kernel must be a positive odd integer")
+        if not queue_order:
+            return self._run_native(layers, query_positions, margin, count, protect_recent,
+                                    pool_kernel, denominator_epsilon, check_finite, timer)
+        mark = timer.mark if timer is not None else (lambda name: None)
         plan = plan_segments(layers, protect_prompt=True, protect_recent=protect_recent,
                              pinned=True)
         device = layers[0].keys.device
@@ -215,6 +237,13 @@ class AuditStep:
         if selection is not None and selection.queue_ready is not None:
             selection.wait_queue()  # join the queue order back before the step ends
             mark("queue_join")
+        return self._finish(plan, info, raw, pooled, selection, count, out_keys, out_values,
+                            out_positions, layers, check_finite)
+
+    @staticmethod
+    def _finish(plan, info, raw, pooled, selection, count, out_keys, out_values, out_positions,
+                layers, check_finite):
+        segments = plan.segment_count
         host_info = info.cpu().numpy()  # the step's only synchronisation
         quotas = host_info[:segments]
         bad = int(host_info[segments:].view(np.int32)[0])
@@ -228,3 +257,31 @@ class AuditStep:
         new_lens = kept.tolist()
         new_layers = PackedLayers(out_keys, out_values, out_positions, kept, layers)
         return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, count)
+
+    def _run_native(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
+                    denominator_epsilon, check_finite, timer=None):
+        """The same step with planning and every launch done by the C++ host module
+        (csrc/host_plan.cpp audit_launch): no Python between the launches."""
+        if len(layers) == 0:
+            raise RuntimeError("No layers to score")
+        planner = _native_planner()
+        device = layers[0].keys.device
+        margin = margin.to(device=device, dtype=torch.float32).reshape(1)
+        (block, meta, segment_info, head_info, scores, info, quotas, offsets, removed, changed,
+         out_keys, out_values, out_positions) = planner.audit_launch(
+            [layer.keys for layer in layers], [layer.values for layer in layers],
+            [layer.positions for layer in layers], [layer.queries for layer in layers],
+            [layer.gradient for layer in layers], [list(layer.head_lens) for layer in layers],
+            [None if layer.prompt_lens is None else list(layer.prompt_lens) for layer in layers],
+            int(protect_recent), query_positions, margin, int(count), int(pool_kernel),
+            float(denominator_epsilon), torch.cuda.current_stream(device).cuda_stream,
+            None if timer is None else timer.mark)
+        plan = SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
+        total = plan.total
+        count = min(max(0, int(count)), total)
+        selection = None
+        if count:
+            selection = DeviceSelection(None, None, None, quotas, offsets, removed, changed,
+                                        plan.segment_info[:2].T)
+        return self._finish(plan, info, scores[:total], scores[total:], selection, count,
+                            out_keys, out_values, out_positions, layers, check_finite)

@@ -10,6 +10,8 @@
 // reads per layer at ~0.2 us each; here the whole 32-layer plan takes a few microseconds.
 #include <torch/extension.h>
 
+#include <algorithm>
+#include <cmath>
 #include <optional>
 #include <stdexcept>
 #include <vector>
@@ -50,13 +52,27 @@ inline int64_t ptr(const torch::Tensor& t) { return reinterpret_cast<int64_t>(t.
 //          per-head [segment index or -1, length] int64 [2, L*H]).
 // meta = (segments, groups, window, dim, max segment length, max candidates, total candidates,
 //         projected floats, head slots, total rows, max head length).
-py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<torch::Tensor>& values,
-                     const std::vector<torch::Tensor>& positions,
-                     const std::vector<torch::Tensor>& queries,
-                     const std::vector<torch::Tensor>& gradients,
-                     const std::vector<std::vector<int64_t>>& head_lens,
-                     const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
-                     bool protect_prompt, int64_t protect_recent, bool pinned) {
+struct Plan {
+  torch::Tensor block, segment_info, head_info;
+  int64_t segments, groups, window, dim, max_seg_length, max_candidates, total, projected, slots,
+      rows_total, max_head_length;
+  // word offsets of the block's parts
+  int64_t bounds_at() const { return segments * LR_SEG_WORDS; }
+  int64_t ends_at() const { return bounds_at() + segments + 1; }
+  int64_t starts_at() const { return ends_at() + segments; }
+  int64_t heads_at() const { return starts_at() + segments; }
+  py::tuple meta() const {
+    return py::make_tuple(segments, groups, window, dim, max_seg_length, max_candidates, total,
+                          projected, slots, rows_total, max_head_length);
+  }
+};
+
+Plan make_plan(const std::vector<torch::Tensor>& keys, const std::vector<torch::Tensor>& values,
+               const std::vector<torch::Tensor>& positions, const std::vector<torch::Tensor>& queries,
+               const std::vector<torch::Tensor>& gradients,
+               const std::vector<std::vector<int64_t>>& head_lens,
+               const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
+               bool protect_prompt, int64_t protect_recent, bool pinned) {
   const size_t layers = keys.size();
   require(layers > 0, "No layers to score");
   require(values.size() == layers && positions.size() == layers && queries.size() == layers &&
@@ -172,9 +188,162 @@ py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<t
     }
     rows_total += base;
   }
-  py::tuple meta = py::make_tuple(segments, groups, window, dim, max_seg_length, max_candidates,
-                                  total, projected, slots, rows_total, max_head_length);
-  return py::make_tuple(block, meta, segment_info, head_info);
+  return Plan{block, segment_info, head_info, segments, groups, window, dim, max_seg_length,
+              max_candidates, total, projected, slots, rows_total, max_head_length};
+}
+
+py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<torch::Tensor>& values,
+                     const std::vector<torch::Tensor>& positions,
+                     const std::vector<torch::Tensor>& queries,
+                     const std::vector<torch::Tensor>& gradients,
+                     const std::vector<std::vector<int64_t>>& head_lens,
+                     const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
+                     bool protect_prompt, int64_t protect_recent, bool pinned) {
+  const Plan plan = make_plan(keys, values, positions, queries, gradients, head_lens, prompt_lens,
+                              protect_prompt, protect_recent, pinned);
+  return py::make_tuple(plan.block, plan.meta(), plan.segment_info, plan.head_info);
+}
+
+// Entry points of liblazyrecall_hip.so, bound once from Python (the addresses of the library
+// that the ctypes layer loaded), so that this module needs no link-time dependency on it.
+struct Library {
+  decltype(&lr_score_workspace_bytes) score_workspace_bytes = nullptr;
+  decltype(&lr_score_segments) score_segments = nullptr;
+  decltype(&lr_pool) pool = nullptr;
+  decltype(&lr_select_workspace_bytes) select_workspace_bytes = nullptr;
+  decltype(&lr_select_refine_sets) select_refine_sets = nullptr;
+  decltype(&lr_compact_heads) compact_heads = nullptr;
+  decltype(&lr_last_error) last_error = nullptr;
+};
+Library library;
+
+template <typename F>
+void bind_one(F& slot, int64_t address) {
+  require(address != 0, "null entry point");
+  slot = reinterpret_cast<F>(static_cast<uintptr_t>(address));
+}
+
+void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t pool,
+                  int64_t select_workspace_bytes, int64_t select_refine_sets,
+                  int64_t compact_heads, int64_t last_error) {
+  bind_one(library.score_workspace_bytes, score_workspace_bytes);
+  bind_one(library.score_segments, score_segments);
+  bind_one(library.pool, pool);
+  bind_one(library.select_workspace_bytes, select_workspace_bytes);
+  bind_one(library.select_refine_sets, select_refine_sets);
+  bind_one(library.compact_heads, compact_heads);
+  bind_one(library.last_error, last_error);
+}
+
+void check_call(int status) {
+  if (status != LR_OK) throw std::runtime_error(library.last_error());
+}
+
+inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
+
+// One whole audit step on the device (controller.py:140-159 without the lazy queue order):
+// plan, one metadata upload, fused scores, Pool7, the removal sets of the allocation-preserving
+// selection and the compaction of every layer, all enqueued on `stream` from here (no Python
+// between the launches). Returns (plan block, meta, segment_info, head_info, scores [2*total]
+// (raw then pooled), info i64 [S+1] (quotas, then the non-finite score count as i32),
+// quotas, offsets, removed positions, changed, out keys, out values, out positions). count is
+// clamped to [0, total]; with count 0 nothing is selected and the layers are copied as they are.
+// `mark` (None or a callable) is called with a stage name after each stage's launches and with
+// "start" before the first (then the scorer is launched stage by stage), for event timing.
+py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
+                       const std::vector<torch::Tensor>& values,
+                       const std::vector<torch::Tensor>& positions,
+                       const std::vector<torch::Tensor>& queries,
+                       const std::vector<torch::Tensor>& gradients,
+                       const std::vector<std::vector<int64_t>>& head_lens,
+                       const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
+                       int64_t protect_recent, const torch::Tensor& query_positions,
+                       const torch::Tensor& margin, int64_t count, int64_t pool_kernel,
+                       double epsilon, int64_t stream_handle, const py::object& mark) {
+  require(library.score_segments != nullptr, "library entry points are not bound");
+  require(pool_kernel > 0 && pool_kernel % 2 == 1, "pool kernel must be a positive odd integer");
+  const Plan plan = make_plan(keys, values, positions, queries, gradients, head_lens, prompt_lens,
+                              true, protect_recent, true);
+  const torch::Device device = keys[0].device();
+  require(query_positions.is_cuda() && query_positions.device() == device &&
+              query_positions.scalar_type() == torch::kInt64 && query_positions.is_contiguous() &&
+              query_positions.numel() == plan.window,
+          "Query positions do not match the window");
+  require(margin.is_cuda() && margin.device() == device && margin.scalar_type() == torch::kFloat32 &&
+              margin.numel() == 1,
+          "Invalid base margin");
+  void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
+  const auto on_device = torch::TensorOptions().device(device);
+  const int64_t S = plan.segments;
+  torch::Tensor block = plan.block.to(device, /*non_blocking=*/true);
+  const int64_t* words = block.data_ptr<int64_t>();
+  count = std::min(std::max<int64_t>(count, 0), plan.total);
+
+  // quotas (written for every segment by the selection) and the non-finite count (cleared by
+  // the first scorer kernel) come back in one small copy
+  torch::Tensor info = count > 0 ? torch::empty({S + 1}, on_device.dtype(torch::kInt64))
+                                 : torch::zeros({S + 1}, on_device.dtype(torch::kInt64));
+  int32_t* nonfinite = reinterpret_cast<int32_t*>(info.data_ptr<int64_t>() + S);
+
+  const size_t score_bytes =
+      library.score_workspace_bytes(S, plan.groups, plan.window, S * plan.groups * plan.max_seg_length);
+  torch::Tensor score_ws = torch::empty({static_cast<int64_t>(score_bytes)}, on_device.dtype(torch::kUInt8));
+  torch::Tensor scores = torch::empty({2 * plan.total}, on_device.dtype(torch::kFloat32));
+  float* raw = scores.data_ptr<float>();
+  float* pooled = raw + plan.total;
+  const bool timed = !mark.is_none();
+  auto stage = [&](const char* name) {
+    if (timed) mark(name);
+  };
+  static const char* kScoreStages[3] = {"projected_values", "row_stats", "column_scores"};
+  stage("start");
+  for (int i = 0; i < (timed ? 3 : 1); ++i) {
+    check_call(library.score_segments(
+        words, S, plan.groups, plan.window, plan.dim, plan.max_seg_length, plan.max_candidates,
+        plan.window, query_positions.data_ptr<int64_t>(), margin.data_ptr<float>(),
+        static_cast<float>(1.0 / std::sqrt(static_cast<double>(plan.dim))), epsilon,
+        dptr(score_ws), score_bytes, raw, nonfinite, timed ? 1 << i : 7, stream));
+    stage(timed ? kScoreStages[i] : "score");
+  }
+  check_call(library.pool(raw, plan.total, words + plan.bounds_at(), S, plan.max_candidates,
+                          pool_kernel, pooled, stream));
+  stage("pool");
+
+  const int64_t out_rows = plan.rows_total - count;
+  const auto kv = on_device.dtype(keys[0].scalar_type());
+  torch::Tensor out_keys = torch::empty({out_rows, plan.dim}, kv);
+  torch::Tensor out_values = torch::empty({out_rows, plan.dim}, kv);
+  torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
+  torch::Tensor sets, quotas, offsets, removed, changed;
+  if (count > 0) {
+    const size_t select_bytes = library.select_workspace_bytes(plan.total, S, count);
+    torch::Tensor select_ws =
+        torch::empty({static_cast<int64_t>(select_bytes)}, on_device.dtype(torch::kUInt8));
+    sets = torch::empty({count + 2 * S + 1}, on_device.dtype(torch::kInt64));
+    quotas = info.narrow(0, 0, S);
+    removed = sets.narrow(0, 0, count);
+    offsets = sets.narrow(0, count, S + 1);
+    changed = sets.narrow(0, count + S + 1, S);
+    check_call(library.select_refine_sets(
+        raw, pooled, plan.total, words + plan.ends_at(), words + plan.starts_at(), S, count,
+        dptr(select_ws), select_bytes, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+        removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(), stream));
+    stage("select");
+    check_call(library.compact_heads(
+        words + plan.heads_at(), plan.slots, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+        removed.data_ptr<int64_t>(), plan.dim, static_cast<int>(keys[0].element_size()),
+        plan.max_head_length, out_rows, dptr(out_keys), dptr(out_values),
+        out_positions.data_ptr<float>(), stream));
+    stage("compact");
+  } else {
+    std::vector<torch::Tensor> flat_positions;
+    for (const torch::Tensor& p : positions) flat_positions.push_back(p.reshape({-1}));
+    out_keys.copy_(torch::cat(keys));
+    out_values.copy_(torch::cat(values));
+    out_positions.copy_(torch::cat(flat_positions));
+  }
+  return py::make_tuple(plan.block, plan.meta(), plan.segment_info, plan.head_info, scores, info,
+                        quotas, offsets, removed, changed, out_keys, out_values, out_positions);
 }
 
 // The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,
@@ -239,6 +408,8 @@ py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
 
 PYBIND11_MODULE(_plan, module) {
   module.def("plan_audit", &plan_audit, "Validate layers and build the audit metadata block");
+  module.def("bind_library", &bind_library, "Bind the entry points of liblazyrecall_hip.so");
+  module.def("audit_launch", &audit_launch, "Enqueue one whole audit step");
   module.def("plan_batch_append", &plan_batch_append,
              "Validate a batch and upload its batch_append descriptors");
   module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;
