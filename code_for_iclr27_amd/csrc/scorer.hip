@@ -290,21 +290,40 @@ struct TileStager {
 // compiler does not see only lengthen its own vmcnt waits (counts drain in order), never
 // shorten them. M0 (the wave's LDS base for the copy) is set inside the same statement; no
 // compiler-generated code in these kernels keeps a value in M0.
-__device__ __forceinline__ uint32_t lds_base(void* wave_base) {
-  const auto lds = (__attribute__((address_space(3))) void*)wave_base;
-  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-}
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // M0 is a reserved register; clobbered on purpose
-__device__ __forceinline__ void dma16(const void* src, void* wave_base) {
+// Copy from a per-lane address to the (wave-uniform) LDS byte address `lds`.
+__device__ __forceinline__ void dma16_to(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds_base(wave_base)) : "memory", "m0");
+               :: "v"(src), "s"(lds) : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void* src, void* wave_base) {
+__device__ __forceinline__ void dma4_to(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(src), "s"(lds_base(wave_base)) : "memory", "m0");
+               :: "v"(src), "s"(lds) : "memory", "m0");
+}
+// The same copies addressed as a wave-uniform base (an SGPR pair) plus a per-lane 32-bit byte
+// offset: the per-copy address arithmetic is then scalar, and a lane's offset can be computed
+// once.
+__device__ __forceinline__ void dma16_at(const void* base, uint32_t offset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(offset), "s"(base), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_at(const void* base, uint32_t offset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(offset), "s"(base), "s"(lds) : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+// LDS byte address of a __shared__ object.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_address(T* object) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) T*)object));
+}
+
+__device__ __forceinline__ uint32_t wave_index() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
 // vmcnt(0) through the builtin, so that the compiler knows every vector-memory load has landed
 // here (loads issued before a loop, such as the resident MFMA operands, are then not waited for
 // again inside it); the empty statement keeps LDS accesses from moving across the wait.
@@ -318,21 +337,39 @@ __device__ __forceinline__ void dma_wait() {
 // touch eight different 16-byte bank groups per eight rows.
 __device__ __forceinline__ int swizzled_chunk(int row, int chunk) { return chunk ^ (row & 7); }
 
-// DMA of `rows` consecutive rows (row0..) of a [*, D] bf16 matrix into swizzled LDS rows; rows
-// at or past `last_row` re-read row `last_row` (callers mask them). All 256 threads call it.
+// DMA of `ROWS` consecutive rows (row0..) of a [*, D] bf16 matrix into swizzled LDS rows at LDS
+// byte address `lds`; rows at or past `last_row` re-read row `last_row` (callers mask them). All
+// 256 threads call it. Copy i moves rows [i * RPI, (i + 1) * RPI), RPI = 256 / (D / 8), a
+// multiple of 8, so a thread's (row % RPI, chunk) and hence its swizzled byte offset within the
+// copy (`dma_row_offset`) are the same for every i: while every row lies before `last_row` the
+// addresses are a scalar base plus that fixed offset.
+template <int D>
+__device__ __forceinline__ uint32_t dma_row_offset() {
+  constexpr int CH = D / 8;
+  const int row = threadIdx.x / CH, chunk = threadIdx.x % CH;
+  return static_cast<uint32_t>((row * D + 8 * swizzled_chunk(row, chunk)) * 2);
+}
+
 template <int D, int ROWS>
 __device__ __forceinline__ void dma_rows(const __bf16* matrix, int row0, int last_row,
-                                         __bf16* lds) {
-  constexpr int CH = D / 8, CHUNKS = ROWS * CH;
-  static_assert(CHUNKS % 256 == 0, "whole waves per copy");
-  const int wave = threadIdx.x >> 6;
+                                         uint32_t lds, uint32_t row_offset) {
+  constexpr int CH = D / 8, CHUNKS = ROWS * CH, RPI = 256 / CH;
+  static_assert(CHUNKS % 256 == 0 && RPI % 8 == 0, "whole waves per copy, whole swizzle periods");
+  const uint32_t wave_lds = lds + wave_index() * 64 * 16;
+  if (row0 + ROWS - 1 <= last_row) {
+    const char* base = reinterpret_cast<const char*>(matrix + static_cast<int64_t>(row0) * D);
 #pragma unroll
-  for (int i = 0; i < CHUNKS / 256; ++i) {
-    const int slot = 256 * i + threadIdx.x;
-    const int row = slot / CH, chunk = slot % CH;
-    const int source = min(row0 + row, last_row);
-    dma16(matrix + static_cast<int64_t>(source) * D + 8 * swizzled_chunk(row, chunk),
-          lds + (256 * i + 64 * wave) * 8);
+    for (int i = 0; i < CHUNKS / 256; ++i)
+      dma16_at(base + static_cast<int64_t>(i) * RPI * D * 2, row_offset, wave_lds + 256 * 16 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < CHUNKS / 256; ++i) {
+      const int slot = 256 * i + threadIdx.x;
+      const int row = slot / CH, chunk = slot % CH;
+      const int source = min(row0 + row, last_row);
+      dma16_to(matrix + static_cast<int64_t>(source) * D + 8 * swizzled_chunk(row, chunk),
+               wave_lds + 256 * 16 * i);
+    }
   }
 }
 
@@ -393,18 +430,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   // positions (rows past the end re-read the last row; commit() then gives their positions
   // +inf, which masks them). No compiler-visible load is left in the loop, so no wait the
   // compiler adds can fall between issuing the copies and the stage's LDS reads.
+  const uint32_t k_lds0 = lds_address(&k_lds[0][0]), pv_lds0 = lds_address(&pv_lds[0][0]);
+  const uint32_t kpos_lds0 = lds_address(&kpos_lds[0][0]);
+  const uint32_t row_offset = dma_row_offset<D>();
+  const int wave_id = static_cast<int>(wave_index());
   auto fetch = [&](int kt, int buf) {
     const int t0 = kt * 64;
-    dma_rows<D, 64>(seg.keys, t0, length - 1, k_lds[buf]);
-    const int wave_slot = 64 * (threadIdx.x >> 6), lane_slot = threadIdx.x & 63;
+    dma_rows<D, 64>(seg.keys, t0, length - 1, k_lds0 + buf * static_cast<uint32_t>(sizeof(k_lds[0])),
+                    row_offset);
+    const bool whole = t0 + 63 <= length - 1;  // no row of the stage past the end
+    const uint32_t lane_bytes = 4 * (threadIdx.x & 63);
 #pragma unroll
     for (int i = 0; i < kMaxGroups / 4; ++i) {
-      const int gg = 4 * i + (threadIdx.x >> 6);  // uniform per wave
-      if (gg < groups)
-        dma4(pv_seg + static_cast<int64_t>(gg) * length + min(t0 + lane_slot, length - 1),
-             &pv_lds[buf][256 * i + wave_slot]);
+      const int gg = 4 * i + wave_id;  // uniform per wave
+      if (gg < groups) {
+        const uint32_t dst = pv_lds0 + buf * static_cast<uint32_t>(sizeof(pv_lds[0])) + 4 * (256 * i + 64 * wave_id);
+        const float* row = pv_seg + static_cast<int64_t>(gg) * length;
+        if (whole) dma4_at(row + t0, lane_bytes, dst);
+        else dma4_to(row + min(t0 + static_cast<int>(threadIdx.x & 63), length - 1), dst);
+      }
     }
-    if (threadIdx.x < 64) dma4(seg.key_positions + min(t0 + lane_slot, length - 1), kpos_lds[buf]);
+    if (wave_id == 0) {
+      const uint32_t dst = kpos_lds0 + buf * static_cast<uint32_t>(sizeof(kpos_lds[0]));
+      if (whole) dma4_at(seg.key_positions + t0, lane_bytes, dst);
+      else dma4_to(seg.key_positions + min(t0 + static_cast<int>(threadIdx.x), length - 1), dst);
+    }
   };
   // After dma_wait(): the wave that copied the key positions overwrites those of rows past the
   // end (its own copy has landed, and LDS accesses of one wave complete in order).
@@ -592,6 +642,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
   bool row_loaded = false;
   int bad_reg = 0;
   int fetch_qt = 0, fetch_g = 0;  // unit of the next fetch, (query tile, group)
+  const uint32_t q_lds0 = lds_address(&q_lds[0][0]);
+  const uint32_t row_offset = dma_row_offset<D>();
   auto fetch = [&](int buf) {
     if (threadIdx.x < 32) {
       const int query = fetch_qt * 32 + threadIdx.x;
@@ -602,7 +654,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
       }
     }
     dma_rows<D, 32>(seg.queries + static_cast<int64_t>(fetch_g) * query_stride * D,
-                    fetch_qt * 32, window - 1, q_lds[buf]);
+                    fetch_qt * 32, window - 1,
+                    q_lds0 + buf * static_cast<uint32_t>(sizeof(q_lds[0])), row_offset);
     if (++fetch_g == groups) {
       fetch_g = 0;
       ++fetch_qt;
