@@ -570,6 +570,12 @@ constexpr int column_key_tiles() { return D == 128 ? 2 : 1; }
 template <int D>
 constexpr int column_waves_per_simd() { return column_key_tiles<D>() == 2 ? 2 : D <= 128 ? 3 : 1; }
 
+// Units per barrier-separated stage: two for d = 128, where the LDS of a second query tile
+// fits the two workgroups per CU that the registers allow (halving the barriers per unit;
+// measured slightly faster there, slightly slower for d = 64).
+template <int D>
+constexpr int column_units_per_stage() { return D == 128 ? 2 : 1; }
+
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_waves_per_simd<D>()))) void column_scores_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
@@ -579,9 +585,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
   constexpr int KS = D / 16;
   constexpr int KT = column_key_tiles<D>();
   constexpr int kKeys = 4 * 32 * KT;  // candidate keys per workgroup
-  __shared__ __bf16 q_lds[2][32 * D];  // swizzled rows, double buffered
-  __shared__ float4 st_lds[2][32];
-  __shared__ float qp_lds[2][32];
+  constexpr int UP = column_units_per_stage<D>();
+  __shared__ __bf16 q_lds[2][UP][32 * D];  // swizzled rows, double-buffered stages of UP units
+  __shared__ float4 st_lds[2][UP][32];
+  __shared__ float qp_lds[2][UP][32];
   __shared__ float pv_lds[kMaxGroups * kKeys];
   __shared__ float kpos_lds[kKeys];
   __shared__ int keybad_lds[kKeys];
@@ -631,38 +638,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
   }
   if (threadIdx.x == 0) rowbad_lds = 0;
 
-  // Stage loader for unit u into buffer buf: the query rows by direct copy (rows past the
-  // window re-read the last query; their results are never used), and on lanes 0..31 of wave 0
-  // the rows' statistics and query positions (padded rows: harmless values that take the fast
-  // epilogue). The statistics loads go first: a wait the compiler adds before them (they reuse
-  // the registers of the previous unit's loads) then falls before the copies are issued. Their
-  // values are first used in commit(), after the wait that also covers the row copies.
+  // Stage loader for the (up to) UP units of a stage into buffer buf: the query rows by direct
+  // copy (rows past the window re-read the last query; their results are never used), and on
+  // lanes 32k..32k+31 of wave 0 the statistics and query positions of the stage's unit k
+  // (padded rows and units past the end: harmless values that take the fast epilogue). The
+  // statistics loads go first: a wait the compiler adds before them (they reuse the registers
+  // of the previous stage's loads) then falls before the copies are issued. Their values are
+  // first used in commit(), after the wait that also covers the row copies.
   float4 st_reg = make_float4(0.0f, 2.0f, 0.0f, 0.0f);
   int64_t qp_raw = 0;
   bool row_loaded = false;
   int bad_reg = 0;
-  int fetch_qt = 0, fetch_g = 0;  // unit of the next fetch, (query tile, group)
-  const uint32_t q_lds0 = lds_address(&q_lds[0][0]);
+  int fetch_u = 0, fetch_qt = 0, fetch_g = 0;  // first unit of the next fetch, (query tile, group)
+  const uint32_t q_lds0 = lds_address(&q_lds[0][0][0]);
   const uint32_t row_offset = dma_row_offset<D>();
   auto fetch = [&](int buf) {
-    if (threadIdx.x < 32) {
-      const int query = fetch_qt * 32 + threadIdx.x;
-      row_loaded = query < window;
+    if (threadIdx.x < 32 * UP) {
+      const int k = threadIdx.x / 32;
+      int g_k = fetch_g + k, qt_k = fetch_qt;
+      if (g_k >= groups) g_k -= groups, ++qt_k;
+      const int query = qt_k * 32 + threadIdx.x % 32;
+      row_loaded = fetch_u + k < units && query < window;
       if (row_loaded) {
-        st_reg = stats_seg[static_cast<int64_t>(fetch_g) * window + query];
+        st_reg = stats_seg[static_cast<int64_t>(g_k) * window + query];
         qp_raw = query_positions[query];
       }
     }
-    dma_rows<D, 32>(seg.queries + static_cast<int64_t>(fetch_g) * query_stride * D,
-                    fetch_qt * 32, window - 1,
-                    q_lds0 + buf * static_cast<uint32_t>(sizeof(q_lds[0])), row_offset);
-    if (++fetch_g == groups) {
-      fetch_g = 0;
-      ++fetch_qt;
+#pragma unroll
+    for (int k = 0; k < UP; ++k) {
+      if (fetch_u < units)
+        dma_rows<D, 32>(seg.queries + static_cast<int64_t>(fetch_g) * query_stride * D,
+                        fetch_qt * 32, window - 1,
+                        q_lds0 + static_cast<uint32_t>((buf * UP + k) * sizeof(q_lds[0][0])),
+                        row_offset);
+      ++fetch_u;
+      if (++fetch_g == groups) {
+        fetch_g = 0;
+        ++fetch_qt;
+      }
     }
   };
   auto commit = [&](int buf) {
-    if (threadIdx.x < 32) {
+    if (threadIdx.x < 32 * UP) {
       float4 st = make_float4(0.0f, 2.0f, 0.0f, 0.0f);  // padded rows take the fast epilogue
       float qp = INFINITY;
       if (row_loaded) {
@@ -670,8 +687,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
         qp = static_cast<float>(qp_raw);
         bad_reg |= !(isfinite(st.x) && isfinite(st.y) && isfinite(st.w));
       }
-      st_lds[buf][threadIdx.x] = st;
-      qp_lds[buf][threadIdx.x] = qp;
+      st_lds[buf][threadIdx.x / 32][threadIdx.x % 32] = st;
+      qp_lds[buf][threadIdx.x / 32][threadIdx.x % 32] = qp;
     }
   };
   fetch(0);
@@ -708,14 +725,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
   const float* kpos_wave = kpos_lds + wave * 32 * KT;
 
   int qt = 0, g = 0;  // unit u = (query tile, group)
-  for (int u = 0; u < units; ++u) {
-    const int buf = u & 1;
-    // unit u + 1 goes to the other buffer; its last readers passed the previous barrier
-    if (u + 1 < units) fetch(buf ^ 1);
+  const int stages = (units + UP - 1) / UP;
+  for (int stage = 0; stage < stages; ++stage) {
+    const int buf = stage & 1;
+    // the next stage goes to the other buffer; its last readers passed the previous barrier
+    const bool more = stage + 1 < stages;
+    if (more) fetch(buf ^ 1);
+#pragma unroll
+    for (int k = 0; k < UP; ++k) {
+    if (stage * UP + k >= units) break;  // uniform
     f32x16 acc[KT];
     {
       bf16x8 b[KS];
-      const __bf16* brow = q_lds[buf] + col * D;
+      const __bf16* brow = q_lds[buf][k] + col * D;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
         b[ks] = *reinterpret_cast<const bf16x8*>(brow + 8 * swizzled_chunk(col, half * KS + ks));
@@ -727,8 +749,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
           acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[t][ks], b[ks], acc[t], 0, 0, 0);
       }
     }
-    const float4 st = st_lds[buf][col];
-    const float query_position = qp_lds[buf][col];
+    const float4 st = st_lds[buf][k][col];
+    const float query_position = qp_lds[buf][k][col];
     // ratio = p / max(1 - p, eps) = e / max(S - e, eps*S) for the lane's (key, query) pairs.
     // The general form applies the causal mask and the clamp. The fast form drops both, which
     // is exact when no key of this wave lies after any query of the unit and every row has
@@ -769,10 +791,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
         for (int j = 0; j < 4; ++j)
           drop[t][4 * c + j] = __builtin_fmaf(ratio[t][4 * c + j], w[j] - st.w, drop[t][4 * c + j]);
       }
-    if (u + 1 < units) {
-      dma_wait();
-      commit(buf ^ 1);
-    }
     if (g == groups - 1) {
       // Min / max of each key tile's drops over the query tile's queries, through this wave's
       // LDS scratch. LDS accesses of one wave complete in order, so the reads see this wave's
@@ -814,11 +832,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
         for (int r = 0; r < 16; ++r) drop[t][r] = 0.0f;
       }
     }
-    __syncthreads();
     if (++g == groups) {
       g = 0;
       ++qt;
     }
+    }  // unit k of the stage
+    if (more) {
+      dma_wait();
+      commit(buf ^ 1);
+    }
+    __syncthreads();
   }
   if (bad_reg) rowbad_lds = 1;
   __syncthreads();
