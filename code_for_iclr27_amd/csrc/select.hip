@@ -286,12 +286,14 @@ __host__ __device__ constexpr PassShape pass_shape(int pass) {
 
 __global__ __launch_bounds__(256) void select_init_kernel(SelectState* __restrict__ states,
                                                           uint32_t* __restrict__ hist,
+                                                          uint32_t* __restrict__ ticket,
                                                           uint32_t count) {
   for (int i = threadIdx.x; i < 3 * kHistStride; i += 256) hist[i] = 0;
   if (threadIdx.x == 0) {
     SelectState st{};
     st.remaining = count;
     states[0] = st;
+    *ticket = 0;
   }
 }
 
@@ -368,13 +370,19 @@ __global__ __launch_bounds__(256) void select_pass_kernel(const float* __restric
 
 // Per segment: how many raw keys are below / equal to the global threshold. Every workgroup
 // first finishes the threshold from the last pass histogram; workgroup 0 publishes it as
-// states[3] = {threshold, all-ones mask, threshold-equal keys to take, keys below}.
+// states[3] = {threshold, all-ones mask, threshold-equal keys to take, keys below}. The last
+// workgroup to finish (a ticket counter, no waiting) then plans the per-segment quotas: the
+// threshold-equal keys are granted in index order, i.e. segment order, and the quotas' exclusive
+// prefix gives each segment's offset.
 __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
     const float* __restrict__ scores, const int64_t* __restrict__ ends,
     SelectState* __restrict__ states, const uint32_t* __restrict__ hist,
-    uint32_t* __restrict__ seg_less, uint32_t* __restrict__ seg_equal) {
+    uint32_t* __restrict__ seg_less, uint32_t* __restrict__ seg_equal,
+    uint32_t* __restrict__ ticket, int64_t segments, uint32_t* __restrict__ take_equal,
+    int64_t* __restrict__ quotas, int64_t* __restrict__ offsets) {
   __shared__ uint32_t wave_sums[kSegThreads / 64][2];
   __shared__ uint32_t found[2];
+  __shared__ bool last;
   const SelectState st = extend_state<2>(states[2], hist, wave_sums, found);
   if (blockIdx.x == 0 && threadIdx.x == 0) states[3] = st;
   const int64_t s = blockIdx.x;
@@ -391,34 +399,30 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
   if (threadIdx.x == 0) {
     seg_less[s] = total_less;
     seg_equal[s] = total_equal;
+    __threadfence();  // the counts are visible device-wide before the ticket is taken
+    last = atomicAdd(ticket, 1u) == gridDim.x - 1;
   }
-}
-
-// One workgroup: per-segment quotas (threshold-equal keys are granted in index order, i.e.
-// segment order) and their exclusive prefix.
-__global__ __launch_bounds__(1024) void segment_plan_kernel(
-    const uint32_t* __restrict__ seg_less, const uint32_t* __restrict__ seg_equal,
-    const SelectState* __restrict__ states, int64_t segments, uint32_t* __restrict__ take_equal,
-    int64_t* __restrict__ quotas, int64_t* __restrict__ offsets) {
-  __shared__ uint32_t wave_sums[16][2];
-  const uint32_t need = states[3].remaining;
+  __syncthreads();
+  if (!last) return;  // uniform across the workgroup
+  __threadfence();
+  const uint32_t need = st.remaining;
   uint32_t carry_equal = 0, carry_quota = 0;
-  for (int64_t base = 0; base < segments; base += 1024) {
-    const int64_t s = base + threadIdx.x;
-    const uint32_t eq = s < segments ? seg_equal[s] : 0;
+  for (int64_t base = 0; base < segments; base += kSegThreads) {
+    const int64_t t = base + threadIdx.x;
+    const uint32_t eq = t < segments ? seg_equal[t] : 0;
     uint32_t eq_before, unused, eq_total, unused_total;
-    block_scan_pair<1024>(eq, 0u, wave_sums, eq_before, unused, eq_total, unused_total);
+    block_scan_pair<kSegThreads>(eq, 0u, wave_sums, eq_before, unused, eq_total, unused_total);
     eq_before += carry_equal;
     uint32_t take = 0;
     if (need > eq_before) take = need - eq_before < eq ? need - eq_before : eq;
-    const uint32_t quota = s < segments ? seg_less[s] + take : 0;
+    const uint32_t quota = t < segments ? seg_less[t] + take : 0;
     uint32_t quota_before, quota_total;
-    block_scan_pair<1024>(quota, 0u, wave_sums, quota_before, unused, quota_total, unused_total);
+    block_scan_pair<kSegThreads>(quota, 0u, wave_sums, quota_before, unused, quota_total, unused_total);
     quota_before += carry_quota;
-    if (s < segments) {
-      take_equal[s] = take;
-      quotas[s] = quota;
-      offsets[s] = quota_before;
+    if (t < segments) {
+      take_equal[t] = take;
+      quotas[t] = quota;
+      offsets[t] = quota_before;
     }
     carry_equal += eq_total;
     carry_quota += quota_total;
@@ -683,6 +687,7 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
 struct SelectWorkspace {
   SelectState* states;  // [4]: before each threshold pass, then final
   uint32_t* hist;       // [3][kHistStride]
+  uint32_t* ticket;     // workgroups of segment_count that have finished
   uint32_t* seg_less;
   uint32_t* seg_equal;
   uint32_t* take_equal;
@@ -703,6 +708,7 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
   };
   w.states = reinterpret_cast<SelectState*>(take(4 * sizeof(SelectState)));
   w.hist = reinterpret_cast<uint32_t*>(take(size_t{3} * kHistStride * 4));
+  w.ticket = reinterpret_cast<uint32_t*>(take(4));
   w.seg_less = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.seg_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.take_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
@@ -722,7 +728,7 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
                 const int64_t* position_starts, int64_t segments, int64_t count,
                 const SelectWorkspace& w, int64_t* quotas, int64_t* offsets,
                 int64_t* removed_positions, int64_t* changed, hipStream_t s) {
-  select_init_kernel<<<1, 256, 0, s>>>(w.states, w.hist, static_cast<uint32_t>(count));
+  select_init_kernel<<<1, 256, 0, s>>>(w.states, w.hist, w.ticket, static_cast<uint32_t>(count));
   if (int rc = check_launch("select_init")) return rc;
   const int64_t chunk = ceil_div(ceil_div(total, kHistBlocks), 1024) * 1024;
   const int blocks = static_cast<int>(ceil_div(total, chunk));
@@ -731,10 +737,9 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
   select_pass_kernel<2><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
   if (int rc = check_launch("select_pass")) return rc;
   segment_count_kernel<<<segments, kSegThreads, 0, s>>>(raw, segment_ends, w.states, w.hist,
-                                                        w.seg_less, w.seg_equal);
-  segment_plan_kernel<<<1, 1024, 0, s>>>(w.seg_less, w.seg_equal, w.states, segments,
-                                         w.take_equal, quotas, offsets);
-  if (int rc = check_launch("segment_plan")) return rc;
+                                                        w.seg_less, w.seg_equal, w.ticket,
+                                                        segments, w.take_equal, quotas, offsets);
+  if (int rc = check_launch("segment_count")) return rc;
   segment_pick_kernel<<<segments, kSegThreads, 0, s>>>(
       raw, pooled, segment_ends, position_starts, w.states, w.take_equal, quotas, offsets,
       w.raw_flags, w.run_keys, w.refined_keys, w.refined_local, removed_positions, changed);
