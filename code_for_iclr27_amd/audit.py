@@ -150,19 +150,29 @@ class AuditStep:
     def run(self, layers: Sequence[LayerState], query_positions: torch.Tensor,
             margin: torch.Tensor, count: int, protect_recent: int = 32, pool_kernel: int = 7,
             denominator_epsilon: float = 1e-6, check_finite: bool = True,
-            queue_order: bool = False, timer=None) -> AuditOutcome:
+            queue_order: bool = False, timer=None, native: bool = True) -> AuditOutcome:
         """Scores, selects and removes ``count`` slots. Every selected slot is removed now
         (immediate == count in controller.run_audit, controller.py:148-158), so the lazy queue
         ``references[immediate:]`` is empty and the removal sets are all the step needs; the
         queue order (``outcome.selection.values/segments/positions``) is computed only with
         ``queue_order=True``, on a side stream, overlapping the compaction.
         ``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
-        stage, on the current stream, for per-stage event timing."""
+        stage, on the current stream, for per-stage event timing. The launches are made by the
+        C++ host module; ``native=False`` makes the same launches from Python (a cross-check).
+        """
         if pool_kernel <= 0 or pool_kernel % 2 == 0:
             raise ValueError("pool kernel must be a positive odd integer")
-        if not queue_order:
-            return self._run_native(layers, query_positions, margin, count, protect_recent,
-                                    pool_kernel, denominator_epsilon, check_finite, timer)
+        if not native:
+            return self._run_python(layers, query_positions, margin, count, protect_recent,
+                                    pool_kernel, denominator_epsilon, check_finite, queue_order,
+                                    timer)
+        return self._run_native(layers, query_positions, margin, count, protect_recent,
+                                pool_kernel, denominator_epsilon, check_finite, timer,
+                                queue_order)
+
+    def _run_python(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
+                    denominator_epsilon, check_finite, queue_order, timer):
+        """The same step launched from Python (plan_segments, ctypes calls)."""
         mark = timer.mark if timer is not None else (lambda name: None)
         plan = plan_segments(layers, protect_prompt=True, protect_recent=protect_recent,
                              pinned=True)
@@ -258,24 +268,56 @@ class AuditStep:
         new_layers = PackedLayers(out_keys, out_values, out_positions, kept, layers)
         return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, count)
 
+    def _queue_native(self, selection, plan, device_block, select_ws, count, sets_done, device):
+        """lr_select_refine_queue (controller.py:148-158's references order) on the side stream,
+        after the removal sets; fills selection.values/segments/positions."""
+        stream = self._queue_stream(device)
+        values = torch.empty((count,), dtype=torch.float32, device=device)
+        order = torch.empty((2 * count,), dtype=torch.int64, device=device)
+        stream.wait_event(sets_done)
+        starts = plan.part("starts", device_block)
+        _lib.call("lr_select_refine_queue", starts.data_ptr(), plan.total, plan.segment_count,
+                  count, select_ws.data_ptr(), select_ws.numel(), selection.quotas.data_ptr(),
+                  selection.offsets.data_ptr(), values.data_ptr(), order.data_ptr(),
+                  order[count:].data_ptr(), stream.cuda_stream)
+        ready = torch.cuda.Event()
+        ready.record(stream)
+        # memory the side stream uses stays reserved until that stream's work is done
+        for tensor in (select_ws, values, order, selection.quotas, selection.offsets, device_block):
+            tensor.record_stream(stream)
+        selection.values, selection.segments, selection.positions = values, order[:count], order[count:]
+        selection.queue_ready = ready
+
     def _run_native(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
-                    denominator_epsilon, check_finite, timer=None):
-        """The same step with planning and every launch done by the C++ host module
-        (csrc/host_plan.cpp audit_launch): no Python between the launches."""
+                    denominator_epsilon, check_finite, timer=None, queue_order=False):
+        """The step with planning and every launch done by the C++ host module
+        (csrc/host_plan.cpp audit_launch): no Python between the launches. With
+        ``queue_order`` the queue half of the selection runs on a side stream after the
+        removal sets (an event recorded between the selection and the compaction), and the
+        current stream joins it before the step's synchronisation."""
         if len(layers) == 0:
             raise RuntimeError("No layers to score")
         planner = _native_planner()
         device = layers[0].keys.device
         margin = margin.to(device=device, dtype=torch.float32).reshape(1)
+        mark = None if timer is None else timer.mark
+        sets_done = None
+        if queue_order:
+            sets_done = torch.cuda.Event()
+
+            def mark(name, inner=mark):
+                if name == "select":
+                    sets_done.record()
+                if inner is not None:
+                    inner(name)
         (block, meta, segment_info, head_info, scores, info, quotas, offsets, removed, changed,
-         out_keys, out_values, out_positions) = planner.audit_launch(
+         out_keys, out_values, out_positions, device_block, select_ws) = planner.audit_launch(
             [layer.keys for layer in layers], [layer.values for layer in layers],
             [layer.positions for layer in layers], [layer.queries for layer in layers],
             [layer.gradient for layer in layers], [list(layer.head_lens) for layer in layers],
             [None if layer.prompt_lens is None else list(layer.prompt_lens) for layer in layers],
             int(protect_recent), query_positions, margin, int(count), int(pool_kernel),
-            float(denominator_epsilon), torch.cuda.current_stream(device).cuda_stream,
-            None if timer is None else timer.mark)
+            float(denominator_epsilon), torch.cuda.current_stream(device).cuda_stream, mark)
         plan = SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
         total = plan.total
         count = min(max(0, int(count)), total)
@@ -283,5 +325,11 @@ class AuditStep:
         if count:
             selection = DeviceSelection(None, None, None, quotas, offsets, removed, changed,
                                         plan.segment_info[:2].T)
+            if queue_order:
+                self._queue_native(selection, plan, device_block, select_ws, count, sets_done,
+                                   device)
+                selection.wait_queue()  # join the queue order back before the step ends
+                if timer is not None:
+                    timer.mark("queue_join")
         return self._finish(plan, info, scores[:total], scores[total:], selection, count,
                             out_keys, out_values, out_positions, layers, check_finite)

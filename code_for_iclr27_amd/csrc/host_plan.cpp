@@ -246,7 +246,8 @@ inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 // selection and the compaction of every layer, all enqueued on `stream` from here (no Python
 // between the launches). Returns (plan block, meta, segment_info, head_info, scores [2*total]
 // (raw then pooled), info i64 [S+1] (quotas, then the non-finite score count as i32),
-// quotas, offsets, removed positions, changed, out keys, out values, out positions). count is
+// quotas, offsets, removed positions, changed, out keys, out values, out positions, the block
+// on the device, the selection workspace (for the queue order, lr_select_refine_queue)). count is
 // clamped to [0, total]; with count 0 nothing is selected and the layers are copied as they are.
 // `mark` (None or a callable) is called with a stage name after each stage's launches and with
 // "start" before the first (then the scorer is launched stage by stage), for event timing.
@@ -314,11 +315,10 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   torch::Tensor out_keys = torch::empty({out_rows, plan.dim}, kv);
   torch::Tensor out_values = torch::empty({out_rows, plan.dim}, kv);
   torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
-  torch::Tensor sets, quotas, offsets, removed, changed;
+  torch::Tensor sets, quotas, offsets, removed, changed, select_ws;
   if (count > 0) {
     const size_t select_bytes = library.select_workspace_bytes(plan.total, S, count);
-    torch::Tensor select_ws =
-        torch::empty({static_cast<int64_t>(select_bytes)}, on_device.dtype(torch::kUInt8));
+    select_ws = torch::empty({static_cast<int64_t>(select_bytes)}, on_device.dtype(torch::kUInt8));
     sets = torch::empty({count + 2 * S + 1}, on_device.dtype(torch::kInt64));
     quotas = info.narrow(0, 0, S);
     removed = sets.narrow(0, 0, count);
@@ -343,7 +343,8 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
     out_positions.copy_(torch::cat(flat_positions));
   }
   return py::make_tuple(plan.block, plan.meta(), plan.segment_info, plan.head_info, scores, info,
-                        quotas, offsets, removed, changed, out_keys, out_values, out_positions);
+                        quotas, offsets, removed, changed, out_keys, out_values, out_positions,
+                        block, select_ws);
 }
 
 // The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,

@@ -127,6 +127,33 @@ def test_refine_arrays_signature(device):
         k: list(v) for k, v in expect.groups([(0, 0), (0, 1), (0, 2)]).items()}
 
 
+@pytest.mark.parametrize("queue_order", [False, True])
+def test_native_and_python_launches_agree(device, queue_order):
+    """The C++ host module and the Python launch sequence make the same launches: every output
+    of the step is bit-identical (prompt protection and a head without candidates included)."""
+    head_lengths = [[400, 380, 35, 410], [390, 10, 400, 402]]
+    layers, qpos = workloads.make_layers(head_lengths, 4, 128, 80, device, seed=5,
+                                         prompt_lengths=[[3, 0, 40, 7], [0, 0, 12, 390]])
+    margin = torch.tensor([2.0], device=device)
+    step = audit.AuditStep()
+    native = step.run(layers, qpos, margin, 500, queue_order=queue_order)
+    python = step.run(layers, qpos, margin, 500, queue_order=queue_order, native=False)
+    torch.cuda.synchronize()
+    assert native.head_lens == python.head_lens and native.removed == python.removed
+    np.testing.assert_array_equal(native.scores.cpu().numpy(), python.scores.cpu().numpy())
+    np.testing.assert_array_equal(native.pooled.cpu().numpy(), python.pooled.cpu().numpy())
+    for a, b in zip(native.layers, python.layers):
+        assert torch.equal(a.keys, b.keys) and torch.equal(a.values, b.values)
+        assert torch.equal(a.positions, b.positions)
+    for name in ("quotas", "offsets", "removed_positions", "changed"):
+        assert torch.equal(getattr(native.selection, name), getattr(python.selection, name))
+    if queue_order:
+        qa, qb = native.selection.references(), python.selection.references()
+        np.testing.assert_array_equal(qa.scores, qb.scores)
+        np.testing.assert_array_equal(qa.segments, qb.segments)
+        np.testing.assert_array_equal(qa.positions, qb.positions)
+
+
 @pytest.mark.parametrize("dim,groups,queue_order", [(128, 4, False), (64, 4, False), (128, 4, True)])
 def test_audit_step_matches_oracle_chain(device, dim, groups, queue_order):
     head_lengths = [[400, 380, 35, 410], [390, 10, 400, 402], [333, 401, 399, 64]]
