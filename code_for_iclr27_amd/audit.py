@@ -10,8 +10,10 @@ torch.topk calls with device->host copies, host list -> tensor copies per layer 
 compaction launch per layer. Here the host builds one int64 metadata block (segment table,
 pool bounds, segment ends, head table), uploads it once from pinned memory, and enqueues:
 3 scoring kernels, 1 pool kernel, the selection kernels and 1 compaction kernel covering all
-layers. The only synchronisation is the final copy of the per-segment quotas, which the host
-needs to describe the new ragged layout (as the reference's metadata rebuild does). The
+layers. The only synchronisation is a wait for the per-segment quotas, which the host needs to
+describe the new ragged layout (as the reference's metadata rebuild does): they are copied to
+pinned memory with an event right after the selection, before the compaction is enqueued, so
+the host builds the layout (and enqueues the caller's next work) while the compaction runs. The
 eviction-queue order (a per-segment sort and a merge of all segments' picks) is only needed
 for a non-empty lazy queue; on request it runs on a side stream while the compaction, which
 needs only the removal sets, runs on the current stream.
@@ -70,11 +72,11 @@ class PackedLayers(abc.Sequence):
     positions buffer (layer-major, heads in order). Layer i's LayerState, with views into those
     buffers, is created when first indexed."""
 
-    def __init__(self, keys, values, positions, kept: np.ndarray, sources: Sequence[LayerState]):
+    def __init__(self, keys, values, positions, kept: List[List[int]], offsets: List[int],
+                 sources: Sequence[LayerState]):
         self.keys, self.values, self.positions = keys, values, positions
-        self.kept = kept                                   # [L, H] rows kept per head
-        rows = kept.sum(axis=1)
-        self.offsets = np.concatenate(([0], np.cumsum(rows))).tolist()
+        self.kept = kept                                   # [L][H] rows kept per head
+        self.offsets = offsets                             # [L + 1] first row of each layer
         self.sources = sources
         self._cache = {}
 
@@ -93,7 +95,7 @@ class PackedLayers(abc.Sequence):
             start, end = self.offsets[index], self.offsets[index + 1]
             source = self.sources[index]
             layer = LayerState(self.keys[start:end], self.values[start:end],
-                               self.positions[start:end], self.kept[index].tolist(),
+                               self.positions[start:end], list(self.kept[index]),
                                source.prompt_lens, source.queries, source.gradient)
             self._cache[index] = layer
         return layer
@@ -137,6 +139,7 @@ class AuditStep:
         self.workspace = _Workspace()
         self.select_workspace = SelectWorkspace()
         self.queue_streams = {}
+        self.syncs = {}
 
     def _queue_stream(self, device) -> torch.cuda.Stream:
         """Side stream (default priority) for the eviction-queue order; the compaction, which
@@ -253,19 +256,20 @@ class AuditStep:
     @staticmethod
     def _finish(plan, info, raw, pooled, selection, count, out_keys, out_values, out_positions,
                 layers, check_finite):
+        """The Python path's end: one copy of the quotas (which waits for the whole step), then
+        the new ragged layout (host metadata, views into the packed buffers)."""
         segments = plan.segment_count
         host_info = info.cpu().numpy()  # the step's only synchronisation
         quotas = host_info[:segments]
         bad = int(host_info[segments:].view(np.int32)[0])
         if check_finite and bad:
             raise RuntimeError("LazyRecall produced non-finite scores; refusing to construct a deletion queue")
-
-        # --- new ragged layout (host metadata, views into the packed buffers) ----------------
         segment_index, lengths = plan.head_info
         removed_per_slot = np.where(segment_index >= 0, quotas[np.maximum(segment_index, 0)], 0)
         kept = (lengths - removed_per_slot).reshape(-1, plan.heads)
+        offsets = np.concatenate(([0], np.cumsum(kept.sum(axis=1)))).tolist()
         new_lens = kept.tolist()
-        new_layers = PackedLayers(out_keys, out_values, out_positions, kept, layers)
+        new_layers = PackedLayers(out_keys, out_values, out_positions, new_lens, offsets, layers)
         return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, count)
 
     def _queue_native(self, selection, plan, device_block, select_ws, count, sets_done, device):
@@ -299,6 +303,9 @@ class AuditStep:
             raise RuntimeError("No layers to score")
         planner = _native_planner()
         device = layers[0].keys.device
+        sync = self.syncs.get(device)
+        if sync is None:
+            sync = self.syncs[device] = planner.StepSync()
         margin = margin.to(device=device, dtype=torch.float32).reshape(1)
         mark = None if timer is None else timer.mark
         sets_done = None
@@ -317,7 +324,7 @@ class AuditStep:
             [layer.gradient for layer in layers], [list(layer.head_lens) for layer in layers],
             [None if layer.prompt_lens is None else list(layer.prompt_lens) for layer in layers],
             int(protect_recent), query_positions, margin, int(count), int(pool_kernel),
-            float(denominator_epsilon), torch.cuda.current_stream(device).cuda_stream, mark)
+            float(denominator_epsilon), torch.cuda.current_stream(device).cuda_stream, mark, sync)
         plan = SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
         total = plan.total
         count = min(max(0, int(count)), total)
@@ -331,5 +338,8 @@ class AuditStep:
                 selection.wait_queue()  # join the queue order back before the step ends
                 if timer is not None:
                     timer.mark("queue_join")
-        return self._finish(plan, info, scores[:total], scores[total:], selection, count,
-                            out_keys, out_values, out_positions, layers, check_finite)
+        # waits for the selection only; the compaction may still run (outputs in stream order)
+        kept, offsets = sync.wait(check_finite)
+        new_layers = PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers)
+        return AuditOutcome(new_layers, [list(lengths) for lengths in kept], scores[:total],
+                            scores[total:], selection, plan, count)

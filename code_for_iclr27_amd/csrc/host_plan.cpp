@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <optional>
 #include <stdexcept>
 #include <vector>
@@ -55,7 +56,7 @@ inline int64_t ptr(const torch::Tensor& t) { return reinterpret_cast<int64_t>(t.
 struct Plan {
   torch::Tensor block, segment_info, head_info;
   int64_t segments, groups, window, dim, max_seg_length, max_candidates, total, projected, slots,
-      rows_total, max_head_length;
+      rows_total, max_head_length, layers;
   // word offsets of the block's parts
   int64_t bounds_at() const { return segments * LR_SEG_WORDS; }
   int64_t ends_at() const { return bounds_at() + segments + 1; }
@@ -189,7 +190,8 @@ Plan make_plan(const std::vector<torch::Tensor>& keys, const std::vector<torch::
     rows_total += base;
   }
   return Plan{block, segment_info, head_info, segments, groups, window, dim, max_seg_length,
-              max_candidates, total, projected, slots, rows_total, max_head_length};
+              max_candidates, total, projected, slots, rows_total, max_head_length,
+              static_cast<int64_t>(layers)};
 }
 
 py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<torch::Tensor>& values,
@@ -241,6 +243,70 @@ void check_call(int status) {
 
 inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 
+// The host's one wait of an audit step. The per-segment quotas and the non-finite score count
+// are final once the selection kernels are done, so audit_launch copies them into pinned
+// memory and records `ready` right after the selection, before it enqueues the compaction;
+// wait() blocks on that event only and builds the new ragged layout while the compaction still
+// runs. One object serves one step at a time (an AuditStep keeps one per device); each step's
+// wait() must return before the next audit_launch with the same object.
+struct StepSync {
+  c10::Event ready{c10::DeviceType::CUDA};
+  torch::Tensor host_info;                          // pinned int64 [segments + 1]
+  std::vector<int64_t> slot_segment, slot_length;   // per (layer, head): segment or -1, length
+  int64_t layers = 0, heads = 0, segments = 0;
+  bool pending = false;
+
+  void post(const Plan& plan, const torch::Tensor& info, const torch::Device& device) {
+    const int64_t words = plan.segments + 1;
+    if (!host_info.defined() || host_info.numel() < words)
+      host_info = torch::empty({words}, torch::dtype(torch::kInt64).pinned_memory(true));
+    host_info.narrow(0, 0, words).copy_(info, /*non_blocking=*/true);
+    ready.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+    const int64_t* slot = plan.head_info.data_ptr<int64_t>();
+    slot_segment.assign(slot, slot + plan.slots);
+    slot_length.assign(slot + plan.slots, slot + 2 * plan.slots);
+    layers = plan.layers;
+    heads = plan.slots / plan.layers;
+    segments = plan.segments;
+    pending = true;
+  }
+
+  // Waits for the selection, refuses non-finite scores (scoring.py:292-293's message), and
+  // returns (rows kept per head as [L][H] lists, row offset of each layer in the packed
+  // output [L + 1]).
+  py::tuple wait(bool check_finite) {
+    require(pending, "no audit step is pending on this StepSync");
+    pending = false;
+    {
+      py::gil_scoped_release release;
+      ready.synchronize();
+    }
+    const int64_t* info = host_info.data_ptr<int64_t>();
+    int32_t bad = 0;
+    std::memcpy(&bad, info + segments, sizeof(bad));
+    if (check_finite && bad != 0)
+      throw std::runtime_error(
+          "LazyRecall produced non-finite scores; refusing to construct a deletion queue");
+    py::list kept(layers);
+    py::list offsets(layers + 1);
+    int64_t row = 0;
+    offsets[0] = py::int_(0);
+    for (int64_t l = 0; l < layers; ++l) {
+      py::list lengths(heads);
+      for (int64_t h = 0; h < heads; ++h) {
+        const int64_t slot = l * heads + h;
+        const int64_t s = slot_segment[slot];
+        const int64_t n = slot_length[slot] - (s >= 0 ? info[s] : 0);
+        lengths[h] = py::int_(n);
+        row += n;
+      }
+      kept[l] = lengths;
+      offsets[l + 1] = py::int_(row);
+    }
+    return py::make_tuple(kept, offsets);
+  }
+};
+
 // One whole audit step on the device (controller.py:140-159 without the lazy queue order):
 // plan, one metadata upload, fused scores, Pool7, the removal sets of the allocation-preserving
 // selection and the compaction of every layer, all enqueued on `stream` from here (no Python
@@ -251,6 +317,8 @@ inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 // clamped to [0, total]; with count 0 nothing is selected and the layers are copied as they are.
 // `mark` (None or a callable) is called with a stage name after each stage's launches and with
 // "start" before the first (then the scorer is launched stage by stage), for event timing.
+// `sync` (or None) receives the quota copy and its event between the selection and the
+// compaction (StepSync above).
 py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        const std::vector<torch::Tensor>& values,
                        const std::vector<torch::Tensor>& positions,
@@ -260,7 +328,8 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
                        int64_t protect_recent, const torch::Tensor& query_positions,
                        const torch::Tensor& margin, int64_t count, int64_t pool_kernel,
-                       double epsilon, int64_t stream_handle, const py::object& mark) {
+                       double epsilon, int64_t stream_handle, const py::object& mark,
+                       StepSync* sync) {
   require(library.score_segments != nullptr, "library entry points are not bound");
   require(pool_kernel > 0 && pool_kernel % 2 == 1, "pool kernel must be a positive odd integer");
   const Plan plan = make_plan(keys, values, positions, queries, gradients, head_lens, prompt_lens,
@@ -329,6 +398,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
         dptr(select_ws), select_bytes, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
         removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(), stream));
     stage("select");
+    if (sync != nullptr) sync->post(plan, info, device);
     check_call(library.compact_heads(
         words + plan.heads_at(), plan.slots, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
         removed.data_ptr<int64_t>(), plan.dim, static_cast<int>(keys[0].element_size()),
@@ -336,6 +406,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
         out_positions.data_ptr<float>(), stream));
     stage("compact");
   } else {
+    if (sync != nullptr) sync->post(plan, info, device);
     std::vector<torch::Tensor> flat_positions;
     for (const torch::Tensor& p : positions) flat_positions.push_back(p.reshape({-1}));
     out_keys.copy_(torch::cat(keys));
@@ -410,6 +481,10 @@ py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
 PYBIND11_MODULE(_plan, module) {
   module.def("plan_audit", &plan_audit, "Validate layers and build the audit metadata block");
   module.def("bind_library", &bind_library, "Bind the entry points of liblazyrecall_hip.so");
+  py::class_<StepSync>(module, "StepSync")
+      .def(py::init<>())
+      .def("wait", &StepSync::wait, py::arg("check_finite"),
+           "Wait for the selection of the pending step; returns (kept [L][H], layer offsets)");
   module.def("audit_launch", &audit_launch, "Enqueue one whole audit step");
   module.def("plan_batch_append", &plan_batch_append,
              "Validate a batch and upload its batch_append descriptors");
