@@ -567,6 +567,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 template <int D>
 constexpr int column_key_tiles() { return D == 128 ? 2 : 1; }
 
+// Transpose scratch of the column reduction: source lane L's 16 drops start at red_slot(L).
+// Rows are 20 floats apart (16-byte aligned; 8 or 16 consecutive lanes' 16-byte writes fall in
+// distinct banks) and lanes 16..31, 32..47, 48..63 are skewed by 16, 32, 48 floats, so a read
+// of one element of 16 consecutive source lanes by the 4 x 16 reducer lanes (same element
+// index r, source lanes L = 16 k + q) touches 64 distinct banks (32 per half-wave).
+constexpr int kRedStride = 20;
+constexpr int kRedFloats = 63 * kRedStride + 48 + 16;
+__device__ __forceinline__ int red_slot(int source_lane) {
+  return source_lane * kRedStride + 16 * ((source_lane >> 4) & 3);
+}
+
 template <int D>
 constexpr int column_waves_per_simd() { return column_key_tiles<D>() == 2 ? 2 : D <= 128 ? 3 : 1; }
 
@@ -592,7 +603,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
   __shared__ float pv_lds[kMaxGroups * kKeys];
   __shared__ float kpos_lds[kKeys];
   __shared__ int keybad_lds[kKeys];
-  __shared__ float red_lds[4][64 * 16];  // per-wave transpose scratch (one key tile at a time)
+  __shared__ float red_lds[4][kRedFloats];  // per-wave transpose scratch (one key tile at a time)
   __shared__ int rowbad_lds;
 
   const int groups = static_cast<int>(groups64), window = static_cast<int>(window64);
@@ -800,25 +811,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
       for (int t = 0; t < KT; ++t) {
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          *reinterpret_cast<f32x4*>(red + lane * 16 + 4 * c) =
+          *reinterpret_cast<f32x4*>(red + red_slot(lane) + 4 * c) =
               f32x4{drop[t][4 * c], drop[t][4 * c + 1], drop[t][4 * c + 2], drop[t][4 * c + 3]};
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-        const float* column = red + (half_red * 32 + part * 16) * 16 + r_red;
+        const float* column = red + red_slot(half_red * 32 + part * 16) + r_red;
         float tile_lo = INFINITY, tile_hi = -INFINITY;
         // NaN-propagating, as torch's amin / amax
         if (valid == 16) {
 #pragma unroll
           for (int q = 0; q < 16; ++q) {
-            const float x = column[q * 16];
+            const float x = column[q * kRedStride];
             tile_lo = __builtin_elementwise_minimum(tile_lo, x);
             tile_hi = __builtin_elementwise_maximum(tile_hi, x);
           }
         } else {
 #pragma unroll
           for (int q = 0; q < 16; ++q) {
-            const float x = column[q * 16];
+            const float x = column[q * kRedStride];
             tile_lo = __builtin_elementwise_minimum(tile_lo, q < valid ? x : INFINITY);
             tile_hi = __builtin_elementwise_maximum(tile_hi, q < valid ? x : -INFINITY);
           }
