@@ -249,36 +249,6 @@ __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __
   }
 }
 
-// Stages a 32-row bf16 tile (rows src_row0.., D wide, rows >= valid_rows zero) into LDS with
-// a 16-byte pad per row. All 256 threads participate.
-template <int D>
-struct TileStager {
-  static constexpr int kChunks = 32 * D / 8;  // 16-byte chunks per tile
-  static constexpr int kPerThread = (kChunks + 255) / 256;
-  uint4 data[kPerThread];
-
-  __device__ __forceinline__ void load(const __bf16* base, int64_t valid_rows) {
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / (D / 8), part = c % (D / 8);
-      data[i] = make_uint4(0, 0, 0, 0);
-      if (c < kChunks && row < valid_rows) {
-        const u32x4 v = gload<u32x4>(base + static_cast<int64_t>(row) * D + 8 * part);
-        data[i] = make_uint4(v.x, v.y, v.z, v.w);
-      }
-    }
-  }
-  __device__ __forceinline__ void store(__bf16* lds) const {
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / (D / 8), part = c % (D / 8);
-      if (c < kChunks) *reinterpret_cast<uint4*>(lds + row * (D + 8) + 8 * part) = data[i];
-    }
-  }
-};
-
 // Direct global -> LDS copies (global_load_lds_dword / _dwordx4): lane L of a wave writes its
 // granule at LDS `wave_base` + L * granule; `wave_base` must be the same for the whole wave.
 // Nothing passes through VGPRs. Completion is awaited with dma_wait() before the barrier that
