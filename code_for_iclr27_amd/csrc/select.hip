@@ -469,15 +469,21 @@ __device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_a
 //   pooled picks: the same rule against the segment's own pooled threshold (bottom-quota).
 // Writes the raw picks' keys (index order, for the queue), the pooled picks (index order:
 // removal positions ascending, their keys and local indexes for the queue), and the count of
-// pooled picks that are not raw picks.
+// pooled picks that are not raw picks. Segments of up to kPickStaged candidates are read from
+// global memory once, with coalesced loads, into LDS keys that every later pass reads; longer
+// segments read global memory in each pass.
+constexpr uint32_t kPickStaged = 4096;
+
 __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
     const float* __restrict__ raw, const float* __restrict__ pooled,
     const int64_t* __restrict__ ends, const int64_t* __restrict__ position_starts,
     const SelectState* __restrict__ states, const uint32_t* __restrict__ take_equal,
     const int64_t* __restrict__ quotas, const int64_t* __restrict__ offsets,
-    uint8_t* __restrict__ raw_flags, uint32_t* __restrict__ run_keys,
-    uint32_t* __restrict__ refined_keys, uint32_t* __restrict__ refined_local,
-    int64_t* __restrict__ removed_positions, int64_t* __restrict__ changed) {
+    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ refined_keys,
+    uint32_t* __restrict__ refined_local, int64_t* __restrict__ removed_positions,
+    int64_t* __restrict__ changed) {
+  __shared__ uint32_t raw_keys[kPickStaged];
+  __shared__ uint32_t pooled_keys[kPickStaged];
   __shared__ uint32_t hist[2048];
   __shared__ uint32_t wave_sums[kSegThreads / 64][2];
   __shared__ uint32_t found[2];
@@ -493,13 +499,27 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
   const int64_t position_start = position_starts[s];
   const uint32_t per = (n + kSegThreads - 1) / kSegThreads;
   const uint32_t lo = min(n, threadIdx.x * per), hi = min(n, lo + per);
+  const bool staged = n <= kPickStaged;  // uniform
+  if (staged) {
+    for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
+      const float r = raw[begin + i], q = pooled[begin + i];
+      raw_keys[i] = float_key(r);
+      pooled_keys[i] = float_key(q);
+    }
+    __syncthreads();
+  }
+  auto raw_key = [&](uint32_t i) { return staged ? raw_keys[i] : float_key(raw[begin + i]); };
+  auto pooled_key = [&](uint32_t i) {
+    return staged ? pooled_keys[i] : float_key(pooled[begin + i]);
+  };
 
   // raw picks in index order
+  const uint32_t threshold = states[3].prefix, take = take_equal[s];
+  uint32_t raw_seen;  // keys equal to the threshold before this thread's run
   {
-    const uint32_t threshold = states[3].prefix, take = take_equal[s];
     uint32_t lt = 0, eq = 0;
     for (uint32_t i = lo; i < hi; ++i) {
-      const uint32_t key = float_key(raw[begin + i]);
+      const uint32_t key = raw_key(i);
       lt += key < threshold;
       eq += key == threshold;
     }
@@ -507,22 +527,21 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
     block_scan_pair<kSegThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
     uint32_t rank = lt_before + min(take, eq_before);
     uint32_t seen = eq_before;
+    raw_seen = eq_before;
     for (uint32_t i = lo; i < hi; ++i) {
-      const uint32_t key = float_key(raw[begin + i]);
+      const uint32_t key = raw_key(i);
       bool picked = key < threshold;
       if (key == threshold) picked = seen++ < take;
-      raw_flags[begin + i] = picked;  // read back below by this same thread only
       if (picked) run_keys[offset + rank++] = key;
     }
   }
 
   // pooled picks: bottom-quota of the segment's pooled keys, in index order
   uint32_t pthreshold, ptake;
-  block_select(n, quota, [&](uint32_t i) { return float_key(pooled[begin + i]); }, hist,
-               wave_sums, found, pthreshold, ptake);
+  block_select(n, quota, pooled_key, hist, wave_sums, found, pthreshold, ptake);
   uint32_t lt = 0, eq = 0;
   for (uint32_t i = lo; i < hi; ++i) {
-    const uint32_t key = float_key(pooled[begin + i]);
+    const uint32_t key = pooled_key(i);
     lt += key < pthreshold;
     eq += key == pthreshold;
   }
@@ -531,7 +550,11 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
   uint32_t rank = lt_before + min(ptake, eq_before);
   uint32_t seen = eq_before, moved = 0;
   for (uint32_t i = lo; i < hi; ++i) {
-    const uint32_t key = float_key(pooled[begin + i]);
+    // the raw rule again, in the same order as above, tells whether slot i was a raw pick
+    const uint32_t rkey = raw_key(i);
+    bool raw_picked = rkey < threshold;
+    if (rkey == threshold) raw_picked = raw_seen++ < take;
+    const uint32_t key = pooled_key(i);
     bool picked = key < pthreshold;
     if (key == pthreshold) picked = seen++ < ptake;
     if (picked) {
@@ -539,7 +562,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
       refined_local[offset + rank] = i;
       removed_positions[offset + rank] = position_start + i;
       ++rank;
-      moved += raw_flags[begin + i] ? 0u : 1u;
+      moved += raw_picked ? 0u : 1u;
     }
   }
   uint32_t moved_before, unused, moved_total, unused_total;
@@ -691,7 +714,6 @@ struct SelectWorkspace {
   uint32_t* seg_less;
   uint32_t* seg_equal;
   uint32_t* take_equal;
-  uint8_t* raw_flags;
   uint32_t *run_keys, *run_slots, *refined_keys, *refined_local, *tmp_keys, *tmp_values;
   uint32_t* segment_of;
   size_t bytes;
@@ -712,7 +734,6 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
   w.seg_less = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.seg_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.take_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
-  w.raw_flags = reinterpret_cast<uint8_t*>(take(total));
   w.run_keys = reinterpret_cast<uint32_t*>(take(count * 4));
   w.run_slots = reinterpret_cast<uint32_t*>(take(count * 4));
   w.refined_keys = reinterpret_cast<uint32_t*>(take(count * 4));
@@ -742,7 +763,7 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
   if (int rc = check_launch("segment_count")) return rc;
   segment_pick_kernel<<<segments, kSegThreads, 0, s>>>(
       raw, pooled, segment_ends, position_starts, w.states, w.take_equal, quotas, offsets,
-      w.raw_flags, w.run_keys, w.refined_keys, w.refined_local, removed_positions, changed);
+      w.run_keys, w.refined_keys, w.refined_local, removed_positions, changed);
   return check_launch("segment_pick");
 }
 
