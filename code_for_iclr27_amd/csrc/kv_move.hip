@@ -124,10 +124,12 @@ __device__ __forceinline__ void copy_batch(const RowBatch<kTwo>& b, int64_t chun
 // sorted removal list `removed` land at out_start + d0... Output d takes input d + j,
 // j = #{i : removed[i] - i <= d} (the gather rule of csrc/scoring.cu:164-188). The block first
 // maps each of its n <= kCompactRows output rows to its source by binary search over the
-// removal list (staged in LDS when it fits), copying the positions on the way; then its lane
-// groups copy the rows in batches. Called by every thread of the block (it has barriers).
-constexpr int kCompactRows = 256;     // most output rows per block
+// removal list (staged in LDS when it fits), one row per thread, copying the positions on the
+// way; then its lane groups copy the rows in batches. Called by every thread of the block (it
+// has barriers).
+constexpr int kCompactRows = 128;     // most output rows per block (measured faster than 256)
 constexpr int kCompactStaged = 4096;  // removal entries staged in LDS (larger lists: global)
+static_assert(kCompactRows <= kThreads, "one thread maps each output row of a block");
 
 template <int G>
 __device__ __forceinline__ void compact_block(const uint8_t* keys, const uint8_t* values,
@@ -583,7 +585,9 @@ extern "C" int lr_merge(const void* keys, const void* values, const float* posit
   LR_REQUIRE(mapping && out_keys && out_values && out_positions, "Expected contiguous CUDA tensor");
   const int64_t row_bytes = dim * elem_bytes;
   const int g = granule_for(row_bytes, {keys, values, recalled, out_keys, out_values});
-  const RowLayout layout = make_layout(row_bytes, g, out_rows, 8);
+  // one batch per lane group: each batch waits for its mapping entries, so more, shorter lane
+  // groups keep more rows in flight (measured faster than two or four batches per group)
+  const RowLayout layout = make_layout(row_bytes, g, out_rows, kBatch);
   const int64_t blocks = blocks_for(layout, out_rows);
   return dispatch_granule(g, [&]<int G>() {
     gather_kernel<G, kMerge><<<blocks, kThreads, 0, as_stream(stream)>>>(
