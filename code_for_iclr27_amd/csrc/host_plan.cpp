@@ -318,7 +318,8 @@ struct StepSync {
 // `mark` (None or a callable) is called with a stage name after each stage's launches and with
 // "start" before the first (then the scorer is launched stage by stage), for event timing.
 // `sync` (or None) receives the quota copy and its event between the selection and the
-// compaction (StepSync above).
+// compaction (StepSync above). `stream_handle` must be torch's current stream on the layers'
+// device: the kernels go to it, and the quota copy and the event go to torch's current stream.
 py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        const std::vector<torch::Tensor>& values,
                        const std::vector<torch::Tensor>& positions,
