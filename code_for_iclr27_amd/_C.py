@@ -9,7 +9,7 @@ stream. There is no CPU path: CPU tensors are rejected exactly as the reference 
 
 from __future__ import annotations
 
-from typing import List, Sequence
+from typing import List
 
 import numpy as np
 import torch

@@ -14,7 +14,7 @@ from __future__ import annotations
 
 from collections.abc import Sequence
 from dataclasses import dataclass
-from typing import List, Optional, Sequence as Seq
+from typing import Optional, Sequence as Seq
 
 import numpy as np
 import torch

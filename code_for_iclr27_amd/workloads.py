@@ -13,10 +13,9 @@ T-W..T-1; margin gradient |N(0,1)| (cfg4: lognormal(0, 1.5)); base margin 2.0.
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
-import numpy as np
 import torch
 
 from .scoring import LayerState

@@ -2,7 +2,6 @@
 checks reject bad calls on the host (no GPU needed, nothing is launched); the torch mirror
 modules expose the reference's function names and reject CPU tensors like the reference."""
 
-import ctypes
 import re
 from pathlib import Path
 

@@ -14,7 +14,6 @@ import math
 from fractions import Fraction
 
 import numpy as np
-import pytest
 import torch
 import torch.nn.functional as F
 
