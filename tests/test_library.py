@@ -92,3 +92,12 @@ def test_host_planner_validates_like_the_reference():
         scoring.plan_segments([])
     with pytest.raises(RuntimeError, match="Query heads must be a multiple of KV heads"):
         scoring.plan_segments([layer(head_lens=[3, 3, 2])])
+
+
+def test_step_sync_requires_a_pending_step():
+    """The audit step's host wait object refuses a wait with no step posted (no GPU needed)."""
+    from code_for_iclr27_amd import scoring
+
+    sync = scoring._planner().StepSync()
+    with pytest.raises(RuntimeError, match="no audit step is pending"):
+        sync.wait(True)
