@@ -58,6 +58,9 @@ def parse_args():
                         help="skip the append / legacy / pack / cfg2 batch-append measurements")
     parser.add_argument("--other-configs", default="cfg0,cfg4",
                         help="comma-separated further audit configurations to time ('' for none)")
+    parser.add_argument("--event-every", type=int, default=5, metavar="K",
+                        help="inside the timed steps, bracket the dominant kernel with events on "
+                             "every K-th step (each event costs the GPU a few microseconds)")
     parser.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                         help="first run one plain elementwise copy (negation) of MIB MiB f32, "
                              "the reference dispatch for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -464,6 +467,7 @@ def main():
                         cfg.epsilon, queue_order=queue_order, timer=timer)
 
     def average_stages(timers):
+        timers = [timer for timer in timers if timer is not None]
         sums = {}
         for timer in timers:
             for name, us in timer.stages().items():
@@ -471,9 +475,9 @@ def main():
         return {name: total / len(timers) for name, total in sums.items()}
 
     def timed(steps, make_timer, queue_order=False):
-        timers = [make_timer() for _ in range(steps)]
+        timers = [make_timer(i) for i in range(steps)]
         for timer in timers:  # create the device events before the timed region
-            for event in timer.events:
+            for event in timer.events if timer is not None else ():
                 event.record()
         torch.cuda.synchronize()
         gc.collect()
@@ -492,14 +496,16 @@ def main():
         outcome = run()
     torch.cuda.synchronize()
     # stage breakdown (not the timed region): every stage bracketed by events
-    _, breakdown, _, _ = timed(max(3, min(args.steps, 10)), lambda: EventTimer(torch))
+    _, breakdown, _, _ = timed(max(3, min(args.steps, 10)), lambda i: EventTimer(torch))
     stages = average_stages(breakdown)
     order = list(stages)
     dominant = max(stages, key=stages.get)
     before = "start" if order.index(dominant) == 0 else order[order.index(dominant) - 1]
-    # timed region: K steps, events only around the dominant kernel
+    # timed region: K steps, events only around the dominant kernel, on every event_every-th
+    # step (the kernel's average launch time comes from those steps)
+    every = max(1, args.event_every)
     outcome, timers, elapsed, step_ms = timed(
-        args.steps, lambda: EventTimer(torch, only={before, dominant}))
+        args.steps, lambda i: EventTimer(torch, only={before, dominant}) if i % every == 0 else None)
     ms_per_step = elapsed * 1e3 / args.steps
     dominant_us = average_stages(timers)[dominant]
     # the same step with the eviction-queue order computed too (it is empty here: every
@@ -507,7 +513,7 @@ def main():
     queue_steps = max(3, min(args.steps, 20))
     for _ in range(3):
         run(queue_order=True)
-    _, _, queue_elapsed, _ = timed(queue_steps, lambda: EventTimer(torch, only=set()), True)
+    _, _, queue_elapsed, _ = timed(queue_steps, lambda i: None, True)
     rows_total = sum(layer.keys.size(0) for layer in layers)
     candidates = int(outcome.scores.numel())
     segments = len(outcome.segments)
@@ -554,6 +560,7 @@ def main():
         "algorithmic_bytes": nbytes,
         "stages_us": {k: round(v, 1) for k, v in stages.items()},
         "dominant_kernel_us": round(dominant_us, 1),
+        "dominant_kernel_samples": sum(timer is not None for timer in timers),
         "queue_order_ms_per_step": round(queue_elapsed * 1e3 / queue_steps, 4),
         "step_ms_min_median_max": [round(float(np.min(step_ms)), 3), round(float(np.median(step_ms)), 3),
                                    round(float(np.max(step_ms)), 3)],
