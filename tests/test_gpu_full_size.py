@@ -1,0 +1,173 @@
+"""GPU checks at the benchmark's full sizes (BASELINE's configurations).
+
+The audit step runs whole at cfg0, cfg1 and cfg4. Every stage after the scorer is checked
+exactly against the oracle fed the GPU's own scores (Pool7, the selection, the compaction of
+sampled layers), and the whole step through properties that do not depend on size:
+  - scores finite and non-negative (a Bernoulli KL);
+  - per-segment quotas sum to the evicted count, each within its candidate range;
+  - every head keeps its length minus its quota, and the packed output holds all kept rows;
+  - each compacted head keeps its positions strictly increasing.
+The scorer's own parity at these sizes is checked on sampled heads (cfg0, cfg1) against the
+oracle fed the GPU's logits, rtol 1e-5 as in the scorer tests. cfg2's batch append and cfg3's
+reinsertion merge run one full-size layer bit-exactly against the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from code_for_iclr27_amd import _C, audit, planning, scoring, workloads
+from oracle import kv_ops
+from oracle import scoring as oscoring
+from oracle import selection as oselection
+
+pytestmark = pytest.mark.gpu
+
+
+def to_np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg0", "cfg4"])
+def test_audit_step_full_size(device, name):
+    cfg = workloads.CONFIGS[name]
+    print(f"full-size audit step {name}", flush=True)
+    layers, qpos, margin = workloads.make_audit(cfg, device, seed=7, generator_device="cuda")
+    outcome = audit.AuditStep().run(layers, qpos, margin, cfg.count, cfg.protect_recent,
+                                    cfg.pool_kernel, cfg.epsilon)
+    torch.cuda.synchronize()
+    raw = outcome.scores.cpu().numpy()
+    assert np.isfinite(raw).all() and (raw >= 0).all()
+
+    ends = np.asarray(outcome.cumulative_ends)
+    bounds = np.concatenate(([0], ends))
+    pooled = kv_ops.pool(raw, bounds, cfg.pool_kernel)
+    np.testing.assert_array_equal(outcome.pooled.cpu().numpy(), pooled)
+
+    starts = [s.position_start for s in outcome.segments]
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, cfg.count)
+    quotas = outcome.selection.quotas.cpu().numpy()
+    np.testing.assert_array_equal(quotas, expect.quotas)
+    assert quotas.sum() == cfg.count
+    assert np.all(quotas <= np.diff(bounds))
+
+    coords = [(s.layer, s.head) for s in outcome.segments]
+    removed = expect.groups(coords)
+    for layer_index, layer in enumerate(layers):
+        kept = [n - len(removed.get((layer_index, h), ())) for h, n in enumerate(layer.head_lens)]
+        assert outcome.head_lens[layer_index] == kept
+        got = outcome.layers[layer_index]
+        assert got.keys.shape[0] == sum(kept)
+        positions = got.positions.cpu().numpy().reshape(-1)
+        start = 0
+        for n in kept:
+            assert np.all(np.diff(positions[start:start + n]) > 0)
+            start += n
+    assert sum(map(sum, outcome.head_lens)) == sum(map(sum, (l.head_lens for l in layers))) - cfg.count
+
+    for layer_index in sorted({0, len(layers) // 2, len(layers) - 1}):
+        layer = layers[layer_index]
+        head_bounds = np.concatenate(([0], np.cumsum(layer.head_lens)))
+        rows = np.sort(np.concatenate(
+            [head_bounds[h] + np.asarray(removed.get((layer_index, h), []), dtype=np.int64)
+             for h in range(len(layer.head_lens))])).astype(np.int64)
+        ek, ev, ep = kv_ops.compact(bits(layer.keys), bits(layer.values),
+                                    layer.positions.cpu().numpy(), rows)
+        got = outcome.layers[layer_index]
+        np.testing.assert_array_equal(bits(got.keys), ek)
+        np.testing.assert_array_equal(bits(got.values), ev)
+        np.testing.assert_array_equal(got.positions.cpu().numpy(), ep.reshape(-1))
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg0"])
+def test_fused_scores_full_size_sampled_heads(device, name):
+    """Sampled heads of a full-size score table against the oracle fed the GPU's logits."""
+    cfg = workloads.CONFIGS[name]
+    print(f"full-size scores {name}", flush=True)
+    layers, qpos, margin = workloads.make_audit(cfg, device, seed=9, generator_device="cuda")
+    plan = scoring.plan_segments(layers, protect_prompt=True, protect_recent=cfg.protect_recent)
+    scores = to_np(scoring.score_plan(plan, qpos, margin))
+    offsets = np.concatenate(([0], np.cumsum([s.count for s in plan.segments])))
+    groups = cfg.groups
+    for segment in (0, len(plan.segments) // 2 + 3, len(plan.segments) - 1):
+        seg = plan.segments[segment]
+        layer = layers[seg.layer]
+        start = plan.head_starts[segment]
+        length = int(plan.table[segment, 5])
+        logits = np.transpose(to_np(scoring.debug_segment_logits(plan, segment, device)), (1, 0, 2))
+        q = to_np(layer.queries[seg.head * groups:(seg.head + 1) * groups]).transpose(1, 0, 2)
+        expect = oscoring.head_scores(
+            q, qpos.cpu().numpy(), to_np(layer.keys[start:start + length]),
+            to_np(layer.positions[start:start + length]), to_np(layer.values[start:start + length]),
+            seg.position_start, seg.position_start + seg.count,
+            to_np(layer.gradient[seg.head * groups:(seg.head + 1) * groups]),
+            np.float32(cfg.margin), cfg.epsilon, logits=logits)
+        np.testing.assert_allclose(scores[offsets[segment]:offsets[segment + 1]], expect,
+                                   rtol=1e-5, atol=1e-12, err_msg=f"{name} segment {segment}")
+
+
+def test_batch_append_full_size(device):
+    """One cfg2 layer: 8 requests x 8 heads, U[1500, 2250] rows per head, bit-exact."""
+    heads, dim, requests = 8, 128, 8
+    rng = np.random.default_rng(12)
+    lengths = [list(rng.integers(1500, 2251, heads)) for _ in range(requests)]
+    gen = torch.Generator(device=device).manual_seed(12)
+    keys = [torch.randn((int(sum(l)), dim), generator=gen, device=device).to(torch.bfloat16)
+            for l in lengths]
+    values = [torch.randn((int(sum(l)), dim), generator=gen, device=device).to(torch.bfloat16)
+              for l in lengths]
+    positions = [torch.arange(int(sum(l)), device=device, dtype=torch.float32)[:, None] for l in lengths]
+    nk = torch.randn((requests, heads, 1, dim), generator=gen, device=device).to(torch.bfloat16)
+    nv = torch.randn((requests, heads, 1, dim), generator=gen, device=device).to(torch.bfloat16)
+    logical = [2250 + r for r in range(requests)]
+    pk, pv, pp = _C.batch_append(keys, values, positions, nk, nv, lengths, logical)
+    ek, ev, ep = kv_ops.batch_append([bits(k) for k in keys], [bits(v) for v in values],
+                                     [p.cpu().numpy() for p in positions], bits(nk), bits(nv),
+                                     lengths, logical)
+    np.testing.assert_array_equal(bits(pk), ek)
+    np.testing.assert_array_equal(bits(pv), ev)
+    np.testing.assert_array_equal(pp.cpu().numpy(), ep)
+
+
+def test_reinsert_merge_full_size(device):
+    """One cfg3 layer: 8 heads x 33,792 rows plus 512 recalled per head, bit-exact, with the
+    merged positions of every head strictly increasing."""
+    heads, dim, per_head, recalled_per_head = 8, 128, 33792, 512
+    rng = np.random.default_rng(13)
+    old_pos, meta = [], []
+    for h in range(heads):
+        universe = np.sort(rng.choice(per_head + 4096, per_head + recalled_per_head, replace=False))
+        recalled = rng.choice(universe.size, recalled_per_head, replace=False)
+        keep = np.ones(universe.size, bool)
+        keep[recalled] = False
+        old_pos.append(universe[keep])
+        meta.extend((5, h, p) for p in universe[~keep])
+    old_pos = np.concatenate(old_pos)
+    meta = np.asarray(meta, dtype=np.int64)[rng.permutation(len(meta))]
+    mapping, lengths = planning.merge_plan(old_pos, [per_head] * heads, meta)
+    oracle_mapping, oracle_lengths = kv_ops.merge_plan(old_pos, [per_head] * heads, meta)
+    np.testing.assert_array_equal(mapping, oracle_mapping)
+    assert list(lengths) == list(oracle_lengths)
+    gen = torch.Generator(device=device).manual_seed(13)
+    keys = torch.randn((old_pos.size, dim), generator=gen, device=device).to(torch.bfloat16)
+    values = torch.randn((old_pos.size, dim), generator=gen, device=device).to(torch.bfloat16)
+    positions = torch.from_numpy(old_pos.astype(np.float32)).to(device)[:, None]
+    recalled = torch.randn((len(meta), 2, dim), generator=gen, device=device).to(torch.bfloat16)
+    recalled_pos = torch.from_numpy(meta[:, 2].astype(np.float32)).to(device)
+    got = _C.merge(keys, values, positions, recalled, recalled_pos,
+                   torch.from_numpy(np.asarray(mapping)).to(device))
+    expect = kv_ops.merge(bits(keys), bits(values), old_pos.astype(np.float32), bits(recalled),
+                          meta[:, 2].astype(np.float32), np.asarray(mapping))
+    np.testing.assert_array_equal(bits(got[0]), expect[0])
+    np.testing.assert_array_equal(bits(got[1]), expect[1])
+    np.testing.assert_array_equal(got[2].cpu().numpy(), expect[2])
+    merged = got[2].cpu().numpy().reshape(-1)
+    start = 0
+    for n in lengths:
+        assert n == per_head + recalled_per_head
+        assert np.all(np.diff(merged[start:start + n]) > 0)
+        start += n
