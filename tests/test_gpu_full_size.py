@@ -7,7 +7,8 @@ sampled layers), and the whole step through properties that do not depend on siz
   - per-segment quotas sum to the evicted count, each within its candidate range;
   - every head keeps its length minus its quota, and the packed output holds all kept rows;
   - each compacted head keeps its positions strictly increasing.
-The scorer's own parity at these sizes is checked on sampled heads (cfg0, cfg1) against the
+The eviction-queue order is checked exactly at cfg1 and cfg4 (where some segments hold more
+than the in-LDS sort's 1024 picks). The scorer's own parity at these sizes is checked on sampled heads (cfg0, cfg1) against the
 oracle fed the GPU's logits, rtol 1e-5 as in the scorer tests. cfg2's batch append and cfg3's
 reinsertion merge run one full-size layer bit-exactly against the oracle.
 """
@@ -81,6 +82,27 @@ def test_audit_step_full_size(device, name):
         np.testing.assert_array_equal(bits(got.keys), ek)
         np.testing.assert_array_equal(bits(got.values), ev)
         np.testing.assert_array_equal(got.positions.cpu().numpy(), ep.reshape(-1))
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg4"])
+def test_queue_order_full_size(device, name):
+    """The eviction-queue order (values, segments, transplanted positions of refine_arrays) at
+    full size, bit-exact against the oracle on the GPU's scores."""
+    cfg = workloads.CONFIGS[name]
+    print(f"full-size queue order {name}", flush=True)
+    layers, qpos, margin = workloads.make_audit(cfg, device, seed=8, generator_device="cuda")
+    outcome = audit.AuditStep().run(layers, qpos, margin, cfg.count, cfg.protect_recent,
+                                    cfg.pool_kernel, cfg.epsilon, queue_order=True)
+    queue = outcome.selection.references()
+    raw = outcome.scores.cpu().numpy()
+    ends = np.asarray(outcome.cumulative_ends)
+    pooled = kv_ops.pool(raw, np.concatenate(([0], ends)), cfg.pool_kernel)
+    starts = [s.position_start for s in outcome.segments]
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, cfg.count)
+    np.testing.assert_array_equal(queue.scores, expect.values)
+    np.testing.assert_array_equal(queue.segments, expect.segments)
+    np.testing.assert_array_equal(queue.positions, expect.positions)
+    assert np.all(np.diff(queue.scores) >= 0)
 
 
 @pytest.mark.parametrize("name", ["cfg1", "cfg0"])
