@@ -474,7 +474,11 @@ def main():
                 sums[name] = sums.get(name, 0.0) + us
         return {name: total / len(timers) for name, total in sums.items()}
 
-    def timed(steps, make_timer, queue_order=False):
+    def timed(steps, make_timer, queue_order=False, warmup=0):
+        """`warmup` untimed steps, then `steps` timed ones between two synchronisations. The
+        garbage collector runs before the warm-up steps and is off until the end: a collection
+        right before the first timed step leaves the host's caches cold, which made that step's
+        host work (0.35-0.55 ms) several times slower than in the following steps."""
         timers = [make_timer(i) for i in range(steps)]
         for timer in timers:  # create the device events before the timed region
             for event in timer.events if timer is not None else ():
@@ -482,6 +486,9 @@ def main():
         torch.cuda.synchronize()
         gc.collect()
         gc.disable()
+        for _ in range(warmup):
+            run(None, queue_order)
+        torch.cuda.synchronize()
         started = time.perf_counter()
         ends = []
         for timer in timers:
@@ -492,11 +499,8 @@ def main():
         gc.enable()
         return outcome, timers, elapsed, np.diff([started] + ends) * 1e3
 
-    for _ in range(args.warmup):
-        outcome = run()
-    torch.cuda.synchronize()
     # stage breakdown (not the timed region): every stage bracketed by events
-    _, breakdown, _, _ = timed(max(3, min(args.steps, 10)), lambda i: EventTimer(torch))
+    _, breakdown, _, _ = timed(max(3, min(args.steps, 10)), lambda i: EventTimer(torch), warmup=3)
     stages = average_stages(breakdown)
     order = list(stages)
     dominant = max(stages, key=stages.get)
@@ -505,15 +509,14 @@ def main():
     # step (the kernel's average launch time comes from those steps)
     every = max(1, args.event_every)
     outcome, timers, elapsed, step_ms = timed(
-        args.steps, lambda i: EventTimer(torch, only={before, dominant}) if i % every == 0 else None)
+        args.steps, lambda i: EventTimer(torch, only={before, dominant}) if i % every == 0 else None,
+        warmup=args.warmup)
     ms_per_step = elapsed * 1e3 / args.steps
     dominant_us = average_stages(timers)[dominant]
     # the same step with the eviction-queue order computed too (it is empty here: every
     # selected slot is removed at once, so the removal sets do not depend on it)
     queue_steps = max(3, min(args.steps, 20))
-    for _ in range(3):
-        run(queue_order=True)
-    _, _, queue_elapsed, _ = timed(queue_steps, lambda i: None, True)
+    _, _, queue_elapsed, _ = timed(queue_steps, lambda i: None, True, warmup=3)
     rows_total = sum(layer.keys.size(0) for layer in layers)
     candidates = int(outcome.scores.numel())
     segments = len(outcome.segments)
