@@ -56,6 +56,9 @@ SIGNATURES = {
     "lr_select_refine_sets": [_P, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
+    "lr_staging_alloc": [_SZ, _P],
+    "lr_staging_free": [_P],
+    "lr_copy_words": [_P, _P, _I64, _P],
 }
 _RESTYPES = {"lr_last_error": ctypes.c_char_p, "lr_score_workspace_bytes": ctypes.c_size_t,
              "lr_select_workspace_bytes": ctypes.c_size_t}

@@ -49,7 +49,8 @@ def _native_planner():
         planner.bind_library(address("lr_score_workspace_bytes"), address("lr_score_segments"),
                              address("lr_pool"), address("lr_select_workspace_bytes"),
                              address("lr_select_refine_sets"), address("lr_compact_heads"),
-                             address("lr_last_error"))
+                             address("lr_last_error"), address("lr_staging_alloc"),
+                             address("lr_staging_free"), address("lr_copy_words"))
         _bound = True
     return planner
 

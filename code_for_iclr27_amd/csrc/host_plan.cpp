@@ -216,6 +216,9 @@ struct Library {
   decltype(&lr_select_refine_sets) select_refine_sets = nullptr;
   decltype(&lr_compact_heads) compact_heads = nullptr;
   decltype(&lr_last_error) last_error = nullptr;
+  decltype(&lr_staging_alloc) staging_alloc = nullptr;
+  decltype(&lr_staging_free) staging_free = nullptr;
+  decltype(&lr_copy_words) copy_words = nullptr;
 };
 Library library;
 
@@ -227,7 +230,8 @@ void bind_one(F& slot, int64_t address) {
 
 void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t pool,
                   int64_t select_workspace_bytes, int64_t select_refine_sets,
-                  int64_t compact_heads, int64_t last_error) {
+                  int64_t compact_heads, int64_t last_error, int64_t staging_alloc,
+                  int64_t staging_free, int64_t copy_words) {
   bind_one(library.score_workspace_bytes, score_workspace_bytes);
   bind_one(library.score_segments, score_segments);
   bind_one(library.pool, pool);
@@ -235,6 +239,9 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
   bind_one(library.select_refine_sets, select_refine_sets);
   bind_one(library.compact_heads, compact_heads);
   bind_one(library.last_error, last_error);
+  bind_one(library.staging_alloc, staging_alloc);
+  bind_one(library.staging_free, staging_free);
+  bind_one(library.copy_words, copy_words);
 }
 
 void check_call(int status) {
@@ -243,18 +250,60 @@ void check_call(int status) {
 
 inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 
-// The host's one wait of an audit step. The per-segment quotas and the non-finite score count
-// are final once the selection kernels are done, so audit_launch copies them into pinned
-// memory and records `ready` right after the selection, before it enqueues the compaction;
-// wait() blocks on that event only and builds the new ragged layout while the compaction still
+// The host side of an audit step's two copies and its one wait.
+//  - upload(): the metadata block goes through this object's pinned, host-coherent staging
+//    buffer and a copy kernel (lr_copy_words) on the step's stream, so the upload costs one small
+//    kernel between the previous work and the step's first kernel, not a copy-engine round trip
+//    (measured ~19 us of idle GPU between two steps). The staging buffer is rewritten only after
+//    the previous copy kernel has finished (`uploaded`).
+//  - post(): the per-segment quotas and the non-finite score count are final once the selection
+//    kernels are done, so they are copied into pinned memory and `ready` is recorded right
+//    after the selection, before the compaction is enqueued.
+// wait() blocks on `ready` only and builds the new ragged layout while the compaction still
 // runs. One object serves one step at a time (an AuditStep keeps one per device); each step's
 // wait() must return before the next audit_launch with the same object.
 struct StepSync {
+  c10::Event uploaded{c10::DeviceType::CUDA};
+  bool upload_pending = false;
+  void* staging = nullptr;
+  size_t staging_bytes = 0;
   c10::Event ready{c10::DeviceType::CUDA};
   torch::Tensor host_info;                          // pinned int64 [segments + 1]
   std::vector<int64_t> slot_segment, slot_length;   // per (layer, head): segment or -1, length
   int64_t layers = 0, heads = 0, segments = 0;
   bool pending = false;
+
+  StepSync() = default;
+  StepSync(const StepSync&) = delete;
+  StepSync& operator=(const StepSync&) = delete;
+  ~StepSync() {
+    if (staging == nullptr) return;
+    if (upload_pending) uploaded.synchronize();
+    library.staging_free(staging);
+  }
+
+  torch::Tensor upload(const torch::Tensor& words, const torch::Device& device, void* stream) {
+    const size_t bytes = static_cast<size_t>(words.numel()) * sizeof(int64_t);
+    if (upload_pending) {
+      uploaded.synchronize();  // normally long done: the previous step waited for its selection
+      upload_pending = false;
+    }
+    if (staging_bytes < bytes) {
+      if (staging != nullptr) check_call(library.staging_free(staging));
+      staging = nullptr;
+      staging_bytes = 0;
+      check_call(library.staging_alloc(bytes, &staging));
+      staging_bytes = bytes;
+    }
+    std::memcpy(staging, words.data_ptr<int64_t>(), bytes);
+    torch::Tensor block = torch::empty({words.numel()},
+                                       torch::TensorOptions().device(device).dtype(torch::kInt64));
+    check_call(library.copy_words(static_cast<const int64_t*>(staging), block.data_ptr<int64_t>(),
+                                  words.numel(), stream));
+    uploaded.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+    upload_pending = true;
+    return block;
+  }
 
   void post(const Plan& plan, const torch::Tensor& info, const torch::Device& device) {
     const int64_t words = plan.segments + 1;
@@ -333,8 +382,9 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        StepSync* sync) {
   require(library.score_segments != nullptr, "library entry points are not bound");
   require(pool_kernel > 0 && pool_kernel % 2 == 1, "pool kernel must be a positive odd integer");
+  // with a StepSync the block goes through its staging buffer, so it need not be pinned
   const Plan plan = make_plan(keys, values, positions, queries, gradients, head_lens, prompt_lens,
-                              true, protect_recent, true);
+                              true, protect_recent, /*pinned=*/sync == nullptr);
   const torch::Device device = keys[0].device();
   require(query_positions.is_cuda() && query_positions.device() == device &&
               query_positions.scalar_type() == torch::kInt64 && query_positions.is_contiguous() &&
@@ -346,7 +396,8 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
   const auto on_device = torch::TensorOptions().device(device);
   const int64_t S = plan.segments;
-  torch::Tensor block = plan.block.to(device, /*non_blocking=*/true);
+  torch::Tensor block = sync != nullptr ? sync->upload(plan.block, device, stream)
+                                        : plan.block.to(device, /*non_blocking=*/true);
   const int64_t* words = block.data_ptr<int64_t>();
   count = std::min(std::max<int64_t>(count, 0), plan.total);
 

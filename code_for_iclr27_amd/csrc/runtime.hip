@@ -1,5 +1,5 @@
-// Error state, ABI version and host-memory registration (module lazy_recall._host,
-// csrc/host.cpp:5-13 in the reference).
+// Error state, ABI version, host-memory registration (module lazy_recall._host,
+// csrc/host.cpp:5-13 in the reference) and the fused step's metadata staging.
 #include "lr_common.hpp"
 
 namespace lr {
@@ -48,4 +48,56 @@ extern "C" int lr_unregister_host(uint64_t address) {
     return LR_ERR_HIP;
   }
   return LR_OK;
+}
+
+// Pinned host memory that kernels read directly: fine-grained (coherent), so a kernel launched
+// after the host wrote it reads the written words.
+extern "C" int lr_staging_alloc(size_t bytes, void** host) {
+  lr::clear_error();
+  LR_REQUIRE(bytes > 0 && host != nullptr, "Invalid staging size");
+  *host = nullptr;
+  const hipError_t status = hipHostMalloc(host, bytes, hipHostMallocCoherent | hipHostMallocMapped);
+  if (status != hipSuccess) {
+    (void)hipGetLastError();
+    *host = nullptr;
+    lr::set_error(std::string("hipHostMalloc failed: ") + hipGetErrorString(status));
+    return LR_ERR_HIP;
+  }
+  return LR_OK;
+}
+
+extern "C" int lr_staging_free(void* host) {
+  lr::clear_error();
+  if (host == nullptr) return LR_OK;
+  const hipError_t status = hipHostFree(host);
+  if (status != hipSuccess) {
+    (void)hipGetLastError();
+    lr::set_error(std::string("hipHostFree failed: ") + hipGetErrorString(status));
+    return LR_ERR_HIP;
+  }
+  return LR_OK;
+}
+
+namespace lr {
+namespace {
+// One word per thread: every load is in flight at once (a host-memory read costs one bus round
+// trip), then every store.
+__global__ __launch_bounds__(256) void copy_words_kernel(const int64_t* __restrict__ source,
+                                                         int64_t* __restrict__ destination,
+                                                         int64_t words) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < words) destination[i] = source[i];
+}
+}  // namespace
+}  // namespace lr
+
+extern "C" int lr_copy_words(const int64_t* source, int64_t* destination, int64_t words,
+                             void* stream) {
+  lr::clear_error();
+  LR_REQUIRE(words >= 0 && words < (int64_t{1} << 31), "Invalid word count");
+  if (words == 0) return LR_OK;
+  LR_REQUIRE(source != nullptr && destination != nullptr, "Expected non-null buffers");
+  const unsigned blocks = static_cast<unsigned>((words + 255) / 256);
+  lr::copy_words_kernel<<<blocks, 256, 0, lr::as_stream(stream)>>>(source, destination, words);
+  return lr::check_launch("copy_words");
 }

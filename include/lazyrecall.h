@@ -238,6 +238,16 @@ int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* qu
                      int elem_bytes, int64_t max_length, int64_t total_out_rows,
                      void* out_keys, void* out_values, float* out_positions, void* stream);
 
+/* Staging of the fused step's metadata block (no reference counterpart: the reference copies
+ * each per-layer index list to the device with its own blocking copy). lr_staging_alloc gives
+ * `bytes` of pinned, host-coherent memory that kernels may read directly; lr_staging_free
+ * releases it (no kernel may still read it). lr_copy_words copies `words` 8-byte words from such
+ * memory (or from device memory) to device memory with a kernel on `stream`, so a small upload
+ * between two kernels needs no copy-engine round trip. */
+int lr_staging_alloc(size_t bytes, void** host);
+int lr_staging_free(void* host);
+int lr_copy_words(const int64_t* source, int64_t* destination, int64_t words, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
