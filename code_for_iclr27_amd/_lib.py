@@ -53,7 +53,8 @@ SIGNATURES = {
     "lr_select_workspace_bytes": [_I64, _I64, _I64],
     "lr_select_refine": [_P, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P, _P,
                          _P],
-    "lr_select_refine_sets": [_P, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P],
+    "lr_select_refine_sets": [_P, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P,
+                              _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
     "lr_staging_alloc": [_SZ, _P],

@@ -11,9 +11,10 @@ compaction launch per layer. Here the host builds one int64 metadata block (segm
 pool bounds, segment ends, head table), uploads it once from pinned memory, and enqueues:
 3 scoring kernels, 1 pool kernel, the selection kernels and 1 compaction kernel covering all
 layers. The only synchronisation is a wait for the per-segment quotas, which the host needs to
-describe the new ragged layout (as the reference's metadata rebuild does): they are copied to
-pinned memory with an event right after the selection, before the compaction is enqueued, so
-the host builds the layout (and enqueues the caller's next work) while the compaction runs. The
+describe the new ragged layout (as the reference's metadata rebuild does): the selection stores
+them into host-coherent memory, with an event right after the selection, before the compaction
+is enqueued, so the host builds the layout (and enqueues the caller's next work) while the
+compaction runs. The
 eviction-queue order (a per-segment sort and a merge of all segments' picks) is only needed
 for a non-empty lazy queue; on request it runs on a side stream while the compaction, which
 needs only the removal sets, runs on the current stream.

@@ -256,9 +256,10 @@ inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 //    kernel between the previous work and the step's first kernel, not a copy-engine round trip
 //    (measured ~19 us of idle GPU between two steps). The staging buffer is rewritten only after
 //    the previous copy kernel has finished (`uploaded`).
-//  - post(): the per-segment quotas and the non-finite score count are final once the selection
-//    kernels are done, so they are copied into pinned memory and `ready` is recorded right
-//    after the selection, before the compaction is enqueued.
+//  - info_buffer() / post(): the per-segment quotas and the non-finite score count are final
+//    once the selection kernels are done; the selection's plan workgroup writes them straight
+//    into this object's host-coherent `info` buffer (no copy), and post() records `ready`
+//    right after the selection, before the compaction is enqueued.
 // wait() blocks on `ready` only and builds the new ragged layout while the compaction still
 // runs. One object serves one step at a time (an AuditStep keeps one per device); each step's
 // wait() must return before the next audit_launch with the same object.
@@ -268,7 +269,8 @@ struct StepSync {
   void* staging = nullptr;
   size_t staging_bytes = 0;
   c10::Event ready{c10::DeviceType::CUDA};
-  torch::Tensor host_info;                          // pinned int64 [segments + 1]
+  int64_t* info = nullptr;  // host-coherent int64 [segments + 1], written by the device
+  size_t info_bytes = 0;
   std::vector<int64_t> slot_segment, slot_length;   // per (layer, head): segment or -1, length
   int64_t layers = 0, heads = 0, segments = 0;
   bool pending = false;
@@ -277,9 +279,27 @@ struct StepSync {
   StepSync(const StepSync&) = delete;
   StepSync& operator=(const StepSync&) = delete;
   ~StepSync() {
-    if (staging == nullptr) return;
     if (upload_pending) uploaded.synchronize();
-    library.staging_free(staging);
+    if (pending) ready.synchronize();
+    if (staging != nullptr) library.staging_free(staging);
+    if (info != nullptr) library.staging_free(info);
+  }
+
+  // The buffer the step's selection writes into. A step's wait() (or the destructor) has seen
+  // the previous writer finish before a new step gets it.
+  int64_t* info_buffer(int64_t words) {
+    require(!pending, "the previous audit step on this StepSync was not waited for");
+    const size_t bytes = static_cast<size_t>(words) * sizeof(int64_t);
+    if (info_bytes < bytes) {
+      if (info != nullptr) check_call(library.staging_free(info));
+      info = nullptr;
+      info_bytes = 0;
+      void* memory = nullptr;
+      check_call(library.staging_alloc(bytes, &memory));
+      info = static_cast<int64_t*>(memory);
+      info_bytes = bytes;
+    }
+    return info;
   }
 
   torch::Tensor upload(const torch::Tensor& words, const torch::Device& device, void* stream) {
@@ -305,11 +325,7 @@ struct StepSync {
     return block;
   }
 
-  void post(const Plan& plan, const torch::Tensor& info, const torch::Device& device) {
-    const int64_t words = plan.segments + 1;
-    if (!host_info.defined() || host_info.numel() < words)
-      host_info = torch::empty({words}, torch::dtype(torch::kInt64).pinned_memory(true));
-    host_info.narrow(0, 0, words).copy_(info, /*non_blocking=*/true);
+  void post(const Plan& plan, const torch::Device& device) {
     ready.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
     const int64_t* slot = plan.head_info.data_ptr<int64_t>();
     slot_segment.assign(slot, slot + plan.slots);
@@ -330,7 +346,6 @@ struct StepSync {
       py::gil_scoped_release release;
       ready.synchronize();
     }
-    const int64_t* info = host_info.data_ptr<int64_t>();
     int32_t bad = 0;
     std::memcpy(&bad, info + segments, sizeof(bad));
     if (check_finite && bad != 0)
@@ -448,9 +463,10 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
     check_call(library.select_refine_sets(
         raw, pooled, plan.total, words + plan.ends_at(), words + plan.starts_at(), S, count,
         dptr(select_ws), select_bytes, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
-        removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(), stream));
+        removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(),
+        sync != nullptr ? sync->info_buffer(S + 1) : nullptr, nonfinite, stream));
     stage("select");
-    if (sync != nullptr) sync->post(plan, info, device);
+    if (sync != nullptr) sync->post(plan, device);
     check_call(library.compact_heads(
         words + plan.heads_at(), plan.slots, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
         removed.data_ptr<int64_t>(), plan.dim, static_cast<int>(keys[0].element_size()),
@@ -458,7 +474,12 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
         out_positions.data_ptr<float>(), stream));
     stage("compact");
   } else {
-    if (sync != nullptr) sync->post(plan, info, device);
+    if (sync != nullptr) {
+      // no selection: the non-finite count (and zero quotas) go to the host buffer by a copy kernel
+      check_call(library.copy_words(info.data_ptr<int64_t>(), sync->info_buffer(S + 1), S + 1,
+                                    stream));
+      sync->post(plan, device);
+    }
     std::vector<torch::Tensor> flat_positions;
     for (const torch::Tensor& p : positions) flat_positions.push_back(p.reshape({-1}));
     out_keys.copy_(torch::cat(keys));

@@ -379,7 +379,8 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
     SelectState* __restrict__ states, const uint32_t* __restrict__ hist,
     uint32_t* __restrict__ seg_less, uint32_t* __restrict__ seg_equal,
     uint32_t* __restrict__ ticket, int64_t segments, uint32_t* __restrict__ take_equal,
-    int64_t* __restrict__ quotas, int64_t* __restrict__ offsets) {
+    int64_t* __restrict__ quotas, int64_t* __restrict__ offsets, int64_t* __restrict__ host_info,
+    const int32_t* __restrict__ nonfinite) {
   __shared__ uint32_t wave_sums[kSegThreads / 64][2];
   __shared__ uint32_t found[2];
   __shared__ bool last;
@@ -423,11 +424,15 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
       take_equal[t] = take;
       quotas[t] = quota;
       offsets[t] = quota_before;
+      if (host_info != nullptr) host_info[t] = quota;
     }
     carry_equal += eq_total;
     carry_quota += quota_total;
   }
-  if (threadIdx.x == 0) offsets[segments] = carry_quota;
+  if (threadIdx.x == 0) {
+    offsets[segments] = carry_quota;
+    if (host_info != nullptr) host_info[segments] = nonfinite != nullptr ? *nonfinite : 0;
+  }
 }
 
 // Radix select inside one workgroup: the k-th smallest (1-based) of the n keys key_at(i), by
@@ -748,7 +753,8 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
 int launch_sets(const float* raw, const float* pooled, int64_t total, const int64_t* segment_ends,
                 const int64_t* position_starts, int64_t segments, int64_t count,
                 const SelectWorkspace& w, int64_t* quotas, int64_t* offsets,
-                int64_t* removed_positions, int64_t* changed, hipStream_t s) {
+                int64_t* removed_positions, int64_t* changed, int64_t* host_info,
+                const int32_t* nonfinite, hipStream_t s) {
   select_init_kernel<<<1, 256, 0, s>>>(w.states, w.hist, w.ticket, static_cast<uint32_t>(count));
   if (int rc = check_launch("select_init")) return rc;
   const int64_t chunk = ceil_div(ceil_div(total, kHistBlocks), 1024) * 1024;
@@ -759,7 +765,8 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
   if (int rc = check_launch("select_pass")) return rc;
   segment_count_kernel<<<segments, kSegThreads, 0, s>>>(raw, segment_ends, w.states, w.hist,
                                                         w.seg_less, w.seg_equal, w.ticket,
-                                                        segments, w.take_equal, quotas, offsets);
+                                                        segments, w.take_equal, quotas, offsets,
+                                                        host_info, nonfinite);
   if (int rc = check_launch("segment_count")) return rc;
   segment_pick_kernel<<<segments, kSegThreads, 0, s>>>(
       raw, pooled, segment_ends, position_starts, w.states, w.take_equal, quotas, offsets,
@@ -812,7 +819,8 @@ extern "C" int lr_select_refine_sets(const float* raw, const float* pooled, int6
                                      const int64_t* segment_ends, const int64_t* position_starts,
                                      int64_t segments, int64_t count, void* workspace,
                                      size_t workspace_bytes, int64_t* quotas, int64_t* offsets,
-                                     int64_t* removed_positions, int64_t* changed, void* stream) {
+                                     int64_t* removed_positions, int64_t* changed,
+                                     int64_t* host_info, const int32_t* nonfinite, void* stream) {
   clear_error();
   LR_SELECT_CHECK_SHAPE();
   LR_REQUIRE(raw && pooled && segment_ends && position_starts && workspace && quotas && offsets &&
@@ -822,7 +830,7 @@ extern "C" int lr_select_refine_sets(const float* raw, const float* pooled, int6
   const SelectWorkspace w = carve(workspace, total, segments, count);
   LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
   return launch_sets(raw, pooled, total, segment_ends, position_starts, segments, count, w, quotas,
-                     offsets, removed_positions, changed, as_stream(stream));
+                     offsets, removed_positions, changed, host_info, nonfinite, as_stream(stream));
 }
 
 extern "C" int lr_select_refine_queue(const int64_t* position_starts, int64_t total,
@@ -851,7 +859,7 @@ extern "C" int lr_select_refine(const float* raw, const float* pooled, int64_t t
                                 void* stream) {
   if (int rc = lr_select_refine_sets(raw, pooled, total, segment_ends, position_starts, segments,
                                      count, workspace, workspace_bytes, quotas, offsets,
-                                     removed_positions, changed, stream))
+                                     removed_positions, changed, nullptr, nullptr, stream))
     return rc;
   return lr_select_refine_queue(position_starts, total, segments, count, workspace,
                                 workspace_bytes, quotas, offsets, out_values, out_segments,

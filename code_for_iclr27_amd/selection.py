@@ -153,7 +153,7 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
         _lib.call("lr_select_refine_sets", raw.data_ptr(), pooled.data_ptr(), total,
                   ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
                   buffer.data_ptr(), buffer.numel(), quotas.data_ptr(), offsets.data_ptr(),
-                  removed.data_ptr(), changed.data_ptr(), _lib.stream_of(raw))
+                  removed.data_ptr(), changed.data_ptr(), None, None, _lib.stream_of(raw))
         return DeviceSelection(None, None, None, quotas, offsets, removed, changed, coordinates)
     if queue_stream is None:
         _lib.call("lr_select_refine", raw.data_ptr(), pooled.data_ptr(), total,
@@ -167,7 +167,7 @@ def select_refine(raw: torch.Tensor, pooled: torch.Tensor, cumulative_ends: Seq[
     _lib.call("lr_select_refine_sets", raw.data_ptr(), pooled.data_ptr(), total,
               ends_device.data_ptr(), starts_device.data_ptr(), segments, count,
               buffer.data_ptr(), buffer.numel(), quotas.data_ptr(), offsets.data_ptr(),
-              removed.data_ptr(), changed.data_ptr(), current.cuda_stream)
+              removed.data_ptr(), changed.data_ptr(), None, None, current.cuda_stream)
     sets_done = torch.cuda.Event()
     sets_done.record(current)
     queue_stream.wait_event(sets_done)

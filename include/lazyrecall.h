@@ -213,12 +213,16 @@ int lr_select_refine(const float* raw, const float* pooled, int64_t total,
  * _sets: quotas, offsets, removed_positions and changed, as lr_select_refine.
  * _queue: out_values, out_segments, out_positions, as lr_select_refine; it reads what _sets
  * left in `workspace`, `quotas` and `offsets`, so it must be ordered after _sets (same stream,
- * or an event) with the same arguments, and before the workspace is reused. */
+ * or an event) with the same arguments, and before the workspace is reused.
+ * host_info (may be NULL): host-coherent memory (lr_staging_alloc) of segments + 1 int64
+ * words; _sets also writes the quotas there, and in word [segments] the i32 at `nonfinite`
+ * (device, may be NULL: 0), so a host that waits for _sets reads them without a copy. */
 int lr_select_refine_sets(const float* raw, const float* pooled, int64_t total,
                           const int64_t* segment_ends, const int64_t* position_starts,
                           int64_t segments, int64_t count, void* workspace,
                           size_t workspace_bytes, int64_t* quotas, int64_t* offsets,
-                          int64_t* removed_positions, int64_t* changed, void* stream);
+                          int64_t* removed_positions, int64_t* changed, int64_t* host_info,
+                          const int32_t* nonfinite, void* stream);
 int lr_select_refine_queue(const int64_t* position_starts, int64_t total, int64_t segments,
                            int64_t count, void* workspace, size_t workspace_bytes,
                            const int64_t* quotas, const int64_t* offsets, float* out_values,
@@ -242,8 +246,9 @@ int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* qu
  * each per-layer index list to the device with its own blocking copy). lr_staging_alloc gives
  * `bytes` of pinned, host-coherent memory that kernels may read directly; lr_staging_free
  * releases it (no kernel may still read it). lr_copy_words copies `words` 8-byte words from such
- * memory (or from device memory) to device memory with a kernel on `stream`, so a small upload
- * between two kernels needs no copy-engine round trip. */
+ * memory (or from device memory) to device memory, or from device memory to such host memory,
+ * with a kernel on `stream`, so a small copy between two kernels needs no copy-engine round
+ * trip. */
 int lr_staging_alloc(size_t bytes, void** host);
 int lr_staging_free(void* host);
 int lr_copy_words(const int64_t* source, int64_t* destination, int64_t words, void* stream);
