@@ -8,7 +8,8 @@ the immediate removal LazyRecallCache.remove_positions (cache.py:92-180) of ever
 The reference runs these as a Python loop of ~4 launches per (layer, head), per-segment
 torch.topk calls with device->host copies, host list -> tensor copies per layer and one
 compaction launch per layer. Here the host builds one int64 metadata block (segment table,
-pool bounds, segment ends, head table), uploads it once from pinned memory, and enqueues:
+pool bounds, segment ends, head table), uploads it once (a host-coherent staging buffer read by
+a copy kernel on the step's stream), and enqueues:
 3 scoring kernels, 1 pool kernel, the selection kernels and 1 compaction kernel covering all
 layers. The only synchronisation is a wait for the per-segment quotas, which the host needs to
 describe the new ragged layout (as the reference's metadata rebuild does): the selection stores
