@@ -11,6 +11,8 @@
 // key (-0.0 and +0.0 are one key; NaN sorts last).
 #include <utility>
 
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "lr_common.hpp"
 
 namespace lr {
@@ -612,8 +614,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(
     const int64_t* __restrict__ quotas, const int64_t* __restrict__ offsets,
     uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_slots,
     uint32_t* __restrict__ refined_keys, uint32_t* __restrict__ refined_local,
-    uint32_t* __restrict__ tmp_keys, uint32_t* __restrict__ tmp_values,
-    uint32_t* __restrict__ segment_of) {
+    uint32_t* __restrict__ tmp_keys, uint32_t* __restrict__ tmp_values) {
   __shared__ uint32_t lds_keys[kRankSortMax];
   __shared__ uint32_t lds_values[kRankSortMax];
   __shared__ SortLds<kSegThreads> sort_lds;
@@ -633,57 +634,22 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(
                                   tmp_keys + offset, tmp_values + offset, quota, sort_lds);
   }
   // Slot payload for the global order: position in the concatenated runs.
-  for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads) {
+  for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads)
     run_slots[offset + i] = static_cast<uint32_t>(offset + i);
-    segment_of[offset + i] = static_cast<uint32_t>(s);
-  }
 }
 
-// Global slot order by merging the per-segment runs. Runs are concatenated in segment
-// (= index) order and each is sorted by (key, index); at level l, blocks of 2^l consecutive
-// segments are merged pairwise. An element of a left block lands at its own rank plus the
-// number of partner keys strictly below it, a right-block element at its rank plus the
-// partner keys below or equal (left elements have the lower indices), so the merge is stable
-// and the final order is the (key, index) order of torch.topk(largest=False, sorted=True).
-__global__ __launch_bounds__(256) void merge_level_kernel(
-    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ slots_in,
-    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ slots_out,
-    const uint32_t* __restrict__ segment_of, const int64_t* __restrict__ offsets,
-    int64_t segments, int level, int64_t count) {
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (p >= count) return;
-  const int64_t block = segment_of[p] >> level;
-  const int64_t pair_first = (block >> 1) << (level + 1);
-  const int64_t mid_segment = pair_first + (int64_t{1} << level);
-  const int64_t end_segment = pair_first + (int64_t{2} << level);
-  const int64_t pair_begin = offsets[pair_first];
-  const int64_t mid = offsets[mid_segment < segments ? mid_segment : segments];
-  const int64_t pair_end = offsets[end_segment < segments ? end_segment : segments];
-  const uint32_t key = keys_in[p];
-  int64_t rank, lo, hi;
-  if (p < mid) {  // left block: partner = [mid, pair_end), count keys < key
-    rank = p - pair_begin;
-    lo = mid;
-    hi = pair_end;
-    while (lo < hi) {
-      const int64_t m = (lo + hi) >> 1;
-      if (keys_in[m] < key) lo = m + 1;
-      else hi = m;
-    }
-    rank += lo - mid;
-  } else {  // right block: partner = [pair_begin, mid), count keys <= key
-    rank = p - mid;
-    lo = pair_begin;
-    hi = mid;
-    while (lo < hi) {
-      const int64_t m = (lo + hi) >> 1;
-      if (keys_in[m] <= key) lo = m + 1;
-      else hi = m;
-    }
-    rank += lo - pair_begin;
-  }
-  keys_out[pair_begin + rank] = key;
-  slots_out[pair_begin + rank] = slots_in[p];
+// Global slot order: the runs are concatenated in segment (= index) order and each is sorted
+// by (key, index), so a stable radix sort of the concatenation by key alone gives the
+// (key, index) order of torch.topk(largest=False, sorted=True). It is rocPRIM's device radix
+// sort (a plain library sort of `count` key/slot pairs).
+size_t order_sort_bytes(int64_t count) {
+  size_t bytes = 0;
+  if (count > 0)
+    (void)rocprim::radix_sort_pairs(nullptr, bytes, static_cast<const uint32_t*>(nullptr),
+                                    static_cast<uint32_t*>(nullptr),
+                                    static_cast<const uint32_t*>(nullptr),
+                                    static_cast<uint32_t*>(nullptr), static_cast<size_t>(count));
+  return bytes;
 }
 
 // Slot j of the global order: its raw value, its segment, and the refined position that the
@@ -720,7 +686,8 @@ struct SelectWorkspace {
   uint32_t* seg_equal;
   uint32_t* take_equal;
   uint32_t *run_keys, *run_slots, *refined_keys, *refined_local, *tmp_keys, *tmp_values;
-  uint32_t* segment_of;
+  void* sort_storage;  // rocPRIM's temporary storage for the global order
+  size_t sort_bytes;
   size_t bytes;
 };
 
@@ -745,7 +712,8 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
   w.refined_local = reinterpret_cast<uint32_t*>(take(count * 4));
   w.tmp_keys = reinterpret_cast<uint32_t*>(take(count * 4));
   w.tmp_values = reinterpret_cast<uint32_t*>(take(count * 4));
-  w.segment_of = reinterpret_cast<uint32_t*>(take(count * 4));
+  w.sort_bytes = order_sort_bytes(count);
+  w.sort_storage = take(w.sort_bytes);
   w.bytes = off;
   return w;
 }
@@ -780,21 +748,19 @@ int launch_queue(const int64_t* position_starts, int64_t segments, int64_t count
                  hipStream_t s) {
   segment_sort_kernel<<<segments, kSegThreads, 0, s>>>(quotas, offsets, w.run_keys, w.run_slots,
                                                        w.refined_keys, w.refined_local,
-                                                       w.tmp_keys, w.tmp_values, w.segment_of);
+                                                       w.tmp_keys, w.tmp_values);
   if (int rc = check_launch("segment_sort")) return rc;
-  uint32_t* keys = w.run_keys;
-  uint32_t* slots = w.run_slots;
-  uint32_t* alt_keys = w.tmp_keys;
-  uint32_t* alt_slots = w.tmp_values;
-  for (int level = 0; (int64_t{1} << level) < segments; ++level) {
-    merge_level_kernel<<<ceil_div(count, 256), 256, 0, s>>>(keys, slots, alt_keys, alt_slots,
-                                                            w.segment_of, offsets, segments,
-                                                            level, count);
-    std::swap(keys, alt_keys);
-    std::swap(slots, alt_slots);
+  size_t sort_bytes = w.sort_bytes;
+  const hipError_t sorted = rocprim::radix_sort_pairs(
+      w.sort_storage, sort_bytes, static_cast<const uint32_t*>(w.run_keys), w.tmp_keys,
+      static_cast<const uint32_t*>(w.run_slots), w.tmp_values, static_cast<size_t>(count), 0u,
+      32u, s);
+  if (sorted != hipSuccess) {
+    (void)hipGetLastError();
+    set_error(std::string("queue order sort failed: ") + hipGetErrorString(sorted));
+    return LR_ERR_HIP;
   }
-  if (int rc = check_launch("merge_level")) return rc;
-  emit_kernel<<<ceil_div(count, 256), 256, 0, s>>>(keys, slots, offsets, segments,
+  emit_kernel<<<ceil_div(count, 256), 256, 0, s>>>(w.tmp_keys, w.tmp_values, offsets, segments,
                                                    position_starts, w.refined_local, count,
                                                    out_values, out_segments, out_positions);
   return check_launch("select_emit");
