@@ -19,6 +19,8 @@ namespace lr {
 namespace {
 
 constexpr int kSegThreads = 256;   // per-segment workgroups
+constexpr int kPickThreads = 512;  // segment_pick workgroups (measured faster than 256:
+                                   // cfg1 selection 50 -> 47 us, cfg4 108 -> 79 us)
 
 __device__ __forceinline__ uint32_t float_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -449,15 +451,15 @@ __device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_a
   auto pass = [&](auto pass_index) {
     constexpr PassShape shape = pass_shape(decltype(pass_index)::value);
     constexpr int BINS = 1 << shape.bits;
-    for (int i = threadIdx.x; i < BINS; i += kSegThreads) hist[i] = 0;
+    for (int i = threadIdx.x; i < BINS; i += kPickThreads) hist[i] = 0;
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
+    for (uint32_t i = threadIdx.x; i < n; i += kPickThreads) {
       const uint32_t key = key_at(i);
       if ((key & st.mask) == st.prefix) atomicAdd(&hist[(key >> shape.shift) & (BINS - 1)], 1u);
     }
     __syncthreads();
     uint32_t digit, below;
-    find_digit<BINS, kSegThreads>(hist, st.remaining, wave_sums, found, digit, below);
+    find_digit<BINS, kPickThreads>(hist, st.remaining, wave_sums, found, digit, below);
     st.prefix |= digit << shape.shift;
     st.mask |= static_cast<uint32_t>(BINS - 1) << shape.shift;
     st.remaining -= below;
@@ -481,7 +483,7 @@ __device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_a
 // segments read global memory in each pass.
 constexpr uint32_t kPickStaged = 4096;
 
-__global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
+__global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
     const float* __restrict__ raw, const float* __restrict__ pooled,
     const int64_t* __restrict__ ends, const int64_t* __restrict__ position_starts,
     const SelectState* __restrict__ states, const uint32_t* __restrict__ take_equal,
@@ -492,7 +494,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
   __shared__ uint32_t raw_keys[kPickStaged];
   __shared__ uint32_t pooled_keys[kPickStaged];
   __shared__ uint32_t hist[2048];
-  __shared__ uint32_t wave_sums[kSegThreads / 64][2];
+  __shared__ uint32_t wave_sums[kPickThreads / 64][2];
   __shared__ uint32_t found[2];
   const int64_t s = blockIdx.x;
   const uint32_t quota = static_cast<uint32_t>(quotas[s]);
@@ -504,11 +506,11 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
   const uint32_t n = static_cast<uint32_t>(end - begin);
   const int64_t offset = offsets[s];
   const int64_t position_start = position_starts[s];
-  const uint32_t per = (n + kSegThreads - 1) / kSegThreads;
+  const uint32_t per = (n + kPickThreads - 1) / kPickThreads;
   const uint32_t lo = min(n, threadIdx.x * per), hi = min(n, lo + per);
   const bool staged = n <= kPickStaged;  // uniform
   if (staged) {
-    for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
+    for (uint32_t i = threadIdx.x; i < n; i += kPickThreads) {
       const float r = raw[begin + i], q = pooled[begin + i];
       raw_keys[i] = float_key(r);
       pooled_keys[i] = float_key(q);
@@ -531,7 +533,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
       eq += key == threshold;
     }
     uint32_t lt_before, eq_before, lt_total, eq_total;
-    block_scan_pair<kSegThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
+    block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
     uint32_t rank = lt_before + min(take, eq_before);
     uint32_t seen = eq_before;
     raw_seen = eq_before;
@@ -553,7 +555,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
     eq += key == pthreshold;
   }
   uint32_t lt_before, eq_before, lt_total, eq_total;
-  block_scan_pair<kSegThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
+  block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
   uint32_t rank = lt_before + min(ptake, eq_before);
   uint32_t seen = eq_before, moved = 0;
   for (uint32_t i = lo; i < hi; ++i) {
@@ -573,7 +575,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_pick_kernel(
     }
   }
   uint32_t moved_before, unused, moved_total, unused_total;
-  block_scan_pair<kSegThreads>(moved, 0u, wave_sums, moved_before, unused, moved_total, unused_total);
+  block_scan_pair<kPickThreads>(moved, 0u, wave_sums, moved_before, unused, moved_total, unused_total);
   if (threadIdx.x == 0) changed[s] = moved_total;
 }
 
@@ -736,7 +738,7 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
                                                         segments, w.take_equal, quotas, offsets,
                                                         host_info, nonfinite);
   if (int rc = check_launch("segment_count")) return rc;
-  segment_pick_kernel<<<segments, kSegThreads, 0, s>>>(
+  segment_pick_kernel<<<segments, kPickThreads, 0, s>>>(
       raw, pooled, segment_ends, position_starts, w.states, w.take_equal, quotas, offsets,
       w.run_keys, w.refined_keys, w.refined_local, removed_positions, changed);
   return check_launch("segment_pick");
