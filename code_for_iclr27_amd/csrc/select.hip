@@ -302,13 +302,14 @@ __global__ __launch_bounds__(256) void select_init_kernel(SelectState* __restric
 }
 
 // Extends `st` (the state before pass `pass`) by that pass's digit, read from its histogram.
-template <int PASS>
+// All BLOCK threads of the workgroup call it.
+template <int PASS, int BLOCK>
 __device__ __forceinline__ SelectState extend_state(SelectState st, const uint32_t* __restrict__ hist,
                                                     uint32_t (*wave_sums)[2], uint32_t* found) {
   constexpr PassShape shape = pass_shape(PASS);
   uint32_t digit, below;
-  find_digit<1 << shape.bits, 256>(hist + PASS * kHistStride, st.remaining, wave_sums, found,
-                                   digit, below);
+  find_digit<1 << shape.bits, BLOCK>(hist + PASS * kHistStride, st.remaining, wave_sums, found,
+                                     digit, below);
   st.prefix |= digit << shape.shift;
   st.mask |= ((1u << shape.bits) - 1u) << shape.shift;
   st.less += below;
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(256) void select_pass_kernel(const float* __restric
   __shared__ uint32_t found[2];
   SelectState st = states[PASS == 0 ? 0 : PASS - 1];
   if constexpr (PASS > 0) {
-    st = extend_state<PASS - 1>(st, hist, wave_sums, found);
+    st = extend_state<PASS - 1, 256>(st, hist, wave_sums, found);
     if (blockIdx.x == 0 && threadIdx.x == 0) states[PASS] = st;
   }
   for (int i = threadIdx.x; i < BINS; i += 256) local[i] = 0;
@@ -388,7 +389,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
   __shared__ uint32_t wave_sums[kSegThreads / 64][2];
   __shared__ uint32_t found[2];
   __shared__ bool last;
-  const SelectState st = extend_state<2>(states[2], hist, wave_sums, found);
+  const SelectState st = extend_state<2, kSegThreads>(states[2], hist, wave_sums, found);
   if (blockIdx.x == 0 && threadIdx.x == 0) states[3] = st;
   const int64_t s = blockIdx.x;
   const int64_t begin = s == 0 ? 0 : ends[s - 1], end = ends[s];
