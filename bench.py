@@ -390,6 +390,39 @@ def ops_bench(torch, seed, reps=5):
         f"cfg2 layer: 8 requests x 8 heads, {n} rows (U[1500,2250] per head) + 1 token each",
         L, device, nbytes, wall)
     del req_k, req_v, req_p
+
+    # query history (history.py:21-38,51-63): one decode step's queries of all 32 layers
+    # (Hq 32, d128, bf16) into the device ring, one launch per step
+    from code_for_iclr27_amd.history import QueryHistory
+    Hq, W = 32, 250
+    history = QueryHistory(L, W)
+    step_queries = [[randn(1, Hq, 1, d) for _ in range(L)] for _ in range(2)]
+    clock = iter(range(1 << 40))
+    device, wall = measure(lambda: [
+        (lambda i=i: history.append(step_queries[i % 2], next(clock))) for i in range(2 * W)], 1)
+    nbytes = 3 * L * Hq * d * 2 + 2 * 8
+    out["history_append"] = _op_line("cfg1 decode step: 32 layers x 32 query heads x d128 into "
+                                     "the [32, 32, 500, 128] ring", 1, device, nbytes, wall)
+    # the audit's window: ring views here, versus the reference's per-layer torch.cat of W
+    # [1, Hq, 1, d] tensors plus a torch.tensor of the positions (history.py:51-63)
+    from collections import deque
+    deques = [deque((randn(1, Hq, 1, d) for _ in range(W)), maxlen=W) for _ in range(L)]
+    walls = {}
+    for name, gather in (
+            ("ring_views", lambda: history.audit_window()),
+            ("deque_cat", lambda: ([torch.cat(list(q), dim=2) for q in deques],
+                                   torch.tensor(list(range(W)), dtype=torch.long, device=dev)))):
+        gather()
+        times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            started = time.perf_counter()
+            gather()
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - started) * 1e3)
+        walls[name] = round(float(np.median(times)), 3)
+    out["history_append"]["audit_window_ms"] = walls
+    del history, step_queries, deques
     torch.cuda.empty_cache()
     return out
 

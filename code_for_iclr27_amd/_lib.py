@@ -19,6 +19,7 @@ LR_OK = 0
 LR_DTYPE_F32, LR_DTYPE_F64, LR_DTYPE_F16, LR_DTYPE_BF16 = 0, 1, 2, 3
 LR_SEG_WORDS = 12
 LR_HEAD_WORDS = 6
+LR_HISTORY_MAX_LAYERS = 128
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -57,6 +58,7 @@ SIGNATURES = {
                               _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
+    "lr_history_append": [_P, _I64, _I64, _I64, _I, _I64, _I64, _P, _I64, _P, _P],
     "lr_staging_alloc": [_SZ, _P],
     "lr_staging_free": [_P],
     "lr_copy_words": [_P, _P, _I64, _P],

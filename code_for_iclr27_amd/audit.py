@@ -215,7 +215,7 @@ class AuditStep:
         mark("start")
         for index, stages in enumerate(stage_masks):
             _lib.call("lr_score_segments", table_ptr, segments, plan.groups,
-                      plan.window, dim, plan.max_length, plan.max_candidates, plan.window,
+                      plan.window, dim, plan.max_length, plan.max_candidates, plan.query_stride,
                       query_positions.data_ptr(), margin.data_ptr(), float(1.0 / math.sqrt(dim)),
                       float(denominator_epsilon), score_ws.data_ptr(), score_bytes,
                       raw.data_ptr(), nonfinite.data_ptr(), stages, stream)

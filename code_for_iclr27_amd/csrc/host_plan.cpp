@@ -28,10 +28,13 @@ void require(bool ok, const char* message) {
 // The same checks, in the same order and with the same messages, as the Python layer checks.
 void validate_layer(const torch::Tensor& k, const torch::Tensor& v, const torch::Tensor& p,
                     const torch::Tensor& q, const torch::Tensor& g, const torch::Device& device,
-                    int64_t hq, int64_t window, int64_t dim) {
-  for (const torch::Tensor* t : {&k, &v, &p, &q, &g})
+                    int64_t hq, int64_t window, int64_t dim, int64_t query_stride) {
+  for (const torch::Tensor* t : {&k, &v, &p, &g})
     require(t->is_cuda() && t->is_contiguous() && t->device() == device,
             "Expected contiguous CUDA tensor");
+  // Queries may be a window of a longer per-head history (a ring view): rows of one query head
+  // are contiguous, and consecutive query heads sit query_stride rows apart.
+  require(q.is_cuda() && q.device() == device, "Expected contiguous CUDA tensor");
   require(k.scalar_type() == torch::kBFloat16 && v.scalar_type() == torch::kBFloat16 &&
               q.scalar_type() == torch::kBFloat16,
           "The fused scorer takes bf16 keys, values and queries");
@@ -39,6 +42,9 @@ void validate_layer(const torch::Tensor& k, const torch::Tensor& v, const torch:
   require(p.scalar_type() == torch::kFloat32 && p.numel() == k.size(0), "Invalid positions");
   require(q.dim() == 3 && q.size(0) == hq && q.size(1) == window && q.size(2) == dim,
           "Historical query-head count changed");
+  require(q.stride(2) == 1 && (window == 1 || q.stride(1) == dim) &&
+              (hq == 1 || q.stride(0) == query_stride * dim),
+          "Queries must be [Hq, W, d] with contiguous rows and one head stride for every layer");
   require(g.scalar_type() == torch::kFloat32 && g.dim() == 2 && g.size(0) == hq &&
               g.size(1) == dim,
           "Invalid margin gradient");
@@ -52,11 +58,11 @@ inline int64_t ptr(const torch::Tensor& t) { return reinterpret_cast<int64_t>(t.
 // Returns (block, meta, per-segment [layer, head, first candidate, count] int64 [4, S],
 //          per-head [segment index or -1, length] int64 [2, L*H]).
 // meta = (segments, groups, window, dim, max segment length, max candidates, total candidates,
-//         projected floats, head slots, total rows, max head length).
+//         projected floats, head slots, total rows, max head length, query stride in rows).
 struct Plan {
   torch::Tensor block, segment_info, head_info;
   int64_t segments, groups, window, dim, max_seg_length, max_candidates, total, projected, slots,
-      rows_total, max_head_length, layers;
+      rows_total, max_head_length, layers, query_stride;
   // word offsets of the block's parts
   int64_t bounds_at() const { return segments * LR_SEG_WORDS; }
   int64_t ends_at() const { return bounds_at() + segments + 1; }
@@ -64,7 +70,7 @@ struct Plan {
   int64_t heads_at() const { return starts_at() + segments; }
   py::tuple meta() const {
     return py::make_tuple(segments, groups, window, dim, max_seg_length, max_candidates, total,
-                          projected, slots, rows_total, max_head_length);
+                          projected, slots, rows_total, max_head_length, query_stride);
   }
 };
 
@@ -82,6 +88,11 @@ Plan make_plan(const std::vector<torch::Tensor>& keys, const std::vector<torch::
           "Layer lists differ in length");
   require(queries[0].dim() == 3, "Historical query-head count changed");
   const int64_t hq = queries[0].size(0), window = queries[0].size(1), dim = queries[0].size(2);
+  require(dim > 0 && (hq == 1 || queries[0].stride(0) % dim == 0),
+          "Queries must be [Hq, W, d] with contiguous rows and one head stride for every layer");
+  const int64_t query_stride = hq == 1 ? window : queries[0].stride(0) / dim;
+  require(query_stride >= window,
+          "Queries must be [Hq, W, d] with contiguous rows and one head stride for every layer");
   const torch::Device device = keys[0].device();
   const int64_t heads = static_cast<int64_t>(head_lens[0].size());
   require(heads > 0 && hq % heads == 0, "Query heads must be a multiple of KV heads");
@@ -92,7 +103,7 @@ Plan make_plan(const std::vector<torch::Tensor>& keys, const std::vector<torch::
   int64_t segments = 0;
   for (size_t l = 0; l < layers; ++l) {
     validate_layer(keys[l], values[l], positions[l], queries[l], gradients[l], device, hq, window,
-                   dim);
+                   dim, query_stride);
     require(static_cast<int64_t>(head_lens[l].size()) == heads,
             "Every layer must have the same number of KV heads");
     int64_t rows = 0;
@@ -160,7 +171,7 @@ Plan make_plan(const std::vector<torch::Tensor>& keys, const std::vector<torch::
         row[0] = kp + base * dim * 2;
         row[1] = vp + base * dim * 2;
         row[2] = pp + base * 4;
-        row[3] = qp + h * groups * window * dim * 2;
+        row[3] = qp + h * groups * query_stride * dim * 2;
         row[4] = gp + h * groups * dim * 4;
         row[5] = n;
         row[6] = first;
@@ -191,7 +202,7 @@ Plan make_plan(const std::vector<torch::Tensor>& keys, const std::vector<torch::
   }
   return Plan{block, segment_info, head_info, segments, groups, window, dim, max_seg_length,
               max_candidates, total, projected, slots, rows_total, max_head_length,
-              static_cast<int64_t>(layers)};
+              static_cast<int64_t>(layers), query_stride};
 }
 
 py::tuple plan_audit(const std::vector<torch::Tensor>& keys, const std::vector<torch::Tensor>& values,
@@ -437,7 +448,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   for (int i = 0; i < (timed ? 3 : 1); ++i) {
     check_call(library.score_segments(
         words, S, plan.groups, plan.window, plan.dim, plan.max_seg_length, plan.max_candidates,
-        plan.window, query_positions.data_ptr<int64_t>(), margin.data_ptr<float>(),
+        plan.query_stride, query_positions.data_ptr<int64_t>(), margin.data_ptr<float>(),
         static_cast<float>(1.0 / std::sqrt(static_cast<double>(plan.dim))), epsilon,
         dptr(score_ws), score_bytes, raw, nonfinite, timed ? 1 << i : 7, stream));
     stage(timed ? kScoreStages[i] : "score");

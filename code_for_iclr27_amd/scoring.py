@@ -114,7 +114,7 @@ class SegmentPlan:
         self.block = block
         (self.segment_count, self.groups, self.window, self.dim, self.max_length,
          self.max_candidates, self.total, self.projected_floats, self.head_slots,
-         self.rows_total, self.max_head_length) = meta
+         self.rows_total, self.max_head_length, self.query_stride) = meta
         self.heads = heads
         self.segment_info = segment_info.numpy()     # [4, S]: layer, head, first, count
         self.head_info = head_info.numpy()           # [2, L*H]: segment or -1, length
@@ -202,7 +202,7 @@ def score_plan(plan: SegmentPlan, query_positions: torch.Tensor, margin: torch.T
         workspace = torch.empty((workspace_bytes,), dtype=torch.uint8, device=device)
         scores = torch.empty((plan.total,), dtype=torch.float32, device=device)
         _lib.call("lr_score_segments", table.data_ptr(), segments, plan.groups, plan.window,
-                  plan.dim, plan.max_length, plan.max_candidates, plan.window,
+                  plan.dim, plan.max_length, plan.max_candidates, plan.query_stride,
                   query_positions.data_ptr(), margin.data_ptr(),
                   float(1.0 / math.sqrt(plan.dim)), float(denominator_epsilon),
                   workspace.data_ptr(), workspace_bytes, scores.data_ptr(), None, 0,
@@ -232,5 +232,5 @@ def debug_segment_logits(plan: SegmentPlan, segment: int, device) -> torch.Tenso
         table = plan.part("table").to(device)
         out = torch.empty((plan.groups, plan.window, length), dtype=torch.bfloat16, device=device)
         _lib.call("lr_debug_segment_logits", table.data_ptr(), segment, plan.groups, plan.window,
-                  plan.dim, length, plan.window, out.data_ptr(), _lib.stream_of(out))
+                  plan.dim, length, plan.query_stride, out.data_ptr(), _lib.stream_of(out))
     return out

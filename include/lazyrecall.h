@@ -253,6 +253,19 @@ int lr_staging_alloc(size_t bytes, void** host);
 int lr_staging_free(void* host);
 int lr_copy_words(const int64_t* source, int64_t* destination, int64_t words, void* stream);
 
+/* Device-resident query history (replaces the per-layer deques and the per-audit torch.cat of
+ * src/lazy_recall/history.py:21-38,51-63). `ring` is [layers, heads, 2 * window, dim] elements
+ * of elem_bytes (2 or 4) and ring_positions [2 * window] i64, both device memory. Writes query l
+ * (layer_queries[l], device, [heads, dim] contiguous) to rows `slot` and `slot + window` of every
+ * head of layer l and `position` to ring_positions[slot] and [slot + window], with one launch per
+ * LR_HISTORY_MAX_LAYERS layers. Appending the k-th query (0-based) at slot k mod window keeps the
+ * last min(n, window) queries in rows [s, s + min(n, window)), s = n mod window once n >= window
+ * (else 0), oldest first: a strided [heads, n, dim] view the fused scorer reads in place. */
+#define LR_HISTORY_MAX_LAYERS 128
+int lr_history_append(const void* const* layer_queries, int64_t layers, int64_t heads,
+                      int64_t dim, int elem_bytes, int64_t window, int64_t slot, void* ring,
+                      int64_t position, int64_t* ring_positions, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
