@@ -266,6 +266,31 @@ int lr_history_append(const void* const* layer_queries, int64_t layers, int64_t 
                       int64_t dim, int elem_bytes, int64_t window, int64_t slot, void* ring,
                       int64_t position, int64_t* ring_positions, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Decode/prefill attention over the packed ragged layout
+ * ------------------------------------------------------------------------------------- */
+
+/* packed_attention (src/lazy_recall/attention.py:15-35; its flash_attn_varlen_func call with
+ * causal=True, softmax_scale = dim^-0.5, one KV head per segment). Segment s = b * kv_heads + h
+ * owns key/value rows [cu_seqlens_k[s], cu_seqlens_k[s+1]) (device i32 [batch*kv_heads + 1]) of
+ * keys/values [key_rows, dim]. queries are [batch, kv_heads*groups, length, dim] elements with
+ * the given element strides (dim contiguous); query head h*groups + g belongs to segment h.
+ * Causal masking is aligned to the segment end (query i sees keys j <= i + n_s - length); a row
+ * with no visible key is zero. out is [batch, length, kv_heads*groups, dim] contiguous, of the
+ * input dtype (LR_DTYPE_BF16 or LR_DTYPE_F16); dim in {64, 128, 256}. max_keys bounds every
+ * segment's key count (keys past it are not read). workspace: device memory of at least
+ * lr_packed_attention_workspace_bytes(...) bytes, 256-byte aligned, ZERO before its first use;
+ * every call leaves it zero again, so calls on one stream may share it (calls that overlap in
+ * time must not). */
+size_t lr_packed_attention_workspace_bytes(int64_t segments, int64_t groups, int64_t length,
+                                           int64_t max_keys, int64_t dim);
+int lr_packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head_stride,
+                        int64_t q_query_stride, const void* keys, const void* values,
+                        int64_t key_rows, const int32_t* cu_seqlens_k, int64_t batch,
+                        int64_t kv_heads, int64_t groups, int64_t length, int64_t dim, int dtype,
+                        int64_t max_keys, float scale, void* out, void* workspace,
+                        size_t workspace_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

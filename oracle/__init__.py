@@ -14,6 +14,7 @@ Modules:
   selection   refine_arrays with canonical (value, index) ties and with CPU torch.topk
   cpu_path    torch-CPU restatement of the reference CPU math path (timed CPU baseline)
   history     the query-history deques and their per-layer concatenation
+  attention   causal grouped-query attention over the packed ragged layout (f64)
 
 How each part is pinned (checked against something other than itself) is listed in the test
 files under tests/ that exercise it; see tests/test_oracle_*.py.
