@@ -391,6 +391,32 @@ def ops_bench(torch, seed, reps=5):
         L, device, nbytes, wall)
     del req_k, req_v, req_p
 
+    # packed decode attention (attention.py:15-35, batch_attention.py:92-97): one query token
+    # per request and query head (G = 4) over every layer's packed K/V. Each of the 32 layers has
+    # its own K/V buffers, as in a decode step, so no layer's rows are cached from the last call.
+    from types import SimpleNamespace
+
+    from code_for_iclr27_amd.attention import packed_attention
+    for label, requests, head_lengths in (
+            ("cfg2 layer: 8 requests x 8 KV heads x G4, U[1500,2250] keys per head", R,
+             [h for l in lengths for h in l]),
+            ("cfg1 layer: 1 request x 8 KV heads x G4, 2250 keys per head", 1, [T] * H)):
+        total = sum(head_lengths)
+        layer_k = [randn(total, d) for _ in range(L)]
+        layer_v = [randn(total, d) for _ in range(L)]
+        queries = randn(requests, H * 4, 1, d)
+        meta = SimpleNamespace(
+            cu_seqlens_k=torch.tensor([0] + list(np.cumsum(head_lengths)), dtype=torch.int32,
+                                      device=dev),
+            max_seqlen_k=max(head_lengths),
+            decoding_cu_seqlens_q=torch.arange(requests * H + 1, dtype=torch.int32, device=dev))
+        device, wall = measure(lambda: [
+            (lambda l=l: packed_attention(queries, layer_k[l], layer_v[l], meta, 1, H))
+            for l in range(L)], L)
+        nbytes = 2 * total * d * 2 + 2 * requests * H * 4 * d * 2 + (requests * H + 1) * 4
+        out["packed_attention_" + label[:4]] = _op_line(label, L, device, nbytes, wall)
+        del layer_k, layer_v
+
     # query history (history.py:21-38,51-63): one decode step's queries of all 32 layers
     # (Hq 32, d128, bf16) into the device ring, one launch per step
     from code_for_iclr27_amd.history import QueryHistory

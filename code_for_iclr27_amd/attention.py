@@ -19,25 +19,10 @@ import torch
 
 from . import _lib
 
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
-
 
 def flash_attn_deterministic_status():
     """attention.py:10-11. No deterministic backward has run through this module."""
     return None
-
-
-def _workspace(device: torch.device, stream: int, size: int) -> torch.Tensor | None:
-    """Zeroed scratch kept per (device, stream). Every call leaves its tickets at zero again, so
-    calls ordered on one stream share it."""
-    if size == 0:
-        return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
-    buffer = _workspaces.get(key)
-    if buffer is None or buffer.numel() < size:
-        buffer = torch.zeros(max(size, 1 << 16), dtype=torch.uint8, device=device)
-        _workspaces[key] = buffer
-    return buffer
 
 
 def _check(condition: bool, message: str) -> None:
@@ -92,7 +77,7 @@ def packed_attention(queries, keys, values, metadata, length, kv_heads):
         stream = _lib.stream_of(queries)
         size = _lib.load().lr_packed_attention_workspace_bytes(segments, groups, length,
                                                                max_keys, dimension)
-        workspace = _workspace(device, stream, size)
+        workspace = torch.empty(size, dtype=torch.uint8, device=device) if size else None
         _lib.call("lr_packed_attention", queries.data_ptr(), queries.stride(0), queries.stride(1),
                   queries.stride(2), _lib.ptr(keys), _lib.ptr(values), keys.shape[0],
                   cumulative.data_ptr(), batch, kv_heads, groups, length, dimension,

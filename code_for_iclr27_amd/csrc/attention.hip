@@ -8,14 +8,17 @@
 // (n = the segment's key count); for decode (L = 1) that is every key. A row with no visible key
 // outputs zeros. Softmax scale `scale`, accumulation in f32, output rounded to the input type.
 //
-// Work split (flash-decoding): a one-wave workgroup owns R query rows of one segment and one
-// chunk of at most `chunk` keys. QK^T runs on v_mfma_f32_16x16x32 (the R rows padded to 16,
-// K rows read straight into the B operand, 16 B per lane), the chunk's scores go to LDS, the wave
-// forms its own max and exp-sum, then accumulates P*V on the VALU with each lane holding 8
-// elements of a V row (16 B loads, D/8 lanes per row). A segment whose keys need more than one
-// chunk writes (max, sum, unnormalised output) partials; the last of its workgroups to finish
-// (a ticket counter, no waiting) merges them and writes the output. Every ticket is reset to zero
-// by the workgroup that consumed it, so a zeroed workspace stays valid across calls.
+// Work split (flash decoding): a workgroup of four waves owns R query rows of one segment and
+// one block of keys; each wave takes 12-16 KB of its K rows (wave_keys) and issues every load
+// (queries, K rows, V slices) before the first use, so one memory round trip covers the wave.
+// QK^T runs on v_mfma_f32_16x16x32 (the R rows padded to 16, K rows straight into the B operand,
+// 16 B per lane); each wave forms its own max and exp-sum in registers, stages p in LDS and
+// accumulates P*V on the VALU with each lane holding 8 elements of a V row (D/8 lanes per row).
+// The four wave states merge in LDS. A segment whose keys need more than one block writes
+// (max, sum, unnormalised output) partials, and a second launch merges them (one workgroup per
+// segment and tile). The launch boundary orders the two: a device-scope fence per workgroup
+// instead (a ticket taken by the last block) costs an L2 writeback and invalidate on every
+// workgroup's XCD, and measured 4-6x slower at the cfg2 decode shape.
 
 #include <algorithm>
 
@@ -29,8 +32,12 @@ typedef _Float16 attn_f16x8 __attribute__((ext_vector_type(8)));
 typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned attn_u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kAttnThreads = 64;
-constexpr int kAttnMaxChunk = 256;  // keys per workgroup (LDS holds kAttnMaxChunk x R scores)
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = 64 * kAttnWaves;
+// Keys per wave: 12 KB of K rows (and as many V bytes) for d64/d128, 16 KB for d256 (a whole
+// number of 16-key MFMA blocks); small enough for three waves per SIMD.
+constexpr int wave_keys(int dim) { return dim == 256 ? 32 : 6144 / dim; }
+constexpr int kMergeUnroll = 4;       // partial blocks each merging thread loads at once
 constexpr float kAttnLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -58,12 +65,10 @@ struct AttnArgs {
   int64_t kv_heads, groups, length;
   int64_t tiles;            // query-row tiles per segment: ceil(L*G / R)
   int64_t splits;           // key chunks per (segment, tile) in the grid
-  int64_t chunk;            // keys per chunk (multiple of 16, <= kAttnMaxChunk)
   float scale;
   void* out;                // [B, L, kv_heads * G, D]
   float* part_o;            // [units * splits, R, D]
   float* part_ml;           // [units * splits, R, 2]
-  uint32_t* tickets;        // [units]
 };
 
 template <typename T>
@@ -114,18 +119,42 @@ __device__ __forceinline__ T* output_row(const AttnArgs& a, int64_t seg, int64_t
   return static_cast<T*>(a.out) + ((b * a.length + i) * heads + h * a.groups + g) * D;
 }
 
+// A (max, exp-sum, unnormalised output slice) softmax state; merge_into folds another in.
+struct MergeState {
+  float m, l, o[8];
+};
+
+__device__ __forceinline__ void merge_into(MergeState& s, float m, float l, const float (&o)[8]) {
+  if (m == kNegInf) return;
+  const float mx = fmaxf(s.m, m);
+  const float ws = s.m == kNegInf ? 0.f : __builtin_amdgcn_exp2f((s.m - mx) * kAttnLog2e);
+  const float wo = __builtin_amdgcn_exp2f((m - mx) * kAttnLog2e);
+  s.l = __builtin_fmaf(wo, l, s.l * ws);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s.o[e] = __builtin_fmaf(wo, o[e], s.o[e] * ws);
+  s.m = mx;
+}
+
 template <typename T, int D, int R>
-__global__ __launch_bounds__(kAttnThreads) void packed_attention_kernel(AttnArgs a) {
-  static_assert(D % 32 == 0 && D >= 64 && D <= 512, "head dim must be a multiple of 32");
+__global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attention_kernel(AttnArgs a) {
+  static_assert(D == 64 || D == 128 || D == 256, "head dim");
   static_assert(R == 4 || R == 8, "rows per tile");
-  constexpr int KS = D / 32;       // MFMA k-steps over the head dimension
-  constexpr int LPK = D / 8;       // lanes per V row in the P*V phase
-  constexpr int KPI = 64 / LPK;    // V rows per wave-wide load
+  constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
+  constexpr int LPK = D / 8;          // lanes per V row in the P*V phase
+  constexpr int KPI = 64 / LPK;       // V rows per wave-wide load
+  constexpr int CH = wave_keys(D);    // keys per wave
+  static_assert(CH % 16 == 0, "whole MFMA key blocks");
+  constexpr int NB = CH / 16;         // 16-key MFMA blocks per wave
+  constexpr int VL = CH / KPI;        // V loads (16 B) per lane
+  constexpr int ITEMS = R * LPK;      // (row, 8-element slice) items of one output tile
+  static_assert(ITEMS <= kAttnThreads, "one merge item per thread");
   using Vec = AttnVec<T>;
   using X8 = typename Vec::x8;
-  __shared__ __align__(16) float scores[kAttnMaxChunk][R];
+  __shared__ __align__(16) float probs[kAttnWaves][CH][R];
+  __shared__ __align__(16) float wave_o[kAttnWaves][R][D];
+  __shared__ float wave_ml[kAttnWaves][R][2];
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t unit = blockIdx.x / a.splits, split = blockIdx.x - unit * a.splits;
   const int64_t seg = unit / a.tiles, tile = unit - seg * a.tiles;
   const int64_t rows = a.length * a.groups;
@@ -140,12 +169,13 @@ __global__ __launch_bounds__(kAttnThreads) void packed_attention_kernel(AttnArgs
   const int64_t last_query = (row0 + rows_here - 1) / a.groups;
   int64_t key_end = last_query + shift + 1;
   key_end = key_end < 0 ? 0 : (key_end > n ? n : key_end);
-  int64_t needed = (key_end + a.chunk - 1) / a.chunk;
-  needed = needed > a.splits ? a.splits : needed;  // keys past splits * chunk are not read
+  constexpr int64_t kBlockKeys = kAttnWaves * CH;
+  int64_t needed = (key_end + kBlockKeys - 1) / kBlockKeys;
+  needed = needed > a.splits ? a.splits : needed;  // keys past splits * block keys are not read
 
   if (needed == 0) {  // no visible key for any row of this tile: zeros
     if (split != 0) return;
-    for (int item = lane; item < R * LPK; item += kAttnThreads) {
+    for (int item = tid; item < ITEMS; item += kAttnThreads) {
       const int r = item / LPK, c = item - r * LPK;
       if (r < rows_here)
         *reinterpret_cast<attn_u32x4*>(output_row<T, D>(a, seg, row0 + r) + 8 * c) =
@@ -153,200 +183,253 @@ __global__ __launch_bounds__(kAttnThreads) void packed_attention_kernel(AttnArgs
     }
     return;
   }
-  if (split >= needed) return;
+  if (split >= needed) return;  // uniform across the workgroup
 
-  const int64_t kb = split * a.chunk;
-  const int64_t ke = kb + a.chunk < key_end ? kb + a.chunk : key_end;
-  const int nk = static_cast<int>(ke - kb);
-  const T* kbase = static_cast<const T*>(a.keys) + (key0 + kb) * D;
-  const T* vbase = static_cast<const T*>(a.values) + (key0 + kb) * D;
-
-  // ---- QK^T: A = query rows (row m = lane & 15), B = 16 key rows; k chunk j = lane >> 4.
+  const int64_t kb = split * kBlockKeys + wave * CH;
+  const int64_t ke = kb + CH < key_end ? kb + CH : key_end;
+  const int nk = kb < ke ? static_cast<int>(ke - kb) : 0;
   const int m = lane & 15, j = lane >> 4;
-  X8 qop[KS];
-  {
-    const bool row_ok = m < rows_here;
-    const int64_t row = row0 + (row_ok ? m : 0);
-    const int64_t b = seg / a.kv_heads, h = seg - b * a.kv_heads;
-    const int64_t i = row / a.groups, g = row - i * a.groups;
-    const T* q = static_cast<const T*>(a.queries) + b * a.q_batch + (h * a.groups + g) * a.q_head +
-                 i * a.q_query + 8 * j;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const attn_u32x4 raw = row_ok ? load16(q + 32 * ks) : attn_u32x4{0u, 0u, 0u, 0u};
-      qop[ks] = __builtin_bit_cast(X8, raw);
-    }
-  }
-  // This lane's output rows are 4 * j + r; their causal limits (keys at or below are visible).
-  int64_t limit[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t row = row0 + 4 * j + r;
-    limit[r] = (4 * j + r < rows_here) ? row / a.groups + shift - kb : -1;
-  }
-  const int blocks = (nk + 15) >> 4;
-  for (int blk = 0; blk < blocks; blk += 2) {
-    attn_u32x4 kraw[2][KS];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      int key = (blk + u) * 16 + m;
-      key = key < nk ? key : nk - 1;  // clamped in-range row; its score is masked below
-      const T* kp = kbase + static_cast<int64_t>(key) * D + 8 * j;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kraw[u][ks] = load16(kp + 32 * ks);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      if (blk + u >= blocks) break;
-      attn_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) acc = Vec::mfma(qop[ks], __builtin_bit_cast(X8, kraw[u][ks]), acc);
-      const int key = (blk + u) * 16 + m;  // D layout: lane holds key (lane & 15), rows 4j + r
-      if (4 * j < R && key < nk) {
-        attn_f32x4 s;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s[r] = key <= limit[r] ? acc[r] * a.scale : kNegInf;
-        *reinterpret_cast<attn_f32x4*>(&scores[key][4 * j]) = s;
-      }
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---- Per-row max and exp-sum over this chunk (lane owns keys lane, lane + 64, ...).
-  float row_max[R], row_sum[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) row_max[r] = kNegInf;
-  for (int key = lane; key < nk; key += kAttnThreads) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) row_max[r] = fmaxf(row_max[r], scores[key][r]);
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    row_max[r] = wave_max(row_max[r]);
-    row_sum[r] = 0.f;
-  }
-  for (int key = lane; key < nk; key += kAttnThreads) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float s = scores[key][r];
-      const float p = s == kNegInf ? 0.f : __builtin_amdgcn_exp2f((s - row_max[r]) * kAttnLog2e);
-      scores[key][r] = p;
-      row_sum[r] += p;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) row_sum[r] = wave_sum(row_sum[r]);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // ---- P*V: lane group kg = lane / LPK takes keys kg, kg + KPI, ...; lane owns 8 elements.
   const int kg = lane / LPK, c = lane - kg * LPK;
+
+  float row_max[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
+  float row_sum[4] = {0.f, 0.f, 0.f, 0.f};
   float acc[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
-  constexpr int kUnroll = 4;
-  for (int base = kg; base < nk; base += kUnroll * KPI) {
-    attn_u32x4 vraw[kUnroll];
+
+  if (nk > 0) {
+    const T* kbase = static_cast<const T*>(a.keys) + (key0 + kb) * D;
+    const T* vbase = static_cast<const T*>(a.values) + (key0 + kb) * D;
+    // Every load of the wave is issued before the first use: queries (A operand, row m = lane
+    // & 15, k chunk j = lane >> 4), K rows (B operand, key m of each 16-key block), V slices.
+    X8 qop[KS];
+    {
+      const bool row_ok = m < rows_here;
+      const int64_t row = row0 + (row_ok ? m : 0);
+      const int64_t b = seg / a.kv_heads, h = seg - b * a.kv_heads;
+      const int64_t i = row / a.groups, g = row - i * a.groups;
+      const T* q = static_cast<const T*>(a.queries) + b * a.q_batch +
+                   (h * a.groups + g) * a.q_head + i * a.q_query + 8 * j;
+      // Unconditional loads from a valid row (padding lanes read row0's) and a select after
+      // them: a load under a branch is waited for inside the branch.
+      attn_u32x4 raw[KS];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int key = base + u * KPI;
+      for (int ks = 0; ks < KS; ++ks) raw[ks] = load16(q + 32 * ks);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qop[ks] = __builtin_bit_cast(X8, row_ok ? raw[ks] : attn_u32x4{0u, 0u, 0u, 0u});
+    }
+    attn_u32x4 kraw[NB][KS];
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      int key = blk * 16 + m;
+      key = key < nk ? key : nk - 1;  // clamped in-range row; its score is masked below
+      const T* kp = kbase + static_cast<int64_t>(key) * D + 8 * j;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kraw[blk][ks] = load16(kp + 32 * ks);
+    }
+    attn_u32x4 vraw[VL];
+#pragma unroll
+    for (int u = 0; u < VL; ++u) {
+      int key = kg + u * KPI;
       key = key < nk ? key : nk - 1;
       vraw[u] = load16(vbase + static_cast<int64_t>(key) * D + 8 * c);
     }
+
+    // QK^T. D layout: lane holds key 16 * blk + (lane & 15) for rows 4j + r.
+    int64_t limit[4];  // causal limit of this lane's rows, relative to kb (keys <= limit seen)
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int key = base + u * KPI;
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = row0 + 4 * j + r;
+      limit[r] = (4 * j + r < rows_here) ? row / a.groups + shift - kb : -1;
+    }
+    float s[NB][4];
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      attn_f32x4 dot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) dot = Vec::mfma(qop[ks], __builtin_bit_cast(X8, kraw[blk][ks]), dot);
+      const int key = blk * 16 + m;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[blk][r] = (key < nk && key <= limit[r]) ? dot[r] * a.scale : kNegInf;
+        row_max[r] = fmaxf(row_max[r], s[blk][r]);
+      }
+    }
+    // Row max and exp-sum over the 16 lanes that share rows 4j .. 4j + 3.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int offset = 1; offset < 16; offset <<= 1)
+        row_max[r] = fmaxf(row_max[r], __shfl_xor(row_max[r], offset));
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      attn_f32x4 p;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = s[blk][r] == kNegInf ? 0.f
+                                    : __builtin_amdgcn_exp2f((s[blk][r] - row_max[r]) * kAttnLog2e);
+        row_sum[r] += p[r];
+      }
+      if (4 * j < R) *reinterpret_cast<attn_f32x4*>(&probs[wave][blk * 16 + m][4 * j]) = p;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int offset = 1; offset < 16; offset <<= 1) row_sum[r] += __shfl_xor(row_sum[r], offset);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // P*V on the prefetched V slices; keys past nk carry p = 0 from a clamped row, skipped.
+#pragma unroll
+    for (int u = 0; u < VL; ++u) {
+      const int key = kg + u * KPI;
       if (key >= nk) break;
       float v[8];
       unpack8<T>(vraw[u], v);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float p = scores[key][r];
+        const float p = probs[wave][key][r];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][e] = __builtin_fmaf(p, v[e], acc[r][e]);
       }
     }
+    // Sum the KPI lane groups (lanes c, c + LPK, ... hold the same elements).
+#pragma unroll
+    for (int offset = LPK; offset < 64; offset <<= 1)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r][e] += __shfl_xor(acc[r][e], offset);
   }
-  // Sum the KPI lane groups (lanes c, c + LPK, ... hold the same elements).
-#pragma unroll
-  for (int offset = LPK; offset < 64; offset <<= 1)
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r][e] += __shfl_xor(acc[r][e], offset);
 
-  if (needed == 1) {  // the only chunk: normalise and write
+  // Wave states to LDS: rows r = 4j + i are held by lanes 16j .. 16j + 15.
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (r % KPI != kg || r >= rows_here) continue;
-      const float inv = row_sum[r] > 0.f ? 1.0f / row_sum[r] : 0.f;
+  for (int r = 0; r < R; ++r) {
+    if (r % KPI != kg) continue;
+    float* wo = &wave_o[wave][r][8 * c];
+    *reinterpret_cast<attn_f32x4*>(wo) = attn_f32x4{acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
+    *reinterpret_cast<attn_f32x4*>(wo + 4) = attn_f32x4{acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
+  }
+  if (m == 0 && 4 * j < R) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      wave_ml[wave][4 * j + r][0] = row_max[r];
+      wave_ml[wave][4 * j + r][1] = row_sum[r];
+    }
+  }
+  __syncthreads();
+
+  // Merge the waves: thread t < ITEMS owns row r = t / LPK, elements 8 * (t % LPK) ...
+  const int r_item = tid / LPK, c_item = tid - r_item * LPK;
+  MergeState st{kNegInf, 0.f, {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
+  if (tid < ITEMS) {
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      float o[8];
+      const float* wo = &wave_o[w][r_item][8 * c_item];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = wo[e];
+      merge_into(st, wave_ml[w][r_item][0], wave_ml[w][r_item][1], o);
+    }
+  }
+  if (needed == 1) {  // the only block of keys: normalise and write
+    if (tid < ITEMS && r_item < rows_here) {
+      const float inv = st.l > 0.f ? 1.0f / st.l : 0.f;
       float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = acc[r][e] * inv;
-      *reinterpret_cast<attn_u32x4*>(output_row<T, D>(a, seg, row0 + r) + 8 * c) = pack8<T>(o);
+      for (int e = 0; e < 8; ++e) o[e] = st.o[e] * inv;
+      *reinterpret_cast<attn_u32x4*>(output_row<T, D>(a, seg, row0 + r_item) + 8 * c_item) =
+          pack8<T>(o);
     }
     return;
   }
 
-  // ---- Partials, then the last workgroup of this (segment, tile) merges them.
+  // ---- Partial state of this block; attention_merge_kernel combines the blocks.
   const int64_t slot = (unit * a.splits + split) * R;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (r % KPI != kg) continue;
-    float* po = a.part_o + (slot + r) * D + 8 * c;
-    *reinterpret_cast<attn_f32x4*>(po) = attn_f32x4{acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
-    *reinterpret_cast<attn_f32x4*>(po + 4) = attn_f32x4{acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
-  }
-  if (lane < R) {
-    float mx = 0.f, sm = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (r == lane) { mx = row_max[r]; sm = row_sum[r]; }
-    a.part_ml[(slot + lane) * 2] = mx;
-    a.part_ml[(slot + lane) * 2 + 1] = sm;
-  }
-  __threadfence();  // partials visible device-wide before the ticket is taken
-  uint32_t ticket = 0;
-  if (lane == 0) ticket = atomicAdd(&a.tickets[unit], 1u);
-  ticket = __shfl(ticket, 0);
-  if (ticket != static_cast<uint32_t>(needed - 1)) return;
-  __threadfence();
-  if (lane == 0) a.tickets[unit] = 0u;  // consumed: the workspace is ready for the next call
-
-  const int64_t first = unit * a.splits * R;
-  for (int item = lane; item < R * LPK; item += kAttnThreads) {
-    const int r = item / LPK, cc = item - r * LPK;
-    if (r >= rows_here) continue;
-    float mx = kNegInf;
-    for (int64_t k = 0; k < needed; ++k) mx = fmaxf(mx, a.part_ml[(first + k * R + r) * 2]);
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float total = 0.f;
-    if (mx != kNegInf) {
-      for (int64_t k = 0; k < needed; ++k) {
-        const float mk = a.part_ml[(first + k * R + r) * 2];
-        if (mk == kNegInf) continue;
-        const float w = __builtin_amdgcn_exp2f((mk - mx) * kAttnLog2e);
-        total = __builtin_fmaf(w, a.part_ml[(first + k * R + r) * 2 + 1], total);
-        const float* po = a.part_o + (first + k * R + r) * D + 8 * cc;
-        const attn_f32x4 lo = *reinterpret_cast<const attn_f32x4*>(po);
-        const attn_f32x4 hi = *reinterpret_cast<const attn_f32x4*>(po + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[e] = __builtin_fmaf(w, lo[e], o[e]);
-          o[4 + e] = __builtin_fmaf(w, hi[e], o[4 + e]);
-        }
-      }
+  if (tid < ITEMS) {
+    float* po = a.part_o + (slot + r_item) * D + 8 * c_item;
+    *reinterpret_cast<attn_f32x4*>(po) = attn_f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
+    *reinterpret_cast<attn_f32x4*>(po + 4) = attn_f32x4{st.o[4], st.o[5], st.o[6], st.o[7]};
+    if (c_item == 0) {
+      a.part_ml[(slot + r_item) * 2] = st.m;
+      a.part_ml[(slot + r_item) * 2 + 1] = st.l;
     }
-    const float inv = total > 0.f ? 1.0f / total : 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] *= inv;
-    *reinterpret_cast<attn_u32x4*>(output_row<T, D>(a, seg, row0 + r) + 8 * cc) = pack8<T>(o);
   }
+}
+
+// Second launch: one workgroup per (segment, tile) whose keys spanned more than one block merges
+// the blocks' partial states. Thread (part, item) folds blocks part, part + PARTS, ... with the
+// loads of kMergeUnroll blocks in flight at once; the PARTS states then meet in LDS.
+template <typename T, int D, int R>
+__global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs a) {
+  constexpr int LPK = D / 8;
+  constexpr int ITEMS = R * LPK;
+  constexpr int PARTS = kAttnThreads / ITEMS;
+  constexpr int64_t kBlockKeys = kAttnWaves * wave_keys(D);
+  __shared__ __align__(16) float merge_o[kAttnThreads][8];
+  __shared__ float merge_ml[kAttnThreads][2];
+  const int tid = threadIdx.x;
+  const int64_t unit = blockIdx.x;
+  const int64_t seg = unit / a.tiles, tile = unit - seg * a.tiles;
+  const int64_t rows = a.length * a.groups;
+  const int64_t row0 = tile * R;
+  const int64_t rows_here = rows - row0 < R ? rows - row0 : R;
+  int64_t key0 = a.cu[seg], n = static_cast<int64_t>(a.cu[seg + 1]) - key0;
+  key0 = key0 < 0 ? 0 : (key0 > a.key_rows ? a.key_rows : key0);
+  n = n < 0 ? 0 : (n > a.key_rows - key0 ? a.key_rows - key0 : n);
+  const int64_t last_query = (row0 + rows_here - 1) / a.groups;
+  int64_t key_end = last_query + n - a.length + 1;
+  key_end = key_end < 0 ? 0 : (key_end > n ? n : key_end);
+  int64_t needed = (key_end + kBlockKeys - 1) / kBlockKeys;
+  needed = needed > a.splits ? a.splits : needed;
+  if (needed <= 1) return;  // the first launch wrote this tile's output
+
+  const int part = tid / ITEMS, item = tid - part * ITEMS;
+  const int r = item / LPK, cc = item - r * LPK;
+  const int64_t first = unit * a.splits * R;
+  MergeState total{kNegInf, 0.f, {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
+  for (int64_t k0 = part; k0 < needed; k0 += PARTS * kMergeUnroll) {
+    float mk[kMergeUnroll], lk[kMergeUnroll];
+    attn_f32x4 lo[kMergeUnroll], hi[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      int64_t k = k0 + u * PARTS;
+      const bool live = k < needed;
+      k = live ? k : k0;
+      const int64_t at = first + k * R + r;
+      mk[u] = live ? a.part_ml[at * 2] : kNegInf;
+      lk[u] = a.part_ml[at * 2 + 1];
+      lo[u] = *reinterpret_cast<const attn_f32x4*>(a.part_o + at * D + 8 * cc);
+      hi[u] = *reinterpret_cast<const attn_f32x4*>(a.part_o + at * D + 8 * cc + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const float o[8] = {lo[u][0], lo[u][1], lo[u][2], lo[u][3],
+                          hi[u][0], hi[u][1], hi[u][2], hi[u][3]};
+      merge_into(total, mk[u], lk[u], o);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) merge_o[tid][e] = total.o[e];
+  merge_ml[tid][0] = total.m;
+  merge_ml[tid][1] = total.l;
+  __syncthreads();
+  if (part != 0 || r >= rows_here) return;
+  for (int p = 1; p < PARTS; ++p) {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = merge_o[p * ITEMS + item][e];
+    merge_into(total, merge_ml[p * ITEMS + item][0], merge_ml[p * ITEMS + item][1], o);
+  }
+  const float inv = total.l > 0.f ? 1.0f / total.l : 0.f;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = total.o[e] * inv;
+  *reinterpret_cast<attn_u32x4*>(output_row<T, D>(a, seg, row0 + r) + 8 * cc) = pack8<T>(o);
 }
 
 struct AttnPlan {
@@ -354,34 +437,37 @@ struct AttnPlan {
   int64_t tiles, splits, chunk, units;
 };
 
-AttnPlan plan_attention(int64_t segments, int64_t groups, int64_t length, int64_t max_keys) {
+// Keys one workgroup covers: four waves of wave_keys(dim) keys each.
+int64_t block_keys(int64_t dim) { return kAttnWaves * wave_keys(static_cast<int>(dim)); }
+
+AttnPlan plan_attention(int64_t segments, int64_t groups, int64_t length, int64_t max_keys,
+                        int64_t dim) {
   AttnPlan p{};
   const int64_t rows = length * groups;
   p.rows_per_tile = rows <= 4 ? 4 : 8;
   p.tiles = ceil_div(rows, p.rows_per_tile);
   p.units = segments * p.tiles;
-  // Enough workgroups to fill the chip (about 8 waves per CU), in chunks of 64..256 keys.
-  constexpr int64_t kTargetWaves = 2048;
-  int64_t chunk = kAttnMaxChunk;
-  while (chunk > 64 && p.units * ceil_div(std::max<int64_t>(max_keys, 1), chunk) < kTargetWaves)
-    chunk /= 2;
-  p.chunk = chunk;
-  p.splits = std::max<int64_t>(1, ceil_div(max_keys, chunk));
+  p.chunk = block_keys(dim);
+  p.splits = std::max<int64_t>(1, ceil_div(max_keys, p.chunk));
   return p;
 }
 
 size_t workspace_bytes(const AttnPlan& p, int64_t dim) {
   if (p.splits == 1) return 0;
   const int64_t slots = p.units * p.splits * p.rows_per_tile;
-  const size_t tickets = static_cast<size_t>(ceil_div(p.units * 4, 256) * 256);
-  return tickets + static_cast<size_t>(slots) * static_cast<size_t>(dim + 2) * 4;
+  return static_cast<size_t>(slots) * static_cast<size_t>(dim + 2) * 4;
 }
 
 template <typename T, int D, int R>
 int launch_attention(const AttnArgs& args, int64_t blocks, hipStream_t stream) {
   hipLaunchKernelGGL((packed_attention_kernel<T, D, R>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kAttnThreads), 0, stream, args);
-  return check_launch("packed_attention");
+  if (int status = check_launch("packed_attention")) return status;
+  if (args.splits == 1) return LR_OK;
+  hipLaunchKernelGGL((attention_merge_kernel<T, D, R>),
+                     dim3(static_cast<unsigned>(blocks / args.splits)), dim3(kAttnThreads), 0,
+                     stream, args);
+  return check_launch("packed_attention merge");
 }
 
 template <typename T, int D>
@@ -409,7 +495,7 @@ extern "C" size_t lr_packed_attention_workspace_bytes(int64_t segments, int64_t 
                                                       int64_t length, int64_t max_keys,
                                                       int64_t dim) {
   if (segments <= 0 || groups <= 0 || length <= 0 || max_keys < 0 || dim <= 0) return 0;
-  return workspace_bytes(plan_attention(segments, groups, length, max_keys), dim);
+  return workspace_bytes(plan_attention(segments, groups, length, max_keys, dim), dim);
 }
 
 extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
@@ -435,7 +521,7 @@ extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
                                                       q_query_stride) * 2);
   LR_REQUIRE(alignment % 16 == 0, "Attention operands must be 16-byte aligned");
   const int64_t segments = batch * kv_heads;
-  const AttnPlan plan = plan_attention(segments, groups, length, max_keys);
+  const AttnPlan plan = plan_attention(segments, groups, length, max_keys, dim);
   const size_t needed = workspace_bytes(plan, dim);
   LR_REQUIRE(workspace_size >= needed && (needed == 0 || workspace != nullptr),
              "Attention workspace too small");
@@ -458,14 +544,10 @@ extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
   args.length = length;
   args.tiles = plan.tiles;
   args.splits = plan.splits;
-  args.chunk = plan.chunk;
   args.scale = scale;
   args.out = out;
   if (needed) {
-    char* base = static_cast<char*>(workspace);
-    args.tickets = reinterpret_cast<uint32_t*>(base);
-    const size_t tickets = static_cast<size_t>(ceil_div(plan.units * 4, 256) * 256);
-    args.part_ml = reinterpret_cast<float*>(base + tickets);
+    args.part_ml = static_cast<float*>(workspace);
     args.part_o = args.part_ml + plan.units * plan.splits * plan.rows_per_tile * 2;
   }
   const hipStream_t s = as_stream(stream);

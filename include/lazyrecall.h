@@ -278,10 +278,10 @@ int lr_history_append(const void* const* layer_queries, int64_t layers, int64_t 
  * Causal masking is aligned to the segment end (query i sees keys j <= i + n_s - length); a row
  * with no visible key is zero. out is [batch, length, kv_heads*groups, dim] contiguous, of the
  * input dtype (LR_DTYPE_BF16 or LR_DTYPE_F16); dim in {64, 128, 256}. max_keys bounds every
- * segment's key count (keys past it are not read). workspace: device memory of at least
- * lr_packed_attention_workspace_bytes(...) bytes, 256-byte aligned, ZERO before its first use;
- * every call leaves it zero again, so calls on one stream may share it (calls that overlap in
- * time must not). */
+ * segment's key count (keys past it are not read). workspace: device scratch of at least
+ * lr_packed_attention_workspace_bytes(...) bytes (0 when every segment fits one block of keys),
+ * 256-byte aligned, no initial contents required; calls that overlap in time need their own.
+ * Two launches when a segment spans several key blocks (blocks, then their merge). */
 size_t lr_packed_attention_workspace_bytes(int64_t segments, int64_t groups, int64_t length,
                                            int64_t max_keys, int64_t dim);
 int lr_packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head_stride,
