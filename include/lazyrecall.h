@@ -291,6 +291,44 @@ int lr_packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_h
                         int64_t max_keys, float scale, void* out, void* workspace,
                         size_t workspace_size, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Audit vector-Jacobian helpers (the margin objective and its gradients)
+ * ------------------------------------------------------------------------------------- */
+
+/* last_token_logits_float32 (src/lazy_recall/_core/scoring.py:34-52): out[r, v] =
+ * sum_d hidden[r, d] * weight[v, d] (+ bias[v]) in f32. hidden [rows, dim] f32, weight
+ * [vocab, dim] and bias [vocab] (may be NULL) of `dtype` (F32/F16/BF16), out [rows, vocab] f32.
+ * dim a multiple of 8, at most 8192; weight 16-byte aligned. */
+int lr_head_logits(const float* hidden, int64_t rows, const void* weight, const void* bias,
+                   int64_t vocab, int64_t dim, int dtype, float* out, void* stream);
+
+/* one_vs_rest_margin / row_margins (src/lazy_recall/_core/scoring.py:27-31,
+ * batch_audit.py:11-15): per logits row r ([rows, vocab] f32), the target t = targets[r]
+ * (device i64, or NULL: the first argmax), the competitor max M = max_{v != t} l_v and sum
+ * S = sum_{v != t} exp(l_v - M); margins[r] = l_t - (M + log S), stats[r] = (M, S). targets_out
+ * (may be NULL) receives t. */
+int lr_margin_stats(const float* logits, int64_t rows, int64_t vocab, const int64_t* targets,
+                    int64_t* targets_out, float* margins, float* stats, void* stream);
+
+/* Workspace of lr_hidden_gradient / lr_pre_gradient (device, 16-byte aligned, no contents). */
+size_t lr_row_sum_workspace_bytes(int64_t rows, int64_t vocab, int64_t dim);
+
+/* one_vs_rest_hidden_gradient / row_hidden_gradients (src/lazy_recall/_core/scoring.py:55-76,
+ * batch_audit.py:18-24): out[r, :] = (weight[t_r, :] - sum_v p[r, v] * weight[v, :]) * due[r],
+ * p[r] the softmax of row r's logits with the target excluded (p = exp(l - M) / S from
+ * lr_margin_stats' stats, 0 at t_r). due (may be NULL: 1) [rows] f32, out [rows, dim] f32. */
+int lr_hidden_gradient(const float* logits, const float* stats, const int64_t* targets,
+                       int64_t rows, const void* weight, int64_t vocab, int64_t dim, int dtype,
+                       const float* due, float* out, void* workspace, size_t workspace_size,
+                       void* stream);
+
+/* Pre-projection margin gradient of one layer (src/lazy_recall/scoring.py:228-237):
+ * out[q] = sum_h post_gradient[h] * o_weight[h, q] (* gate[q] when gate is not NULL).
+ * post_gradient [hidden] f32, o_weight [hidden, width] of `dtype`, gate [width] f32. */
+int lr_pre_gradient(const float* post_gradient, const void* o_weight, int64_t hidden,
+                    int64_t width, int dtype, const float* gate, float* out, void* workspace,
+                    size_t workspace_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ Modules:
   cpu_path    torch-CPU restatement of the reference CPU math path (timed CPU baseline)
   history     the query-history deques and their per-layer concatenation
   attention   causal grouped-query attention over the packed ragged layout (f64)
+  vjp         head logits, one-vs-rest margins and their hidden / pre-projection gradients
 
 How each part is pinned (checked against something other than itself) is listed in the test
 files under tests/ that exercise it; see tests/test_oracle_*.py.
