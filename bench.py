@@ -417,6 +417,33 @@ def ops_bench(torch, seed, reps=5):
         out["packed_attention_" + label[:4]] = _op_line(label, L, device, nbytes, wall)
         del layer_k, layer_v
 
+    # the audit's margin helpers at the Llama-3.1-8B head (vocab 128,256 x hidden 4096, bf16)
+    # and its 32 o_proj matrices [4096, 4096] (_core/scoring.py:34-76, scoring.py:228-237)
+    from code_for_iclr27_amd import vjp
+    vocab, hidden_size = 128256, 4096
+    head = SimpleNamespace(weight=randn(vocab, hidden_size) * 0.02, bias=None)
+    model = SimpleNamespace(get_output_embeddings=lambda: head)
+    final_hidden = torch.randn((1, hidden_size), generator=gen, device=dev)
+    logits = vjp.last_token_logits_float32(model, final_hidden)
+    target = int(logits.argmax().item())
+    head_bytes = vocab * hidden_size * 2
+    for name, call, nbytes in (
+            ("head_logits", lambda: vjp.last_token_logits_float32(model, final_hidden),
+             head_bytes + vocab * 4 + hidden_size * 4),
+            ("hidden_gradient", lambda: vjp.one_vs_rest_hidden_gradient(model, logits, target),
+             head_bytes + 3 * vocab * 4 + hidden_size * 4)):
+        device, wall = measure(lambda: [call for _ in range(8)], 1)
+        out[name] = _op_line(f"Llama-3.1-8B head: {vocab} x {hidden_size} bf16, 1 row", 1,
+                             device, nbytes, wall)
+    o_weights = [randn(hidden_size, hidden_size) * 0.02 for _ in range(L)]
+    posts = [torch.randn(hidden_size, generator=gen, device=dev) for _ in range(L)]
+    device, wall = measure(lambda: [
+        (lambda l=l: vjp.pre_gradient(posts[l], o_weights[l], 32, 128)) for l in range(L)], L)
+    out["pre_gradient"] = _op_line("Llama-3.1-8B layer: post @ o_proj [4096, 4096] bf16", L,
+                                   device, hidden_size * hidden_size * 2 + 3 * hidden_size * 4,
+                                   wall)
+    del head, logits, o_weights
+
     # query history (history.py:21-38,51-63): one decode step's queries of all 32 layers
     # (Hq 32, d128, bf16) into the device ring, one launch per step
     from code_for_iclr27_amd.history import QueryHistory

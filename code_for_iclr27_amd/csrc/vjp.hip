@@ -9,11 +9,13 @@
 // weight chunks (written and re-read) and the [rows, V] probability matrix.
 //   head_logits_kernel   Y[r, v] = sum_d X[r, d] * W[v, d] (+ b[v]); a wave owns 4 rows of W,
 //                        lanes split D (16 B loads), X staged in LDS, one wave reduction per row.
-//   margin_stats_kernel  per logits row: target (given, or the first argmax), competitor max M,
-//                        competitor sum S = sum_{v != t} exp(l_v - M), margin l_t - (M + log S).
+//   margin stats         per logits row: target (given, or the first argmax), competitor max M,
+//                        competitor sum S = sum_{v != t} exp(l_v - M), margin l_t - (M + log S)
+//                        (three launches over 4096-logit chunks).
 //   row_sum_kernel       Z_blk[r, :] = sum_{v in blk} c[r, v] * W[v, :] over a block of rows of
 //                        W, with c = softmax over the competitors (exp(l - M) / S, 0 at the
-//                        target) or a given coefficient vector; one thread per 8 columns.
+//                        target) or a given coefficient vector; one thread per 8 columns of
+//                        a 2048-column block, 8 rows of W in flight per thread.
 //   row_sum_reduce_kernel  the blocks' partials summed in a fixed order, then
 //                        out = (base - Z) * due (hidden gradient, base = W[target]) or
 //                        out = Z * gate (pre-projection gradient).
@@ -32,7 +34,6 @@ constexpr int kLogitThreads = 256;
 constexpr int kLogitRowsPerWave = 4;
 constexpr int kLogitRowsPerBlock = kLogitRowsPerWave * (kLogitThreads / 64);
 constexpr int kLogitLdsFloats = 16384;  // X rows staged per launch: rows * D <= this (64 KB)
-constexpr int kStatThreads = 1024;
 constexpr int kReduceThreads = 1024;
 constexpr int kReduceColumns = 64;
 
@@ -127,75 +128,177 @@ __global__ __launch_bounds__(kLogitThreads) void head_logits_kernel(
   }
 }
 
-// (value, index) pairs reduced across the block: larger value wins, ties to the lower index.
-__device__ __forceinline__ void better(float& value, int64_t& index, float v2, int64_t i2) {
-  if (v2 > value || (v2 == value && i2 < index)) {
-    value = v2;
-    index = i2;
+// Per-thread top-two state: the best (value, index), larger value first and ties to the lower
+// index, and the largest value at any other index.
+struct TopTwo {
+  float v1;
+  int64_t i1;
+  float v2;
+};
+
+__device__ __forceinline__ void top_two_add(TopTwo& s, float v, int64_t i) {
+  if (v > s.v1 || (v == s.v1 && i < s.i1)) {
+    s.v2 = fmaxf(s.v2, s.v1);
+    s.v1 = v;
+    s.i1 = i;
+  } else {
+    s.v2 = fmaxf(s.v2, v);
   }
 }
 
-// grid: one block per logits row.
-__global__ __launch_bounds__(kStatThreads) void margin_stats_kernel(
-    const float* __restrict__ logits, int64_t vocab, const int64_t* __restrict__ targets_in,
-    int64_t* __restrict__ targets_out, float* __restrict__ margins, float* __restrict__ stats) {
-  __shared__ float red_v[kStatThreads / 64];
-  __shared__ int64_t red_i[kStatThreads / 64];
-  __shared__ int64_t target_s;
-  __shared__ float max_s;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int64_t r = blockIdx.x;
+__device__ __forceinline__ void top_two_merge(TopTwo& s, const TopTwo& o) {
+  if (o.v1 > s.v1 || (o.v1 == s.v1 && o.i1 < s.i1)) {
+    s.v2 = fmaxf(fmaxf(s.v2, s.v1), o.v2);
+    s.v1 = o.v1;
+    s.i1 = o.i1;
+  } else {
+    s.v2 = fmaxf(fmaxf(s.v2, o.v1), o.v2);
+  }
+}
+
+// Margin statistics in three short launches over chunks of kStatChunk logits (a single block
+// per row is latency-bound at vocab 128K):
+//   chunk_top_kernel    per (row, chunk): the top-two state (argmax mode) or, with a given
+//                       target, that target's logit and the max of the chunk's other logits;
+//   chunk_sum_kernel    per (row, chunk): every block merges the row's chunk states in chunk
+//                       order (target t, competitor max M), then sums exp(l - M) over the
+//                       chunk's logits other than t;
+//   margin_finish_kernel  per row: the same merge, the chunk sums in chunk order, the margin.
+constexpr int kStatChunk = 4096;
+constexpr int kStatBlock = 256;
+
+__device__ __forceinline__ void visit_logit(TopTwo& st, float value, int64_t i, int64_t given) {
+  if (given >= 0) {
+    if (i == given) {
+      st.v1 = value;
+      st.i1 = i;
+    } else {
+      st.v2 = fmaxf(st.v2, value);
+    }
+  } else {
+    top_two_add(st, value, i);
+  }
+}
+
+__device__ __forceinline__ void merge_state(TopTwo& st, const TopTwo& o, int64_t given) {
+  if (given >= 0) {
+    if (o.i1 == given) {
+      st.v1 = o.v1;
+      st.i1 = o.i1;
+    }
+    st.v2 = fmaxf(st.v2, o.v2);
+  } else {
+    top_two_merge(st, o);
+  }
+}
+
+// Block-wide merge of per-thread states; the result is returned to every thread.
+__device__ TopTwo block_merge(TopTwo st, int64_t given, TopTwo* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const TopTwo o{__shfl_xor(st.v1, offset), __shfl_xor(st.i1, offset), __shfl_xor(st.v2, offset)};
+    merge_state(st, o, given);
+  }
+  __syncthreads();
+  if (lane == 0) scratch[wave] = st;
+  __syncthreads();
+  TopTwo total = scratch[0];
+  for (int w = 1; w < kStatBlock / 64; ++w) merge_state(total, scratch[w], given);
+  return total;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = scratch[0];
+  for (int w = 1; w < kStatBlock / 64; ++w) total += scratch[w];
+  return total;
+}
+
+// The row's chunk states merged in chunk order (threads take chunks tid, tid + 256, ...).
+__device__ TopTwo merge_chunks(const TopTwo* states, int64_t chunks, int64_t vocab, int64_t given,
+                               TopTwo* scratch) {
+  constexpr float kNegInf = -__builtin_huge_valf();
+  TopTwo st{kNegInf, vocab, kNegInf};
+  for (int64_t c = threadIdx.x; c < chunks; c += kStatBlock) merge_state(st, states[c], given);
+  TopTwo total = block_merge(st, given, scratch);
+  if (given >= 0) total.i1 = given;
+  return total;
+}
+
+__global__ __launch_bounds__(kStatBlock) void chunk_top_kernel(
+    const float* __restrict__ logits, int64_t vocab, const int64_t* __restrict__ targets,
+    TopTwo* __restrict__ states, int64_t chunks) {
+  __shared__ TopTwo scratch[kStatBlock / 64];
+  constexpr float kNegInf = -__builtin_huge_valf();
+  const int64_t r = blockIdx.y, c = blockIdx.x;
+  const int64_t given = targets ? targets[r] : -1;
   const float* row = logits + r * vocab;
-  int64_t target;
-  if (targets_in) {
-    target = targets_in[r];
-  } else {  // torch.argmax: the first index of the largest value
-    float best = -__builtin_huge_valf();
-    int64_t at = vocab;
-    for (int64_t v = tid; v < vocab; v += kStatThreads) better(best, at, row[v], v);
-    for (int offset = 32; offset > 0; offset >>= 1)
-      better(best, at, __shfl_xor(best, offset), __shfl_xor(at, offset));
-    if (lane == 0) {
-      red_v[wave] = best;
-      red_i[wave] = at;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < kStatThreads / 64; ++w) better(best, at, red_v[w], red_i[w]);
-      target_s = at < vocab ? at : 0;
-    }
-    __syncthreads();
-    target = target_s;
+  const int64_t begin = c * kStatChunk, end = begin + kStatChunk < vocab ? begin + kStatChunk : vocab;
+  TopTwo st{kNegInf, vocab, kNegInf};
+  constexpr int kPer = kStatChunk / kStatBlock;
+  if (end - begin == kStatChunk) {  // whole chunk: every load issued before use
+    float v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) v[u] = row[begin + threadIdx.x + u * kStatBlock];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) visit_logit(st, v[u], begin + threadIdx.x + u * kStatBlock, given);
+  } else {
+    for (int64_t i = begin + threadIdx.x; i < end; i += kStatBlock) visit_logit(st, row[i], i, given);
   }
-  // Competitor max, then the competitor exp-sum against it.
-  float mx = -__builtin_huge_valf();
-  for (int64_t v = tid; v < vocab; v += kStatThreads)
-    if (v != target) mx = fmaxf(mx, row[v]);
-  for (int offset = 32; offset > 0; offset >>= 1) mx = fmaxf(mx, __shfl_xor(mx, offset));
-  __syncthreads();
-  if (lane == 0) red_v[wave] = mx;
-  __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < kStatThreads / 64; ++w) mx = fmaxf(mx, red_v[w]);
-    max_s = mx;
-  }
-  __syncthreads();
-  mx = max_s;
+  const TopTwo total = block_merge(st, given, scratch);
+  if (threadIdx.x == 0) states[r * chunks + c] = total;
+}
+
+__global__ __launch_bounds__(kStatBlock) void chunk_sum_kernel(
+    const float* __restrict__ logits, int64_t vocab, const int64_t* __restrict__ targets,
+    const TopTwo* __restrict__ states, int64_t chunks, float* __restrict__ sums) {
+  __shared__ TopTwo scratch[kStatBlock / 64];
+  __shared__ float sum_scratch[kStatBlock / 64];
+  const int64_t r = blockIdx.y, c = blockIdx.x;
+  const int64_t given = targets ? targets[r] : -1;
+  const TopTwo total = merge_chunks(states + r * chunks, chunks, vocab, given, scratch);
+  const int64_t target = total.i1;
+  const float mx = total.v2;
+  const float* row = logits + r * vocab;
+  const int64_t begin = c * kStatChunk, end = begin + kStatChunk < vocab ? begin + kStatChunk : vocab;
   float sum = 0.f;
-  for (int64_t v = tid; v < vocab; v += kStatThreads)
-    if (v != target) sum += expf(row[v] - mx);
-  for (int offset = 32; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset);
-  __syncthreads();
-  if (lane == 0) red_v[wave] = sum;
-  __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < kStatThreads / 64; ++w) sum += red_v[w];
-    const bool valid = target >= 0 && target < vocab;
-    margins[r] = valid ? row[target] - (mx + logf(sum)) : __builtin_nanf("");
-    stats[2 * r] = mx;
-    stats[2 * r + 1] = sum;
-    if (targets_out) targets_out[r] = target;
+  constexpr int kPer = kStatChunk / kStatBlock;
+  if (end - begin == kStatChunk) {
+    float v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) v[u] = row[begin + threadIdx.x + u * kStatBlock];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      sum += begin + threadIdx.x + u * kStatBlock == target ? 0.f : expf(v[u] - mx);
+  } else {
+    for (int64_t i = begin + threadIdx.x; i < end; i += kStatBlock)
+      if (i != target) sum += expf(row[i] - mx);
   }
+  sum = block_sum(sum, sum_scratch);
+  if (threadIdx.x == 0) sums[r * chunks + c] = sum;
+}
+
+__global__ __launch_bounds__(kStatBlock) void margin_finish_kernel(
+    int64_t vocab, const int64_t* __restrict__ targets, const TopTwo* __restrict__ states,
+    const float* __restrict__ sums, int64_t chunks, int64_t* __restrict__ targets_out,
+    float* __restrict__ margins, float* __restrict__ stats) {
+  __shared__ TopTwo scratch[kStatBlock / 64];
+  const int64_t r = blockIdx.x;
+  const int64_t given = targets ? targets[r] : -1;
+  const TopTwo total = merge_chunks(states + r * chunks, chunks, vocab, given, scratch);
+  if (threadIdx.x != 0) return;
+  float sum = 0.f;
+  for (int64_t c = 0; c < chunks; ++c) sum += sums[r * chunks + c];
+  const int64_t target = total.i1;
+  const bool valid = target >= 0 && target < vocab;
+  margins[r] = valid ? total.v1 - (total.v2 + logf(sum)) : __builtin_nanf("");
+  stats[2 * r] = total.v2;
+  stats[2 * r + 1] = sum;
+  if (targets_out) targets_out[r] = target;
 }
 
 struct RowSumArgs {
@@ -212,14 +315,20 @@ struct RowSumArgs {
   float* partial;             // [blocks, rows, dim]
 };
 
-// grid: ceil(vocab / rows_per_block) blocks of dim / 8 threads (<= 1024).
+// grid: (ceil(dim / 2048) column blocks, ceil(vocab / rows_per_block) row blocks) of 256
+// threads; thread t owns columns 8t .. 8t + 7 of its column block. kRowUnroll rows of W are
+// loaded before they are used.
+constexpr int kRowSumThreads = 256;
+constexpr int kRowSumColumns = 8 * kRowSumThreads;
+constexpr int kRowUnroll = 8;
+
 template <typename T, int RP>
-__global__ __launch_bounds__(1024) void row_sum_kernel(RowSumArgs a) {
+__global__ __launch_bounds__(kRowSumThreads) void row_sum_kernel(RowSumArgs a) {
   extern __shared__ float coef[];  // [rows_per_block][RP]
   const int tid = threadIdx.x;
-  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_block;
+  const int64_t v0 = static_cast<int64_t>(blockIdx.y) * a.rows_per_block;
   const int64_t count = a.vocab - v0 < a.rows_per_block ? a.vocab - v0 : a.rows_per_block;
-  for (int64_t i = tid; i < a.rows_per_block * RP; i += blockDim.x) {
+  for (int64_t i = tid; i < a.rows_per_block * RP; i += kRowSumThreads) {
     const int64_t k = i / RP, r = i - k * RP;
     float c = 0.f;
     if (k < count && r < a.rows) {
@@ -234,34 +343,42 @@ __global__ __launch_bounds__(1024) void row_sum_kernel(RowSumArgs a) {
     coef[i] = c;
   }
   __syncthreads();
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * kRowSumColumns + 8 * tid;
+  if (col >= a.dim) return;  // no barrier follows
   const T* weight = static_cast<const T*>(a.weight);
-  const int64_t col = 8 * static_cast<int64_t>(tid);
   float acc[RP][8];
 #pragma unroll
   for (int r = 0; r < RP; ++r)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
-  constexpr int kUnroll = 4;
-  for (int64_t k = 0; k < count; k += kUnroll) {
-    float w[kUnroll][8];
+  // Whole groups of kRowUnroll rows with no per-row branch (a load under a branch is waited
+  // for inside it), then the remaining rows one by one.
+  int64_t k = 0;
+  for (; k + kRowUnroll <= count; k += kRowUnroll) {
+    float w[kRowUnroll][8];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t v = v0 + (k + u < count ? k + u : count - 1);  // clamped; coefficient 0
-      load8<T>(weight + v * a.dim + col, w[u]);
-    }
+    for (int u = 0; u < kRowUnroll; ++u) load8<T>(weight + (v0 + k + u) * a.dim + col, w[u]);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (k + u >= count) break;
+    for (int u = 0; u < kRowUnroll; ++u)
 #pragma unroll
       for (int r = 0; r < RP; ++r) {
         const float c = coef[(k + u) * RP + r];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][e] = __builtin_fmaf(c, w[u][e], acc[r][e]);
       }
+  }
+  for (; k < count; ++k) {
+    float w[8];
+    load8<T>(weight + (v0 + k) * a.dim + col, w);
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+      const float c = coef[k * RP + r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[r][e] = __builtin_fmaf(c, w[e], acc[r][e]);
     }
   }
   for (int r = 0; r < RP && r < a.rows; ++r) {
-    float* p = a.partial + (static_cast<int64_t>(blockIdx.x) * a.rows + r) * a.dim + col;
+    float* p = a.partial + (static_cast<int64_t>(blockIdx.y) * a.rows + r) * a.dim + col;
     *reinterpret_cast<vjp_f32x4*>(p) = vjp_f32x4{acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
     *reinterpret_cast<vjp_f32x4*>(p + 4) = vjp_f32x4{acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
   }
@@ -319,9 +436,13 @@ int dispatch_weight(int dtype, F&& f) {
 
 int row_pass(int64_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
 
-int64_t rows_per_block(int64_t vocab) {
-  const int64_t per = std::min<int64_t>(256, std::max<int64_t>(8, ceil_div(vocab, 512)));
-  return ceil_div(per, 4) * 4;
+// Rows of W per block: enough blocks to fill the chip (about 1024), but at least 32 rows per
+// coefficient row so that the f32 partials stay a few percent of the weight bytes.
+int64_t rows_per_block(int64_t vocab, int64_t dim, int64_t rows_pass) {
+  const int64_t column_blocks = ceil_div(dim, kRowSumColumns);
+  const int64_t row_blocks = std::max<int64_t>(1, 1024 / column_blocks);
+  const int64_t per = std::max<int64_t>(32 * rows_pass, ceil_div(vocab, row_blocks));
+  return ceil_div(std::min<int64_t>(per, std::max<int64_t>(vocab, 1)), 4) * 4;
 }
 
 int check_weight(int dtype, int64_t vocab, int64_t dim, const void* weight) {
@@ -378,21 +499,44 @@ extern "C" int lr_head_logits(const float* hidden, int64_t rows, const void* wei
   return LR_OK;
 }
 
+extern "C" size_t lr_margin_stats_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  const int64_t chunks = ceil_div(vocab, kStatChunk);
+  return static_cast<size_t>(rows * chunks) * (sizeof(TopTwo) + sizeof(float));
+}
+
 extern "C" int lr_margin_stats(const float* logits, int64_t rows, int64_t vocab,
                                const int64_t* targets, int64_t* targets_out, float* margins,
-                               float* stats, void* stream) {
+                               float* stats, void* workspace, size_t workspace_size,
+                               void* stream) {
   clear_error();
   LR_REQUIRE(rows > 0 && vocab > 1 && logits && margins && stats, "Invalid logits");
-  hipLaunchKernelGGL(margin_stats_kernel, dim3(static_cast<unsigned>(rows)), dim3(kStatThreads), 0,
-                     as_stream(stream), logits, vocab, targets, targets_out, margins, stats);
+  LR_REQUIRE(rows < 65536, "Too many logits rows");
+  LR_REQUIRE(workspace && workspace_size >= lr_margin_stats_workspace_bytes(rows, vocab) &&
+                 reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+             "Margin workspace too small");
+  const int64_t chunks = ceil_div(vocab, kStatChunk);
+  TopTwo* states = static_cast<TopTwo*>(workspace);
+  float* sums = reinterpret_cast<float*>(states + rows * chunks);
+  const hipStream_t s = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
+  hipLaunchKernelGGL(chunk_top_kernel, grid, dim3(kStatBlock), 0, s, logits, vocab, targets,
+                     states, chunks);
+  if (int status = check_launch("margin_stats")) return status;
+  hipLaunchKernelGGL(chunk_sum_kernel, grid, dim3(kStatBlock), 0, s, logits, vocab, targets,
+                     states, chunks, sums);
+  if (int status = check_launch("margin_stats")) return status;
+  hipLaunchKernelGGL(margin_finish_kernel, dim3(static_cast<unsigned>(rows)), dim3(kStatBlock), 0,
+                     s, vocab, targets, states, sums, chunks, targets_out, margins, stats);
   return check_launch("margin_stats");
 }
 
 extern "C" size_t lr_row_sum_workspace_bytes(int64_t rows, int64_t vocab, int64_t dim) {
   if (rows <= 0 || vocab <= 0 || dim <= 0) return 0;
-  const int64_t blocks = ceil_div(vocab, rows_per_block(vocab));
-  return static_cast<size_t>(blocks) * static_cast<size_t>(std::min<int64_t>(rows, 8)) *
-         static_cast<size_t>(dim) * sizeof(float);
+  const int64_t pass = std::min<int64_t>(rows, 8);
+  const int64_t blocks = ceil_div(vocab, rows_per_block(vocab, dim, row_pass(pass)));
+  return static_cast<size_t>(blocks) * static_cast<size_t>(pass) * static_cast<size_t>(dim) *
+         sizeof(float);
 }
 
 namespace lr {
@@ -402,14 +546,14 @@ int weighted_rows(const void* weight, int dtype, int64_t vocab, int64_t dim, int
                   const float* logits, const float* stats, const int64_t* targets,
                   const float* coefficients, const float* due, const float* gate, float* out,
                   void* workspace, size_t workspace_size, hipStream_t stream) {
-  const int64_t per_block = rows_per_block(vocab);
-  const int64_t blocks = ceil_div(vocab, per_block);
   LR_REQUIRE(workspace && workspace_size >= lr_row_sum_workspace_bytes(rows, vocab, dim),
              "Row-sum workspace too small");
   LR_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "Workspace must be 16-byte aligned");
   for (int64_t r0 = 0; r0 < rows; r0 += 8) {
     const int64_t here = std::min<int64_t>(8, rows - r0);
     const int rp = row_pass(here);
+    const int64_t per_block = rows_per_block(vocab, dim, rp);
+    const int64_t blocks = ceil_div(vocab, per_block);
     RowSumArgs args{};
     args.weight = weight;
     args.vocab = vocab;
@@ -422,11 +566,11 @@ int weighted_rows(const void* weight, int dtype, int64_t vocab, int64_t dim, int
     args.coefficients = coefficients ? coefficients + r0 * vocab : nullptr;
     args.partial = static_cast<float*>(workspace);
     const size_t lds = static_cast<size_t>(per_block) * rp * sizeof(float);
-    const unsigned threads = static_cast<unsigned>(dim / 8);
+    const dim3 grid(static_cast<unsigned>(ceil_div(dim, kRowSumColumns)),
+                    static_cast<unsigned>(blocks));
     int status = dispatch_weight(dtype, [&]<typename T>() {
       auto launch = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), lds, stream,
-                           args);
+        hipLaunchKernelGGL(kernel, grid, dim3(kRowSumThreads), lds, stream, args);
         return check_launch("row_sum");
       };
       switch (rp) {

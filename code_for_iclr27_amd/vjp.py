@@ -49,8 +49,11 @@ def _stats(logits: torch.Tensor, targets: torch.Tensor | None):
     margins = torch.empty(rows, dtype=torch.float32, device=device)
     stats = torch.empty((rows, 2), dtype=torch.float32, device=device)
     chosen = torch.empty(rows, dtype=torch.int64, device=device)
+    size = _lib.load().lr_margin_stats_workspace_bytes(rows, vocab)
+    workspace = torch.empty(max(size, 16), dtype=torch.uint8, device=device)
     _lib.call("lr_margin_stats", logits.data_ptr(), rows, vocab, _lib.ptr(targets),
-              chosen.data_ptr(), margins.data_ptr(), stats.data_ptr(), _lib.stream_of(logits))
+              chosen.data_ptr(), margins.data_ptr(), stats.data_ptr(), workspace.data_ptr(),
+              workspace.numel(), _lib.stream_of(logits))
     return margins, chosen, stats
 
 

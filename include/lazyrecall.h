@@ -306,9 +306,12 @@ int lr_head_logits(const float* hidden, int64_t rows, const void* weight, const 
  * batch_audit.py:11-15): per logits row r ([rows, vocab] f32), the target t = targets[r]
  * (device i64, or NULL: the first argmax), the competitor max M = max_{v != t} l_v and sum
  * S = sum_{v != t} exp(l_v - M); margins[r] = l_t - (M + log S), stats[r] = (M, S). targets_out
- * (may be NULL) receives t. */
+ * (may be NULL) receives t. workspace: device scratch of lr_margin_stats_workspace_bytes bytes,
+ * 16-byte aligned, no initial contents. */
+size_t lr_margin_stats_workspace_bytes(int64_t rows, int64_t vocab);
 int lr_margin_stats(const float* logits, int64_t rows, int64_t vocab, const int64_t* targets,
-                    int64_t* targets_out, float* margins, float* stats, void* stream);
+                    int64_t* targets_out, float* margins, float* stats, void* workspace,
+                    size_t workspace_size, void* stream);
 
 /* Workspace of lr_hidden_gradient / lr_pre_gradient (device, 16-byte aligned, no contents). */
 size_t lr_row_sum_workspace_bytes(int64_t rows, int64_t vocab, int64_t dim);
