@@ -1,5 +1,6 @@
-"""Build liblazyrecall_hip.so (gfx950) from csrc/*.hip with hipcc, and the host planner
-module _plan from csrc/host_plan.cpp with g++ against torch's headers.
+"""Build liblazyrecall_hip.so (gfx950) from csrc/*.hip with hipcc, the host planner module
+_plan from csrc/host_plan.cpp with g++ against torch's headers, and the recall archive
+liblazyrecall_archive.so from csrc/archive.cpp with g++.
 
 Run as ``python -m code_for_iclr27_amd.build``. Each translation unit is compiled in parallel,
 then linked into ``code_for_iclr27_amd/liblazyrecall_hip.so`` next to this file; the planner
@@ -84,6 +85,21 @@ def build_host_plan(verbose: bool = False) -> Path:
     return target
 
 
+ARCHIVE = PACKAGE_DIR / "liblazyrecall_archive.so"
+
+
+def build_archive(verbose: bool = False) -> Path:
+    """The recall archive (host C++, no GPU code, no torch): liblazyrecall_archive.so."""
+    temporary = ARCHIVE.with_suffix(".so.tmp")
+    command = ["g++", "-O3", "-std=c++17", "-march=x86-64-v3", "-shared", "-fPIC", "-pthread",
+               "-Wall", str(SOURCE_DIR / "archive.cpp"), "-o", str(temporary)]
+    if verbose:
+        print(" ".join(command), flush=True)
+    _run(command)
+    os.replace(temporary, ARCHIVE)
+    return ARCHIVE
+
+
 def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     sources = sorted(SOURCE_DIR.glob("*.hip"))
@@ -103,8 +119,10 @@ def build(verbose: bool = False) -> Path:
     workers = min(len(sources) + 1, max(1, (os.cpu_count() or 4)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         planner = pool.submit(build_host_plan, verbose)
+        archive = pool.submit(build_archive, verbose)
         list(pool.map(compile_one, zip(sources, objects)))
         planner.result()
+        archive.result()
     temporary = LIBRARY.with_suffix(".so.tmp")
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(temporary),
             *map(str, objects)]

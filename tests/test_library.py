@@ -101,3 +101,14 @@ def test_step_sync_requires_a_pending_step():
     sync = scoring._planner().StepSync()
     with pytest.raises(RuntimeError, match="no audit step is pending"):
         sync.wait(True)
+
+
+def test_archive_library_exports_every_declared_symbol():
+    from code_for_iclr27_amd import archive
+
+    text = (HEADER.parent / "lazyrecall_archive.h").read_text()
+    declared = sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(lra_\w+)\s*\(", text, re.M)))
+    assert declared == sorted(archive.SIGNATURES)
+    library = archive.load()
+    for name in declared:
+        assert hasattr(library, name), name
