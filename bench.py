@@ -477,6 +477,42 @@ def ops_bench(torch, seed, reps=5):
         "add_ms": round(add_ms, 1), "rows": int(L * H * rows_per_head)}
     del archive, bits
 
+    # recall transport round trip (transport.py:129-307): one eviction batch of 2048 rows
+    # (evict_interval 8 x 32 layers x 8 heads) packed, copied out and archived, then one search
+    # of 256 group-mean queries, its 1024 results back in HBM
+    from code_for_iclr27_amd.transport import RecallTransport
+    cache = SimpleNamespace(
+        key_cache=[randn(rows, d) for _ in range(L)], value_cache=[randn(rows, d) for _ in range(L)],
+        position_cache=[torch.arange(rows, dtype=torch.float32, device=dev)[:, None]] * L,
+        metadata_list=[SimpleNamespace(head_lens_cpu=[T] * H)] * L)
+    blocks = [SimpleNamespace(self_attn=SimpleNamespace(_last_query_states=randn(1, 4 * H, 1, d)))
+              for _ in range(L)]
+    model = SimpleNamespace(model=SimpleNamespace(layers=blocks))
+    transport = RecallTransport(L, H, 4 * H, d, search_interval=1, topk=4, archive_buffers=4,
+                                cpu_threads=threads)
+    archive_ms, search_ms = [], []
+    for rep in range(reps):
+        removals = {(l, h): list(rng.choice(T, 8, replace=False)) for l in range(L) for h in range(H)}
+        torch.cuda.synchronize()
+        started = time.perf_counter()
+        transport.record_evicted(cache, removals)
+        transport.wait_pending()
+        archive_ms.append((time.perf_counter() - started) * 1e3)
+        started = time.perf_counter()
+        transport.step(model, cache, rep + 1)
+        transport.wait_pending()
+        ready = transport.ready_result()
+        search_ms.append((time.perf_counter() - started) * 1e3)
+        transport.release_result(ready[0])
+    transport.finish()
+    out["recall_transport"] = {
+        "workload": "cfg1: 2048 evicted rows per batch archived; 256 queries, top-4 per head",
+        "archive_batch_ms": round(float(np.median(archive_ms)), 3),
+        "search_round_trip_ms": round(float(np.median(search_ms)), 3),
+        "indexed": transport.counters["indexed_vectors"], "cpu_threads": threads}
+    transport.close()
+    del cache, blocks, transport
+
     # query history (history.py:21-38,51-63): one decode step's queries of all 32 layers
     # (Hq 32, d128, bf16) into the device ring, one launch per step
     from code_for_iclr27_amd.history import QueryHistory
