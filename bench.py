@@ -445,6 +445,11 @@ def ops_bench(torch, seed, reps=5):
     out["pre_gradient"] = _op_line("Llama-3.1-8B layer: post @ o_proj [4096, 4096] bf16", L,
                                    device, hidden_size * hidden_size * 2 + 3 * hidden_size * 4,
                                    wall)
+    device, wall = measure(lambda: [
+        (lambda: vjp.pre_gradients(posts, o_weights, 32, 128)) for _ in range(4)], 1)
+    out["pre_gradients_all_layers"] = _op_line(
+        "Llama-3.1-8B: all 32 layers' post @ o_proj in one launch pair", 1, device,
+        L * (hidden_size * hidden_size * 2 + 3 * hidden_size * 4) + L * 32, wall)
     del head, logits, o_weights
 
     # recall archive (cpu_worker.py:17-137, host C++): exact-MIPS search of one query per

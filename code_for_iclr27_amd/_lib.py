@@ -71,12 +71,15 @@ SIGNATURES = {
     "lr_row_sum_workspace_bytes": [_I64, _I64, _I64],
     "lr_hidden_gradient": [_P, _P, _P, _I64, _P, _I64, _I64, _I, _P, _P, _P, _SZ, _P],
     "lr_pre_gradient": [_P, _P, _I64, _I64, _I, _P, _P, _P, _SZ, _P],
+    "lr_pre_gradient_layers_workspace_bytes": [_I64, _I64, _I64],
+    "lr_pre_gradient_layers": [_P, _I64, _I64, _I64, _I, _P, _SZ, _P],
 }
 _RESTYPES = {"lr_last_error": ctypes.c_char_p, "lr_score_workspace_bytes": ctypes.c_size_t,
              "lr_select_workspace_bytes": ctypes.c_size_t,
              "lr_packed_attention_workspace_bytes": ctypes.c_size_t,
              "lr_row_sum_workspace_bytes": ctypes.c_size_t,
-             "lr_margin_stats_workspace_bytes": ctypes.c_size_t}
+             "lr_margin_stats_workspace_bytes": ctypes.c_size_t,
+             "lr_pre_gradient_layers_workspace_bytes": ctypes.c_size_t}
 
 _library = None
 

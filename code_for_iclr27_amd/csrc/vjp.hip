@@ -312,7 +312,10 @@ struct RowSumArgs {
   const float* stats;
   const int64_t* targets;
   const float* coefficients;
-  float* partial;             // [blocks, rows, dim]
+  float* partial;             // [blocks, rows, dim] (per layer with a layer table)
+  // Several weights in one launch (blockIdx.z = layer): device [layers, 4] words (weight,
+  // coefficients, gate or 0, out); weight and coefficients above are then unused.
+  const int64_t* layer_table;
 };
 
 // grid: (ceil(dim / 2048) column blocks, ceil(vocab / rows_per_block) row blocks) of 256
@@ -326,6 +329,15 @@ template <typename T, int RP>
 __global__ __launch_bounds__(kRowSumThreads) void row_sum_kernel(RowSumArgs a) {
   extern __shared__ float coef[];  // [rows_per_block][RP]
   const int tid = threadIdx.x;
+  const void* weight_ptr = a.weight;
+  const float* coefficients = a.coefficients;
+  float* partial = a.partial;
+  if (a.layer_table) {
+    const int64_t* entry = a.layer_table + 4 * static_cast<int64_t>(blockIdx.z);
+    weight_ptr = reinterpret_cast<const void*>(entry[0]);
+    coefficients = reinterpret_cast<const float*>(entry[1]);
+    partial += static_cast<int64_t>(blockIdx.z) * gridDim.y * a.rows * a.dim;
+  }
   const int64_t v0 = static_cast<int64_t>(blockIdx.y) * a.rows_per_block;
   const int64_t count = a.vocab - v0 < a.rows_per_block ? a.vocab - v0 : a.rows_per_block;
   for (int64_t i = tid; i < a.rows_per_block * RP; i += kRowSumThreads) {
@@ -337,7 +349,7 @@ __global__ __launch_bounds__(kRowSumThreads) void row_sum_kernel(RowSumArgs a) {
         c = v == a.targets[r] ? 0.f
                               : expf(a.logits[r * a.vocab + v] - a.stats[2 * r]) / a.stats[2 * r + 1];
       } else {
-        c = a.coefficients[r * a.vocab + v];
+        c = coefficients[r * a.vocab + v];
       }
     }
     coef[i] = c;
@@ -345,7 +357,7 @@ __global__ __launch_bounds__(kRowSumThreads) void row_sum_kernel(RowSumArgs a) {
   __syncthreads();
   const int64_t col = static_cast<int64_t>(blockIdx.x) * kRowSumColumns + 8 * tid;
   if (col >= a.dim) return;  // no barrier follows
-  const T* weight = static_cast<const T*>(a.weight);
+  const T* weight = static_cast<const T*>(weight_ptr);
   float acc[RP][8];
 #pragma unroll
   for (int r = 0; r < RP; ++r)
@@ -378,7 +390,7 @@ __global__ __launch_bounds__(kRowSumThreads) void row_sum_kernel(RowSumArgs a) {
     }
   }
   for (int r = 0; r < RP && r < a.rows; ++r) {
-    float* p = a.partial + (static_cast<int64_t>(blockIdx.y) * a.rows + r) * a.dim + col;
+    float* p = partial + (static_cast<int64_t>(blockIdx.y) * a.rows + r) * a.dim + col;
     *reinterpret_cast<vjp_f32x4*>(p) = vjp_f32x4{acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
     *reinterpret_cast<vjp_f32x4*>(p + 4) = vjp_f32x4{acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
   }
@@ -390,10 +402,17 @@ template <typename T>
 __global__ __launch_bounds__(kReduceThreads) void row_sum_reduce_kernel(
     const float* __restrict__ partial, int64_t blocks, int64_t rows, int64_t dim,
     const T* __restrict__ weight, int64_t vocab, const int64_t* __restrict__ targets,
-    const float* __restrict__ due, const float* __restrict__ gate, float* __restrict__ out) {
+    const float* __restrict__ due, const float* __restrict__ gate, float* __restrict__ out,
+    const int64_t* __restrict__ layer_table) {
   constexpr int kGroups = kReduceThreads / kReduceColumns;
   __shared__ float sums[kGroups][kReduceColumns];
   const int tid = threadIdx.x, g = tid / kReduceColumns, c = tid - g * kReduceColumns;
+  if (layer_table) {  // blockIdx.z = layer: its partials, gate and output
+    const int64_t* entry = layer_table + 4 * static_cast<int64_t>(blockIdx.z);
+    partial += static_cast<int64_t>(blockIdx.z) * blocks * rows * dim;
+    gate = reinterpret_cast<const float*>(entry[2]);
+    out = reinterpret_cast<float*>(entry[3]);
+  }
   const int64_t r = blockIdx.y;
   const int64_t d = static_cast<int64_t>(blockIdx.x) * kReduceColumns + c;
   float s = 0.f;
@@ -588,7 +607,7 @@ int weighted_rows(const void* weight, int dtype, int64_t vocab, int64_t dim, int
                          dim3(kReduceThreads), 0, stream, static_cast<const float*>(workspace),
                          blocks, here, dim, static_cast<const T*>(weight), vocab,
                          targets ? targets + r0 : nullptr, due ? due + r0 : nullptr, gate,
-                         out + r0 * dim);
+                         out + r0 * dim, nullptr);
       return check_launch("row_sum_reduce");
     });
     if (status) return status;
@@ -618,4 +637,51 @@ extern "C" int lr_pre_gradient(const float* post_gradient, const void* o_weight,
   LR_REQUIRE(post_gradient && out, "Invalid gradient inputs");
   return weighted_rows(o_weight, dtype, hidden, width, 1, nullptr, nullptr, nullptr, post_gradient,
                        nullptr, gate, out, workspace, workspace_size, as_stream(stream));
+}
+
+extern "C" size_t lr_pre_gradient_layers_workspace_bytes(int64_t layers, int64_t hidden,
+                                                         int64_t width) {
+  if (layers <= 0) return 0;
+  return static_cast<size_t>(layers) * lr_row_sum_workspace_bytes(1, hidden, width);
+}
+
+extern "C" int lr_pre_gradient_layers(const int64_t* layer_table, int64_t layers, int64_t hidden,
+                                      int64_t width, int dtype, void* workspace,
+                                      size_t workspace_size, void* stream) {
+  clear_error();
+  LR_REQUIRE(dtype == LR_DTYPE_BF16 || dtype == LR_DTYPE_F16 || dtype == LR_DTYPE_F32,
+             "Weights must be float32, float16 or bfloat16");
+  LR_REQUIRE(hidden > 0 && width > 0 && width % 8 == 0, "Weight rows must be a multiple of 8 elements");
+  LR_REQUIRE(layer_table && layers > 0 && layers < 65536, "Invalid layer table");
+  LR_REQUIRE(workspace && workspace_size >= lr_pre_gradient_layers_workspace_bytes(layers, hidden, width) &&
+                 reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+             "Row-sum workspace too small");
+  const int64_t per_block = rows_per_block(hidden, width, 1);
+  const int64_t blocks = ceil_div(hidden, per_block);
+  RowSumArgs args{};
+  args.vocab = hidden;
+  args.dim = width;
+  args.rows = 1;
+  args.rows_per_block = per_block;
+  args.partial = static_cast<float*>(workspace);
+  args.layer_table = layer_table;
+  const hipStream_t s = as_stream(stream);
+  const size_t lds = static_cast<size_t>(per_block) * sizeof(float);
+  int status = dispatch_weight(dtype, [&]<typename T>() {
+    hipLaunchKernelGGL((row_sum_kernel<T, 1>),
+                       dim3(static_cast<unsigned>(ceil_div(width, kRowSumColumns)),
+                            static_cast<unsigned>(blocks), static_cast<unsigned>(layers)),
+                       dim3(kRowSumThreads), lds, s, args);
+    return check_launch("row_sum");
+  });
+  if (status) return status;
+  return dispatch_weight(dtype, [&]<typename T>() {
+    hipLaunchKernelGGL(row_sum_reduce_kernel<T>,
+                       dim3(static_cast<unsigned>(ceil_div(width, kReduceColumns)), 1u,
+                            static_cast<unsigned>(layers)),
+                       dim3(kReduceThreads), 0, s, static_cast<const float*>(workspace), blocks,
+                       int64_t{1}, width, static_cast<const T*>(nullptr), hidden, nullptr,
+                       nullptr, nullptr, nullptr, layer_table);
+    return check_launch("row_sum_reduce");
+  });
 }

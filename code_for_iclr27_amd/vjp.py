@@ -161,3 +161,39 @@ def pre_gradient(post_gradient: torch.Tensor, o_proj_weight: torch.Tensor, num_q
                   _lib.DTYPE_CODES[weight.dtype], _lib.ptr(gate), out.data_ptr(),
                   workspace.data_ptr(), workspace.numel(), _lib.stream_of(weight))
     return out.view(num_query_heads, head_dim)
+
+
+def pre_gradients(post_gradients, o_proj_weights, num_query_heads: int, head_dim: int,
+                  gates=None) -> list:
+    """The pre-projection gradient of every layer (the per-layer lines of scoring.py:228-237 over
+    all layers) in one launch pair: a list of f32 [Hq, d] tensors, layer by layer."""
+    layers = len(o_proj_weights)
+    _check(layers > 0 and len(post_gradients) == layers, "One post gradient per layer")
+    gates = [None] * layers if gates is None else list(gates)
+    _check(len(gates) == layers, "One gate (or None) per layer")
+    weights = [_weight(w) for w in o_proj_weights]
+    hidden, width = weights[0].shape
+    device, dtype = weights[0].device, weights[0].dtype
+    _check(all(w.shape == (hidden, width) and w.dtype == dtype and w.device == device
+               for w in weights), "Every o_proj must share shape, dtype and device")
+    _check(width == num_query_heads * head_dim, "o_proj width differs from Hq * head_dim")
+    posts = [p.detach().float().reshape(-1).contiguous() for p in post_gradients]
+    _check(all(p.numel() == hidden and p.device == device for p in posts),
+           "Post-projection gradient size differs")
+    gates = [None if g is None else g.detach().float().reshape(-1).contiguous() for g in gates]
+    _check(all(g is None or (g.numel() == width and g.device == device) for g in gates),
+           "Missing current Qwen3.5 attention output gate")
+    with torch.cuda.device(device):
+        out = torch.empty((layers, width), dtype=torch.float32, device=device)
+        table = torch.tensor([[w.data_ptr(), p.data_ptr(), 0 if g is None else g.data_ptr(),
+                               out[l].data_ptr()]
+                              for l, (w, p, g) in enumerate(zip(weights, posts, gates))],
+                             dtype=torch.int64).pin_memory().to(device, non_blocking=True)
+        size = _lib.load().lr_pre_gradient_layers_workspace_bytes(layers, hidden, width)
+        workspace = torch.empty(max(size, 16), dtype=torch.uint8, device=device)
+        _lib.call("lr_pre_gradient_layers", table.data_ptr(), layers, hidden, width,
+                  _lib.DTYPE_CODES[dtype], workspace.data_ptr(), workspace.numel(),
+                  _lib.stream_of(weights[0]))
+        # the table and the inputs stay referenced until the launch pair has run
+        out._lr_keepalive = (table, posts, gates, weights)
+    return [out[l].view(num_query_heads, head_dim) for l in range(layers)]

@@ -332,6 +332,16 @@ int lr_pre_gradient(const float* post_gradient, const void* o_weight, int64_t hi
                     int64_t width, int dtype, const float* gate, float* out, void* workspace,
                     size_t workspace_size, void* stream);
 
+/* The pre-projection gradients of several layers in one launch pair (the loop of
+ * src/lazy_recall/scoring.py:219-237 over layers; no single reference counterpart). layer_table:
+ * DEVICE [layers, 4] i64 = (o_weight [hidden, width] of `dtype`, post_gradient [hidden] f32,
+ * gate [width] f32 or 0, out [width] f32) per layer, all valid device addresses, weights 16-byte
+ * aligned; every layer shares hidden, width and dtype. */
+size_t lr_pre_gradient_layers_workspace_bytes(int64_t layers, int64_t hidden, int64_t width);
+int lr_pre_gradient_layers(const int64_t* layer_table, int64_t layers, int64_t hidden,
+                           int64_t width, int dtype, void* workspace, size_t workspace_size,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

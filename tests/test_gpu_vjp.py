@@ -113,3 +113,19 @@ def test_pre_gradient(device, hidden, width, dtype, gated):
     if gate is not None:
         scale = scale * np.abs(gate.double().numpy())
     assert np.all(np.abs(got.reshape(-1).cpu().numpy() - expect) <= 1e-5 * scale + 1e-6)
+
+
+@pytest.mark.parametrize("dtype,gated", [(torch.bfloat16, False), (torch.float32, True)])
+def test_pre_gradients_all_layers_match_per_layer(device, dtype, gated):
+    layers, hidden, heads, dim = 5, 2048, 16, 128
+    g = torch.Generator().manual_seed(21)
+    weights = [(torch.randn((hidden, heads * dim), generator=g) * 0.02).to(dtype).to(device)
+               for _ in range(layers)]
+    posts = [torch.randn(hidden, generator=g).to(device) for _ in range(layers)]
+    gates = [torch.rand(heads * dim, generator=g).to(device) if gated and l % 2 == 0 else None
+             for l in range(layers)]
+    batched = vjp.pre_gradients(posts, weights, heads, dim, gates)
+    for l in range(layers):
+        single = vjp.pre_gradient(posts[l], weights[l], heads, dim, gates[l])
+        assert batched[l].shape == (heads, dim)
+        torch.testing.assert_close(batched[l], single, rtol=0, atol=0)  # same kernels, same order
