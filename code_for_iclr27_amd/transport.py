@@ -158,23 +158,28 @@ class RecallTransport:
             self.pump()
             time.sleep(0.001)
         slot = self.archive_states.index("free")
-        cursor = 0
+        # Every layer's absolute rows and head ids in one host array, uploaded with one
+        # non-blocking copy from pinned memory (the reference uploads two tensors per layer).
+        plan = []
+        rows_all, heads_all = [], []
         for layer in sorted({layer for layer, _ in removals}):
             bounds = np.concatenate(([0], np.cumsum(cache.metadata_list[layer].head_lens_cpu)))
-            indices, head_ids = [], []
+            start = len(rows_all)
             for (record_layer, head), positions in sorted(removals.items()):
                 if record_layer == layer:
                     selected = sorted(set(int(position) for position in positions))
-                    indices.extend(int(bounds[head]) + position for position in selected)
-                    head_ids.extend([head] * len(selected))
-            if not indices:
-                continue
-            end = cursor + len(indices)
+                    rows_all.extend(int(bounds[head]) + position for position in selected)
+                    heads_all.extend([head] * len(selected))
+            if len(rows_all) > start:
+                plan.append((layer, start, len(rows_all)))
+        table = torch.tensor([rows_all, heads_all], dtype=torch.int64).pin_memory()
+        table = table.to("cuda", non_blocking=True)
+        cursor = 0
+        for layer, start, end in plan:
             _C.pack(cache.key_cache[layer].contiguous(), cache.value_cache[layer].contiguous(),
-                    cache.position_cache[layer].contiguous(),
-                    torch.tensor(indices, device="cuda", dtype=torch.int64),
-                    torch.tensor(head_ids, device="cuda", dtype=torch.int64), layer,
-                    self.archive_gpu[slot, cursor:end], self.archive_meta_gpu[slot, cursor:end])
+                    cache.position_cache[layer].contiguous(), table[0, start:end],
+                    table[1, start:end], layer, self.archive_gpu[slot, start:end],
+                    self.archive_meta_gpu[slot, start:end])
             cursor = end
         if cursor != count:
             raise AssertionError("Archive packing count mismatch")
