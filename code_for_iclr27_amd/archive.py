@@ -1,8 +1,8 @@
 """The recall worker's exact maximum-inner-product archive (``ArchiveIndex`` of
-src/lazy_recall/recall/cpu_worker.py:97-137, over ``HeadArchive`` :17-94) on the host, without
+src/lazy_recall/recall/cpu_worker.py:94-134, over ``HeadArchive`` :17-92) on the host, without
 faiss: liblazyrecall_archive.so (csrc/archive.cpp), loaded with ctypes. Same constructor,
 methods, properties, argument shapes, results and error messages as the reference class; the
-CPU worker process (cpu_worker.py:140-182) can construct it in place of its own.
+CPU worker process (cpu_worker.py:136-182) can construct it in place of its own.
 
 Equal inner products rank in the order the rows were indexed (the scan order of a faiss flat
 index); faiss itself leaves the order of exact ties unspecified.
@@ -53,7 +53,7 @@ def _raise(status: int) -> None:
 
 
 class ArchiveIndex:
-    """cpu_worker.py:97-137: one bounded exact-MIPS archive per (layer, KV head)."""
+    """cpu_worker.py:94-134: one bounded exact-MIPS archive per (layer, KV head)."""
 
     def __init__(self, layers, heads, dimension, threads, capacity):
         self.layers, self.heads, self.dimension = int(layers), int(heads), int(dimension)

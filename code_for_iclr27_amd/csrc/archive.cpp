@@ -1,5 +1,5 @@
 // CPU-owned bounded exact maximum-inner-product archive of evicted KV rows: the recall worker's
-// ArchiveIndex / HeadArchive (src/lazy_recall/recall/cpu_worker.py:17-133) without faiss.
+// ArchiveIndex / HeadArchive (src/lazy_recall/recall/cpu_worker.py:17-134) without faiss.
 //
 // Per (layer, KV head) segment the rows live in slot-indexed arrays: f32 keys [slots, dim] for
 // the inner products, the bf16 payload [slots, 2, dim], the position (identity, -1 = empty) and
@@ -65,7 +65,7 @@ struct Head {
     sequence.resize(static_cast<size_t>(length), 0);
   }
 
-  void remove(const int64_t* list, int64_t count) {  // cpu_worker.py:39-47
+  void remove(const int64_t* list, int64_t count) {  // cpu_worker.py:37-46
     for (int64_t i = 0; i < count; ++i) {
       const auto it = lookup.find(list[i]);
       if (it == lookup.end()) continue;
@@ -76,7 +76,7 @@ struct Head {
     }
   }
 
-  // cpu_worker.py:49-82. rows: indices into the batch arrays of this segment's rows.
+  // cpu_worker.py:48-82. rows: indices into the batch arrays of this segment's rows.
   void add(const std::vector<int64_t>& rows, const int64_t* metadata, const uint16_t* batch) {
     std::vector<int64_t> present;
     for (const int64_t row : rows) present.push_back(metadata[3 * row + 2]);

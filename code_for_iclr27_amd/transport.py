@@ -33,7 +33,7 @@ from .archive import ArchiveIndex
 
 
 def _worker(index, topk, views, commands, replies):
-    """cpu_worker.py:140-182 as a thread: the same commands and replies."""
+    """cpu_worker.py:136-182 as a thread: the same commands and replies."""
     try:
         while True:
             message = commands.get()
@@ -140,7 +140,7 @@ class RecallTransport:
 
     @torch.no_grad()
     def record_evicted(self, cache, removals):
-        """transport.py:129-177: gather {(layer, head): positions} into a free staging slot with
+        """transport.py:130-177: gather {(layer, head): positions} into a free staging slot with
         the pack kernel and start its copy to host memory."""
         self.pump()
         count = sum(len(set(positions)) for positions in removals.values())
@@ -194,7 +194,7 @@ class RecallTransport:
 
     @torch.no_grad()
     def pump(self):
-        """transport.py:179-228: advance every slot whose copy or worker job has finished."""
+        """transport.py:180-229: advance every slot whose copy or worker job has finished."""
         if self.closed:
             return
         if not self.thread.is_alive():
@@ -261,7 +261,7 @@ class RecallTransport:
                 self.query_states[slot] = "free"
 
     def ready_result(self):
-        """transport.py:242-256: the newest search result resident in HBM, older ones released:
+        """transport.py:243-258: the newest search result resident in HBM, older ones released:
         (slot, step, payload [n, 2, d] bf16, metadata [n, 3] i64 on the device, metadata host)."""
         self.pump()
         self.retire_finished()
@@ -297,7 +297,7 @@ class RecallTransport:
 
     @torch.no_grad()
     def step(self, model, cache, step):
-        """transport.py:279-307: every search_interval steps, submit one query per (layer, KV
+        """transport.py:277-301: every search_interval steps, submit one query per (layer, KV
         head): the mean over its query group of the last decode query."""
         del cache
         self.pump()

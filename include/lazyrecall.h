@@ -316,7 +316,7 @@ int lr_margin_stats(const float* logits, int64_t rows, int64_t vocab, const int6
 /* Workspace of lr_hidden_gradient / lr_pre_gradient (device, 16-byte aligned, no contents). */
 size_t lr_row_sum_workspace_bytes(int64_t rows, int64_t vocab, int64_t dim);
 
-/* one_vs_rest_hidden_gradient / row_hidden_gradients (src/lazy_recall/_core/scoring.py:55-76,
+/* one_vs_rest_hidden_gradient / row_hidden_gradients (src/lazy_recall/_core/scoring.py:54-76,
  * batch_audit.py:18-24): out[r, :] = (weight[t_r, :] - sum_v p[r, v] * weight[v, :]) * due[r],
  * p[r] the softmax of row r's logits with the target excluded (p = exp(l - M) / S from
  * lr_margin_stats' stats, 0 at t_r). due (may be NULL: 1) [rows] f32, out [rows, dim] f32. */
@@ -333,7 +333,7 @@ int lr_pre_gradient(const float* post_gradient, const void* o_weight, int64_t hi
                     size_t workspace_size, void* stream);
 
 /* The pre-projection gradients of several layers in one launch pair (the loop of
- * src/lazy_recall/scoring.py:219-237 over layers; no single reference counterpart). layer_table:
+ * src/lazy_recall/scoring.py:218-237 over layers; no single reference counterpart). layer_table:
  * DEVICE [layers, 4] i64 = (o_weight [hidden, width] of `dtype`, post_gradient [hidden] f32,
  * gate [width] f32 or 0, out [width] f32) per layer, all valid device addresses, weights 16-byte
  * aligned; every layer shares hidden, width and dtype. */

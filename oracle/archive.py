@@ -1,6 +1,6 @@
 """Oracle (test infrastructure only): the recall worker's bounded exact-MIPS archive.
 
-Restates HeadArchive and ArchiveIndex of src/lazy_recall/recall/cpu_worker.py:17-137 in plain
+Restates HeadArchive and ArchiveIndex of src/lazy_recall/recall/cpu_worker.py:17-134 in plain
 Python/numpy, with faiss IndexIDMap2(IndexFlatIP) replaced by what it computes: a list of
 (position, f32 key) in the order rows were added (removal keeps the others' order), searched by
 brute force for the largest inner products (computed in f64), equal products in list order.
@@ -17,7 +17,7 @@ def bf16_to_float32(values):
 
 
 class HeadArchive:
-    """cpu_worker.py:17-94."""
+    """cpu_worker.py:17-92."""
 
     def __init__(self, dimension, capacity):
         self.dimension, self.capacity = dimension, capacity
@@ -87,7 +87,7 @@ class HeadArchive:
 
 
 class ArchiveIndex:
-    """cpu_worker.py:97-137."""
+    """cpu_worker.py:94-134."""
 
     def __init__(self, layers, heads, dimension, capacity):
         self.layers, self.heads, self.dimension = layers, heads, dimension

@@ -1,5 +1,5 @@
 """The recall archive (liblazyrecall_archive.so through code_for_iclr27_amd.archive) against the
-oracle restatement of cpu_worker.py:17-137, and the oracle pinned by hand-worked answers.
+oracle restatement of cpu_worker.py:17-134, and the oracle pinned by hand-worked answers.
 
 Host code: these run without a GPU. Keys and queries with small integer entries make every inner
 product exact in f32 and f64, so search results (order included, ties in insertion order) are
