@@ -452,7 +452,7 @@ def ops_bench(torch, seed, reps=5):
         L * (hidden_size * hidden_size * 2 + 3 * hidden_size * 4) + L * 32, wall)
     del head, logits, o_weights
 
-    # recall archive (cpu_worker.py:17-137, host C++): exact-MIPS search of one query per
+    # recall archive (cpu_worker.py:17-134, host C++): exact-MIPS search of one query per
     # (layer, KV head) over 4096 archived keys per head, cfg1 shape, on the host's cores
     from code_for_iclr27_amd.archive import ArchiveIndex
     threads = len(os.sched_getaffinity(0))
