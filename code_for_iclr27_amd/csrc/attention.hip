@@ -21,6 +21,8 @@
 // workgroup's XCD, and measured 4-6x slower at the cfg2 decode shape.
 
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "lr_common.hpp"
 
@@ -498,14 +500,19 @@ extern "C" size_t lr_packed_attention_workspace_bytes(int64_t segments, int64_t 
   return workspace_bytes(plan_attention(segments, groups, length, max_keys, dim), dim);
 }
 
-extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
-                                   int64_t q_head_stride, int64_t q_query_stride,
-                                   const void* keys, const void* values, int64_t key_rows,
-                                   const int32_t* cu_seqlens_k, int64_t batch, int64_t kv_heads,
-                                   int64_t groups, int64_t length, int64_t dim, int dtype,
-                                   int64_t max_keys, float scale, void* out, void* workspace,
-                                   size_t workspace_size, void* stream) {
-  clear_error();
+namespace lr {
+namespace {
+
+// The checks and launches shared by lr_packed_attention and lr_packed_attention_noalloc.
+// `scratch_limit` is nonzero for the allocation-free variant: its workspace is the library's
+// fixed per-device array of that size, and a call that needs more is refused with its own
+// message before anything is enqueued.
+int packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head_stride,
+                     int64_t q_query_stride, const void* keys, const void* values,
+                     int64_t key_rows, const int32_t* cu_seqlens_k, int64_t batch,
+                     int64_t kv_heads, int64_t groups, int64_t length, int64_t dim, int dtype,
+                     int64_t max_keys, float scale, void* out, void* workspace,
+                     size_t workspace_size, size_t scratch_limit, void* stream) {
   LR_REQUIRE(dtype == LR_DTYPE_BF16 || dtype == LR_DTYPE_F16,
              "FlashAttention only supports fp16 and bf16 data type");
   LR_REQUIRE(dim == 64 || dim == 128 || dim == 256, "Head dimension must be 64, 128 or 256");
@@ -523,6 +530,12 @@ extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
   const int64_t segments = batch * kv_heads;
   const AttnPlan plan = plan_attention(segments, groups, length, max_keys, dim);
   const size_t needed = workspace_bytes(plan, dim);
+  if (scratch_limit) {
+    LR_REQUIRE(needed <= scratch_limit,
+               "Attention needs " + std::to_string(needed) +
+                   " bytes of scratch; the allocation-free entry point holds at most " +
+                   std::to_string(scratch_limit) + " bytes per device");
+  }
   LR_REQUIRE(workspace_size >= needed && (needed == 0 || workspace != nullptr),
              "Attention workspace too small");
   LR_REQUIRE(needed == 0 || reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
@@ -554,4 +567,91 @@ extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
   return dtype == LR_DTYPE_BF16
              ? launch_dim<__bf16>(args, dim, plan.rows_per_tile, blocks, s)
              : launch_dim<_Float16>(args, dim, plan.rows_per_tile, blocks, s);
+}
+
+// Workspace of the allocation-free entry point: one fixed array per device, held from the
+// library's load onto that device until the process ends. Host code never passes `scratch`
+// itself to a kernel (on the host the name is only a stand-in for the symbol); it passes the
+// device address hipGetSymbolAddress gives, looked up once per device.
+constexpr size_t kAttentionScratchBytes = size_t{16} << 20;
+__device__ __align__(256) unsigned char scratch[kAttentionScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+// The device address of `scratch` on the device that owns `stream` (the current device for the
+// null stream). The first call on a device makes that device current for the lookup and then
+// restores the caller's device.
+int scratch_address(hipStream_t stream, void** address) {
+  int device = 0;
+  if (stream != nullptr) {
+    LR_HIP_TRY(hipStreamGetDevice(stream, &device));
+  } else {
+    LR_HIP_TRY(hipGetDevice(&device));
+  }
+  LR_REQUIRE(device >= 0 && device < kMaxDevices, "Device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    int current = 0;
+    LR_HIP_TRY(hipGetDevice(&current));
+    if (current != device) LR_HIP_TRY(hipSetDevice(device));
+    void* found = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    if (current != device) LR_HIP_TRY(hipSetDevice(current));
+    if (status != hipSuccess || found == nullptr) {
+      (void)hipGetLastError();
+      set_error(std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(status));
+      return LR_ERR_HIP;
+    }
+    g_scratch_address[device] = found;
+  }
+  *address = g_scratch_address[device];
+  return LR_OK;
+}
+
+}  // namespace
+}  // namespace lr
+
+extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
+                                   int64_t q_head_stride, int64_t q_query_stride,
+                                   const void* keys, const void* values, int64_t key_rows,
+                                   const int32_t* cu_seqlens_k, int64_t batch, int64_t kv_heads,
+                                   int64_t groups, int64_t length, int64_t dim, int dtype,
+                                   int64_t max_keys, float scale, void* out, void* workspace,
+                                   size_t workspace_size, void* stream) {
+  clear_error();
+  return packed_attention(queries, q_batch_stride, q_head_stride, q_query_stride, keys, values,
+                          key_rows, cu_seqlens_k, batch, kv_heads, groups, length, dim, dtype,
+                          max_keys, scale, out, workspace, workspace_size, 0, stream);
+}
+
+extern "C" size_t lr_packed_attention_scratch_bytes(void) { return kAttentionScratchBytes; }
+
+extern "C" int lr_packed_attention_noalloc(const void* queries, int64_t q_batch_stride,
+                                           int64_t q_head_stride, int64_t q_query_stride,
+                                           const void* keys, const void* values,
+                                           int64_t key_rows, const int32_t* cu_seqlens_k,
+                                           int64_t batch, int64_t kv_heads, int64_t groups,
+                                           int64_t length, int64_t dim, int dtype,
+                                           int64_t max_keys, float scale, void* out,
+                                           void* stream) {
+  clear_error();
+  // The size check comes first and needs no HIP call; a call that needs no partial states
+  // (every segment within one key block) does not touch the scratch array at all.
+  const int64_t segments =
+      batch > 0 && kv_heads > 0 && batch <= (int64_t{1} << 31) / kv_heads ? batch * kv_heads : 0;
+  const size_t needed = lr_packed_attention_workspace_bytes(segments, groups, length, max_keys, dim);
+  LR_REQUIRE(needed <= kAttentionScratchBytes,
+             "Attention needs " + std::to_string(needed) +
+                 " bytes of scratch; the allocation-free entry point holds at most " +
+                 std::to_string(kAttentionScratchBytes) + " bytes per device");
+  void* workspace = nullptr;
+  if (needed) {
+    if (int status = scratch_address(as_stream(stream), &workspace)) return status;
+  }
+  return packed_attention(queries, q_batch_stride, q_head_stride, q_query_stride, keys, values,
+                          key_rows, cu_seqlens_k, batch, kv_heads, groups, length, dim, dtype,
+                          max_keys, scale, out, workspace, needed ? kAttentionScratchBytes : 0,
+                          kAttentionScratchBytes, stream);
 }

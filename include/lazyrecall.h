@@ -291,6 +291,25 @@ int lr_packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_h
                         int64_t max_keys, float scale, void* out, void* workspace,
                         size_t workspace_size, void* stream);
 
+/* Allocation-free packed attention. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, kernels and results as lr_packed_attention, without
+ * the workspace: the partial states live in one fixed array per device of
+ * lr_packed_attention_scratch_bytes() bytes (16 MiB), held from the library's first use on that
+ * device until the process ends. The call allocates and frees nothing. A call whose
+ * lr_packed_attention_workspace_bytes(...) exceeds that size returns LR_ERR_INVALID with a
+ * message naming both sizes, before anything is enqueued. Every call on one device shares that
+ * device's array and leaves its contents behind (none are needed at the next call): two calls
+ * that can overlap in time on one device (different streams without an order between them)
+ * race on it. The device is the one that owns `stream` (the current device for NULL). */
+size_t lr_packed_attention_scratch_bytes(void);
+int lr_packed_attention_noalloc(const void* queries, int64_t q_batch_stride,
+                                int64_t q_head_stride, int64_t q_query_stride, const void* keys,
+                                const void* values, int64_t key_rows,
+                                const int32_t* cu_seqlens_k, int64_t batch, int64_t kv_heads,
+                                int64_t groups, int64_t length, int64_t dim, int dtype,
+                                int64_t max_keys, float scale, void* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Audit vector-Jacobian helpers (the margin objective and its gradients)
  * ------------------------------------------------------------------------------------- */

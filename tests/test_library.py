@@ -40,6 +40,14 @@ def test_invalid_arguments_fail_on_host():
     assert library.lr_score_workspace_bytes(2, 4, 250, 1000) > 0
 
 
+def test_noalloc_attention_size_check_needs_no_gpu():
+    library = _lib.load()
+    assert library.lr_packed_attention_scratch_bytes() == 16 << 20
+    status = library.lr_packed_attention_noalloc(None, 0, 0, 0, None, None, 0, None, 1, 1, 1, 1,
+                                                 128, _lib.LR_DTYPE_BF16, 1 << 24, 0.1, None, None)
+    assert status == 1 and "holds at most 16777216 bytes" in _lib.last_error()
+
+
 def test_zero_work_calls_succeed_without_launching():
     library = _lib.load()
     assert library.lr_compact(None, None, None, 5, 8, 2, None, 5, None, None, None, None) == 0
