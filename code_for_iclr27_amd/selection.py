@@ -22,15 +22,28 @@ import torch
 from . import _C, _lib
 
 
+@dataclass(order=True)
+class KVReference:
+    """_core/scoring.py:214-219: one queued slot. Instances order by score, then layer, head and
+    position (dataclass field order), as the reference's."""
+    score: float
+    layer: int
+    head: int
+    position: int
+
+
 class ArrayReferences(Sequence):
-    """selection.py:8-39: parallel (score, segment, position) columns of a deletion queue."""
+    """The deletion-queue type of selection.py:8-39: three parallel columns in queue order (raw
+    score, score-segment id, position within the head) and the (layer, head) of every segment.
+    An integer index gives a ``KVReference``; a slice gives another queue over the same
+    segments."""
 
     def __init__(self, scores, segments, positions, coordinates):
         self.scores = np.asarray(scores)
         self.segments = np.asarray(segments, dtype=np.int64)
         self.positions = np.asarray(positions, dtype=np.int64)
         self.coordinates = np.asarray(coordinates, dtype=np.int64).reshape(-1, 2)
-        if len(self.scores) != len(self.segments) or len(self.scores) != len(self.positions):
+        if not len(self.scores) == len(self.segments) == len(self.positions):
             raise ValueError("Queue column lengths differ")
 
     def __len__(self):
@@ -40,21 +53,21 @@ class ArrayReferences(Sequence):
         if isinstance(index, slice):
             return ArrayReferences(self.scores[index], self.segments[index],
                                    self.positions[index], self.coordinates)
-        layer, head = self.coordinates[self.segments[index]]
-        return (float(self.scores[index]), int(layer), int(head), int(self.positions[index]))
+        layer, head = (int(v) for v in self.coordinates[self.segments[index]])
+        return KVReference(float(self.scores[index]), layer, head, int(self.positions[index]))
 
     def groups(self):
-        """Per (layer, head), the sorted positions of its queued slots."""
+        """The queued positions of each (layer, head), ascending, keyed in segment order. One
+        sort by (segment, position) covers every head; each head is then one run of it."""
         if not len(self):
             return {}
-        order = np.argsort(self.segments, kind="stable")
-        sorted_segments = self.segments[order]
-        boundaries = np.flatnonzero(sorted_segments[1:] != sorted_segments[:-1]) + 1
-        grouped = {}
-        for indexes in np.split(order, boundaries):
-            layer, head = self.coordinates[self.segments[indexes[0]]]
-            grouped[(int(layer), int(head))] = np.sort(self.positions[indexes])
-        return grouped
+        order = np.lexsort((self.positions, self.segments))
+        segments, positions = self.segments[order], self.positions[order]
+        firsts = np.flatnonzero(np.concatenate(([True], segments[1:] != segments[:-1])))
+        lasts = np.append(firsts[1:], len(segments))
+        coordinates = self.coordinates[segments[firsts]]
+        return {(int(layer), int(head)): positions[first:last]
+                for (layer, head), first, last in zip(coordinates, firsts, lasts)}
 
 
 @dataclass
