@@ -651,7 +651,10 @@ extern "C" int lr_pre_gradient_layers(const int64_t* layer_table, int64_t layers
   clear_error();
   LR_REQUIRE(dtype == LR_DTYPE_BF16 || dtype == LR_DTYPE_F16 || dtype == LR_DTYPE_F32,
              "Weights must be float32, float16 or bfloat16");
-  LR_REQUIRE(hidden > 0 && width > 0 && width % 8 == 0, "Weight rows must be a multiple of 8 elements");
+  // The same row bounds as check_weight on the per-layer path; the weights' 16-byte alignment
+  // cannot be checked here (their addresses are in device memory) and is the caller's to keep.
+  LR_REQUIRE(hidden > 0 && width > 0 && width % 8 == 0 && width <= 8192,
+             "Weight rows must be a multiple of 8 elements, at most 8192");
   LR_REQUIRE(layer_table && layers > 0 && layers < 65536, "Invalid layer table");
   LR_REQUIRE(workspace && workspace_size >= lr_pre_gradient_layers_workspace_bytes(layers, hidden, width) &&
                  reinterpret_cast<uintptr_t>(workspace) % 16 == 0,

@@ -177,6 +177,9 @@ def pre_gradients(post_gradients, o_proj_weights, num_query_heads: int, head_dim
     _check(all(w.shape == (hidden, width) and w.dtype == dtype and w.device == device
                for w in weights), "Every o_proj must share shape, dtype and device")
     _check(width == num_query_heads * head_dim, "o_proj width differs from Hq * head_dim")
+    # the kernels read weight rows 16 bytes at a time; the device table hides the addresses
+    # from the library's own check, so it is made here
+    _check(all(w.data_ptr() % 16 == 0 for w in weights), "Weights must be 16-byte aligned")
     posts = [p.detach().float().reshape(-1).contiguous() for p in post_gradients]
     _check(all(p.numel() == hidden and p.device == device for p in posts),
            "Post-projection gradient size differs")

@@ -129,3 +129,16 @@ def test_pre_gradients_all_layers_match_per_layer(device, dtype, gated):
         single = vjp.pre_gradient(posts[l], weights[l], heads, dim, gates[l])
         assert batched[l].shape == (heads, dim)
         torch.testing.assert_close(batched[l], single, rtol=0, atol=0)  # same kernels, same order
+
+
+def test_misaligned_weight_views_rejected(device):
+    hidden, heads, dim = 64, 2, 64
+    backing = torch.zeros(hidden * heads * dim + 1, dtype=torch.bfloat16, device=device)
+    misaligned = backing[1:].view(hidden, heads * dim)  # contiguous, 2 bytes off 16-byte alignment
+    assert misaligned.data_ptr() % 16 == 2
+    aligned = torch.zeros((hidden, heads * dim), dtype=torch.bfloat16, device=device)
+    post = torch.ones(hidden, device=device)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        vjp.pre_gradient(post, misaligned, heads, dim)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        vjp.pre_gradients([post, post], [aligned, misaligned], heads, dim)

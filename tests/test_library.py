@@ -48,6 +48,12 @@ def test_noalloc_attention_size_check_needs_no_gpu():
     assert status == 1 and "holds at most 16777216 bytes" in _lib.last_error()
 
 
+def test_pre_gradient_layers_width_bound_matches_per_layer_check():
+    library = _lib.load()
+    status = library.lr_pre_gradient_layers(None, 2, 16, 8200, _lib.LR_DTYPE_BF16, None, 0, None)
+    assert status == 1 and "at most 8192" in _lib.last_error()
+
+
 def test_zero_work_calls_succeed_without_launching():
     library = _lib.load()
     assert library.lr_compact(None, None, None, 5, 8, 2, None, 5, None, None, None, None) == 0
