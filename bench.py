@@ -23,7 +23,8 @@ Also reported on the same line:
                 Llama-3.1-8B shapes): device time per call from a held stream, GB/s against the
                 HBM peak, host-inclusive step time; and the host recall archive's exact-MIPS
                 search (cfg1 shape, 4096 archived rows per head)
-  audit_configs the audit step on cfg0 (Llama-3.2-1B) and cfg4 (Qwen3.5-style, d256, G6)
+  audit_configs the audit step on cfg0 (Llama-3.2-1B), cfg4 (Qwen3.5-style, d256, G6) and cfg3
+                (Llama-3.1-8B long budget: 33,792 tokens per head, 1,024 evicted per head)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg1]
 """
@@ -59,7 +60,7 @@ def parse_args():
     parser.add_argument("--no-reinsert", action="store_true", help="skip the cfg3 reinsertion")
     parser.add_argument("--no-ops", action="store_true",
                         help="skip the append / legacy / pack / cfg2 batch-append measurements")
-    parser.add_argument("--other-configs", default="cfg0,cfg4",
+    parser.add_argument("--other-configs", default="cfg0,cfg4,cfg3",
                         help="comma-separated further audit configurations to time ('' for none)")
     parser.add_argument("--event-every", type=int, default=5, metavar="K",
                         help="inside the timed steps, bracket the dominant kernel with events on "
@@ -555,7 +556,7 @@ def ops_bench(torch, seed, reps=5):
 
 
 def audit_config_bench(torch, name, seed, steps=10, warmup=3):
-    """A shorter audit-step measurement of another BASELINE configuration (cfg0, cfg4)."""
+    """A shorter audit-step measurement of another BASELINE configuration (cfg0, cfg4, cfg3)."""
     import numpy as np
 
     from code_for_iclr27_amd import audit, workloads

@@ -477,16 +477,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
     A *= factor;
     const float nml = (m_new == -INFINITY) ? 0.0f : -m_new * kLog2e;
     const float* pv_row = pv_lds[buf] + g * 64;
+    // The stage's 32 terms go into partial sums that join the running sums once per stage:
+    // a lane's running sums then take one addition per stage instead of one per key, which
+    // keeps their rounding error at the reference's level over long heads (33,792 keys:
+    // 2e-6 against 3e-5 relative on the scores, per key summed straight into S and A).
+    float s_part = 0.0f, a_part = 0.0f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z[4 * c + j], kLog2e, nml));
-        S += e;
-        A = __builtin_fmaf(e, w[j], A);
+        s_part += e;
+        a_part = __builtin_fmaf(e, w[j], a_part);
       }
     }
+    S += s_part;
+    A += a_part;
     m_run = m_new;
   };
 
