@@ -58,6 +58,8 @@ SIGNATURES = {
                               _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
+    "lr_queue_index": [_P, _P, _I64, _P, _P, _P, _I64, _P, _P],
+    "lr_queue_evict_plan": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P],
     "lr_history_append": [_P, _I64, _I64, _I64, _I, _I64, _I64, _P, _I64, _P, _P],
     "lr_staging_alloc": [_SZ, _P],
     "lr_staging_free": [_P],

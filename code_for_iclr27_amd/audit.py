@@ -34,7 +34,7 @@ import torch
 
 from . import _C, _lib
 from .scoring import LayerState, ScoreSegment, ScoreTable, SegmentPlan, _planner, plan_segments
-from .selection import DeviceSelection, SelectWorkspace, select_refine
+from .selection import ArrayReferences, DeviceSelection, SelectWorkspace, select_refine
 
 _bound = False
 
@@ -50,9 +50,11 @@ def _native_planner():
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_library(address("lr_score_workspace_bytes"), address("lr_score_segments"),
                              address("lr_pool"), address("lr_select_workspace_bytes"),
-                             address("lr_select_refine_sets"), address("lr_compact_heads"),
-                             address("lr_last_error"), address("lr_staging_alloc"),
-                             address("lr_staging_free"), address("lr_copy_words"))
+                             address("lr_select_refine_sets"), address("lr_select_refine_queue"),
+                             address("lr_queue_index"), address("lr_queue_evict_plan"),
+                             address("lr_compact_heads"), address("lr_last_error"),
+                             address("lr_staging_alloc"), address("lr_staging_free"),
+                             address("lr_copy_words"))
         _bound = True
     return planner
 
@@ -104,15 +106,89 @@ class PackedLayers(abc.Sequence):
         return layer
 
 
+class EvictionQueue:
+    """The deletion queue an audit leaves behind, kept on the device: controller.py:148-158
+    removes the first ``immediate`` selected slots and keeps ``references[immediate:]`` as
+    ``self.queue``; evict_prefix (controller.py:57-70) later removes its next batches, each
+    position shifted down by the earlier removals of its head below it.
+
+    ``len(queue)`` counts the slots still queued, ``references()`` copies them to the host as
+    the reference's ``ArrayReferences``, and ``evict_prefix(layers, count)`` removes the next
+    ``count`` of them from ``layers`` as they are now (the audit's compacted layers, with any
+    tokens appended since): one plan launch and one compaction of every layer
+    (lr_queue_evict_plan, lr_compact_heads), then a wait for the plan only. The queue is tied to
+    the cache it was selected from; after a recall splice the reference starts a new one
+    (controller.py:113-114)."""
+
+    def __init__(self, values, order, rank, quotas, offsets, removed, coordinates, slot_segment,
+                 consumed, sync):
+        """Enqueues, on the current stream, a copy of the queue's segment ids to pinned host
+        memory: each batch's per-segment counts (and so the new layout) are then counted on
+        the host, and evict_prefix never waits for the device."""
+        self.count = int(values.numel())
+        self.values = values                     # f32 [count], queue order
+        self.segments = order[:self.count]       # i64 [count]
+        self.positions = order[self.count:]      # i64 [count], audit-time positions
+        self.rank = rank                         # i32: queue slot of each position-sorted pick
+        self.quotas, self.offsets, self.removed = quotas, offsets, removed
+        self.coordinates = coordinates           # (layer, head) of every segment
+        self.slot_segment = slot_segment         # segment (or -1) of every (layer, head) slot
+        self.consumed = int(consumed)            # queue slots already removed (a prefix)
+        self._sync = sync
+        self._segments_host = torch.empty((self.count,), dtype=torch.int64, pin_memory=True)
+        self._segments_host.copy_(self.segments, non_blocking=True)
+        self._host_ready = torch.cuda.Event()
+        self._host_ready.record()
+
+    def __len__(self) -> int:
+        return self.count - self.consumed
+
+    def references(self) -> ArrayReferences:
+        """The slots still queued, in queue order (controller.queue)."""
+        start = self.consumed
+        return ArrayReferences(self.values[start:].cpu().numpy(),
+                               self.segments[start:].cpu().numpy(),
+                               self.positions[start:].cpu().numpy(), self.coordinates)
+
+    def evict_prefix(self, layers: Sequence[LayerState], count: int):
+        """controller.py:57-70 for the device queue: removes the next ``count`` queued slots
+        and returns the new layers (a PackedLayers; ``.kept`` holds the head lengths)."""
+        count = int(count)
+        if not count:
+            return layers
+        if count < 0 or count > len(self):
+            raise RuntimeError("Discard queue underflow")
+        planner = _native_planner()
+        device = (layers.keys if isinstance(layers, PackedLayers) else layers[0].keys).device
+        if self._host_ready is not None:  # the audit's copy of the segment ids, once
+            self._host_ready.synchronize()
+            self._host_ready = None
+        if isinstance(layers, PackedLayers):  # the packed buffers, without per-layer views
+            tensors = ([layers.keys], [layers.values], [layers.positions])
+            lengths, packed_offsets = layers.kept, layers.offsets
+        else:
+            tensors = ([layer.keys for layer in layers], [layer.values for layer in layers],
+                       [layer.positions for layer in layers])
+            lengths, packed_offsets = [list(layer.head_lens) for layer in layers], []
+        out_keys, out_values, out_positions, kept, offsets = planner.queue_evict_launch(
+            *tensors, lengths, self.slot_segment, self.quotas, self.offsets, self.removed,
+            self.rank, self._segments_host, self.consumed, self.consumed + count,
+            torch.cuda.current_stream(device).cuda_stream, self._sync, packed_offsets)
+        self.consumed += count
+        return PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers)
+
+
 @dataclass
 class AuditOutcome:
-    layers: PackedLayers              # compacted layers (views into one packed K/V/pos buffer)
+    layers: Sequence[LayerState]      # compacted layers (a PackedLayers: views into one packed
+                                      # K/V/pos buffer), or the input layers if none was removed
     head_lens: List[List[int]]
     scores: torch.Tensor              # raw temporal scores [S]
     pooled: torch.Tensor              # Pool7 scores [S]
     selection: Optional[DeviceSelection]
     plan: SegmentPlan
     removed: int
+    queue: Optional[EvictionQueue] = None  # the lazy queue (run(..., immediate=k), k < count)
 
     @property
     def segments(self) -> List[ScoreSegment]:
@@ -156,28 +232,36 @@ class AuditStep:
     def run(self, layers: Sequence[LayerState], query_positions: torch.Tensor,
             margin: torch.Tensor, count: int, protect_recent: int = 32, pool_kernel: int = 7,
             denominator_epsilon: float = 1e-6, check_finite: bool = True,
-            queue_order: bool = False, timer=None, native: bool = True) -> AuditOutcome:
-        """Scores, selects and removes ``count`` slots. Every selected slot is removed now
-        (immediate == count in controller.run_audit, controller.py:148-158), so the lazy queue
-        ``references[immediate:]`` is empty and the removal sets are all the step needs; the
-        queue order (``outcome.selection.values/segments/positions``) is computed only with
-        ``queue_order=True``, on a side stream, overlapping the compaction.
+            queue_order: bool = False, timer=None, native: bool = True,
+            immediate: Optional[int] = None) -> AuditOutcome:
+        """Scores and selects ``count`` slots (controller.run_audit, controller.py:140-159).
+
+        ``immediate`` None (or >= count) removes every selected slot now; the lazy queue
+        ``references[immediate:]`` is then empty and the removal sets are all the step needs,
+        so the queue order (``outcome.selection.values/segments/positions``) is computed only
+        with ``queue_order=True``, on a side stream, overlapping the compaction.
+        ``0 <= immediate < count`` is the lazy form: the queue order is computed, its first
+        ``immediate`` slots are removed (with 0 the layers are returned as they are) and the rest
+        stay queued on the device as ``outcome.queue`` (an EvictionQueue) for evict_prefix.
         ``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
         stage, on the current stream, for per-stage event timing. The launches are made by the
         C++ host module; ``native=False`` makes the same launches from Python (a cross-check).
         """
         if pool_kernel <= 0 or pool_kernel % 2 == 0:
             raise ValueError("pool kernel must be a positive odd integer")
+        immediate = -1 if immediate is None else int(immediate)
+        if immediate < -1:
+            raise ValueError("immediate must be non-negative")
         if not native:
             return self._run_python(layers, query_positions, margin, count, protect_recent,
                                     pool_kernel, denominator_epsilon, check_finite, queue_order,
-                                    timer)
+                                    timer, immediate)
         return self._run_native(layers, query_positions, margin, count, protect_recent,
                                 pool_kernel, denominator_epsilon, check_finite, timer,
-                                queue_order)
+                                queue_order, immediate)
 
     def _run_python(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
-                    denominator_epsilon, check_finite, queue_order, timer):
+                    denominator_epsilon, check_finite, queue_order, timer, immediate=-1):
         """The same step launched from Python (plan_segments, ctypes calls)."""
         mark = timer.mark if timer is not None else (lambda name: None)
         plan = plan_segments(layers, protect_prompt=True, protect_recent=protect_recent,
@@ -228,11 +312,17 @@ class AuditStep:
 
         # --- selection ---------------------------------------------------------------------
         count = min(max(0, int(count)), total)
+        if immediate > count:
+            raise RuntimeError("Not enough unprotected candidates to enforce the budget")
+        lazy = count > 0 and 0 <= immediate < count
         selection = select_refine(raw, pooled, None, None, plan.segment_info[:2].T, count,
                                   ends_device=ends_d, starts_device=starts_d,
                                   workspace=self.select_workspace, quotas_out=info[:segments],
-                                  queue=queue_order,
-                                  queue_stream=self._queue_stream(device) if queue_order else None)
+                                  queue=queue_order or lazy,
+                                  queue_stream=self._queue_stream(device) if queue_order and not lazy else None)
+        if lazy:
+            return self._finish_lazy(plan, info, raw, pooled, selection, count, immediate, layers,
+                                     heads_ptr, max_length, check_finite, stream, mark)
         mark("select")
 
         # --- compaction of every layer -----------------------------------------------------
@@ -255,6 +345,59 @@ class AuditStep:
             mark("queue_join")
         return self._finish(plan, info, raw, pooled, selection, count, out_keys, out_values,
                             out_positions, layers, check_finite)
+
+    def _finish_lazy(self, plan, info, raw, pooled, selection, count, immediate, layers,
+                     heads_ptr, max_length, check_finite, stream, mark):
+        """The Python path's lazy form: the queue index and the plan of the queue's first
+        ``immediate`` slots, their compaction, then one copy of the batch quotas."""
+        device = raw.device
+        segments = plan.segment_count
+        rank = torch.empty((count,), dtype=torch.int32, device=device)
+        _lib.call("lr_queue_index", selection.segments.data_ptr(), selection.positions.data_ptr(),
+                  count, selection.quotas.data_ptr(), selection.offsets.data_ptr(),
+                  selection.removed_positions.data_ptr(), segments, rank.data_ptr(), stream)
+        batch = torch.zeros((count + segments,), dtype=torch.int64, device=device)
+        if immediate:
+            _lib.call("lr_queue_evict_plan", selection.quotas.data_ptr(),
+                      selection.offsets.data_ptr(), selection.removed_positions.data_ptr(),
+                      rank.data_ptr(), segments, 0, immediate, batch[count:].data_ptr(),
+                      batch.data_ptr(), None, stream)
+        mark("select")
+        out_rows = plan.rows_total - immediate
+        out_keys = out_values = out_positions = None
+        if immediate:
+            out_keys = torch.empty((out_rows, plan.dim), dtype=layers[0].keys.dtype, device=device)
+            out_values = torch.empty_like(out_keys)
+            out_positions = torch.empty((out_rows,), dtype=torch.float32, device=device)
+            _lib.call("lr_compact_heads", heads_ptr, plan.head_slots, batch[count:].data_ptr(),
+                      selection.offsets.data_ptr(), batch.data_ptr(), plan.dim, 2, max_length,
+                      out_rows, out_keys.data_ptr(), out_values.data_ptr(),
+                      out_positions.data_ptr(), stream)
+            mark("compact")
+        host_info = info.cpu().numpy()
+        if check_finite and int(host_info[segments:].view(np.int32)[0]):
+            raise RuntimeError("LazyRecall produced non-finite scores; refusing to construct a deletion queue")
+        quotas = batch[count:].cpu().numpy()
+        segment_index, lengths = plan.head_info
+        removed_per_slot = np.where(segment_index >= 0, quotas[np.maximum(segment_index, 0)], 0)
+        kept = (lengths - removed_per_slot).reshape(-1, plan.heads)
+        new_lens = kept.tolist()
+        if immediate:
+            offsets = np.concatenate(([0], np.cumsum(kept.sum(axis=1)))).tolist()
+            new_layers = PackedLayers(out_keys, out_values, out_positions, new_lens, offsets, layers)
+        else:
+            new_layers = list(layers)
+        order = torch.cat((selection.segments, selection.positions))
+        queue = EvictionQueue(selection.values, order, rank, selection.quotas, selection.offsets,
+                              selection.removed_positions, plan.segment_info[:2].T,
+                              [int(v) for v in segment_index], immediate, self._sync_for(device))
+        return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, immediate, queue)
+
+    def _sync_for(self, device):
+        sync = self.syncs.get(device)
+        if sync is None:
+            sync = self.syncs[device] = _native_planner().StepSync()
+        return sync
 
     @staticmethod
     def _finish(plan, info, raw, pooled, selection, count, out_keys, out_values, out_positions,
@@ -296,7 +439,8 @@ class AuditStep:
         selection.queue_ready = ready
 
     def _run_native(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
-                    denominator_epsilon, check_finite, timer=None, queue_order=False):
+                    denominator_epsilon, check_finite, timer=None, queue_order=False,
+                    immediate=-1):
         """The step with planning and every launch done by the C++ host module
         (csrc/host_plan.cpp audit_launch): no Python between the launches. With
         ``queue_order`` the queue half of the selection runs on a side stream after the
@@ -306,9 +450,7 @@ class AuditStep:
             raise RuntimeError("No layers to score")
         planner = _native_planner()
         device = layers[0].keys.device
-        sync = self.syncs.get(device)
-        if sync is None:
-            sync = self.syncs[device] = planner.StepSync()
+        sync = self._sync_for(device)
         margin = margin.to(device=device, dtype=torch.float32).reshape(1)
         mark = None if timer is None else timer.mark
         sets_done = None
@@ -321,17 +463,34 @@ class AuditStep:
                 if inner is not None:
                     inner(name)
         (block, meta, segment_info, head_info, scores, info, quotas, offsets, removed, changed,
-         out_keys, out_values, out_positions, device_block, select_ws) = planner.audit_launch(
+         out_keys, out_values, out_positions, device_block, select_ws,
+         queue_state) = planner.audit_launch(
             [layer.keys for layer in layers], [layer.values for layer in layers],
             [layer.positions for layer in layers], [layer.queries for layer in layers],
             [layer.gradient for layer in layers], [list(layer.head_lens) for layer in layers],
             [None if layer.prompt_lens is None else list(layer.prompt_lens) for layer in layers],
-            int(protect_recent), query_positions, margin, int(count), int(pool_kernel),
-            float(denominator_epsilon), torch.cuda.current_stream(device).cuda_stream, mark, sync)
+            int(protect_recent), query_positions, margin, int(count), int(immediate),
+            int(pool_kernel), float(denominator_epsilon),
+            torch.cuda.current_stream(device).cuda_stream, mark, sync)
         plan = SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
         total = plan.total
         count = min(max(0, int(count)), total)
         selection = None
+        if queue_state is not None:  # the lazy form
+            values, order, rank = queue_state
+            selection = DeviceSelection(values, order[:count], order[count:], quotas, offsets,
+                                        removed, changed, plan.segment_info[:2].T)
+            kept, offsets_out = sync.wait(check_finite)
+            if immediate:
+                new_layers = PackedLayers(out_keys, out_values, out_positions, kept, offsets_out,
+                                          layers)
+            else:
+                new_layers = list(layers)
+            queue = EvictionQueue(values, order, rank, quotas, offsets, removed,
+                                  plan.segment_info[:2].T, [int(v) for v in plan.head_info[0]],
+                                  immediate, sync)
+            return AuditOutcome(new_layers, [list(lengths) for lengths in kept], scores[:total],
+                                scores[total:], selection, plan, immediate, queue)
         if count:
             selection = DeviceSelection(None, None, None, quotas, offsets, removed, changed,
                                         plan.segment_info[:2].T)

@@ -225,6 +225,9 @@ struct Library {
   decltype(&lr_pool) pool = nullptr;
   decltype(&lr_select_workspace_bytes) select_workspace_bytes = nullptr;
   decltype(&lr_select_refine_sets) select_refine_sets = nullptr;
+  decltype(&lr_select_refine_queue) select_refine_queue = nullptr;
+  decltype(&lr_queue_index) queue_index = nullptr;
+  decltype(&lr_queue_evict_plan) queue_evict_plan = nullptr;
   decltype(&lr_compact_heads) compact_heads = nullptr;
   decltype(&lr_last_error) last_error = nullptr;
   decltype(&lr_staging_alloc) staging_alloc = nullptr;
@@ -241,6 +244,7 @@ void bind_one(F& slot, int64_t address) {
 
 void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t pool,
                   int64_t select_workspace_bytes, int64_t select_refine_sets,
+                  int64_t select_refine_queue, int64_t queue_index, int64_t queue_evict_plan,
                   int64_t compact_heads, int64_t last_error, int64_t staging_alloc,
                   int64_t staging_free, int64_t copy_words) {
   bind_one(library.score_workspace_bytes, score_workspace_bytes);
@@ -248,6 +252,9 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
   bind_one(library.pool, pool);
   bind_one(library.select_workspace_bytes, select_workspace_bytes);
   bind_one(library.select_refine_sets, select_refine_sets);
+  bind_one(library.select_refine_queue, select_refine_queue);
+  bind_one(library.queue_index, queue_index);
+  bind_one(library.queue_evict_plan, queue_evict_plan);
   bind_one(library.compact_heads, compact_heads);
   bind_one(library.last_error, last_error);
   bind_one(library.staging_alloc, staging_alloc);
@@ -285,6 +292,7 @@ struct StepSync {
   std::vector<int64_t> slot_segment, slot_length;   // per (layer, head): segment or -1, length
   int64_t layers = 0, heads = 0, segments = 0;
   bool pending = false;
+  bool subtract = true;  // heads lose info[segment] rows (false: the step removed nothing)
 
   StepSync() = default;
   StepSync(const StepSync&) = delete;
@@ -336,15 +344,24 @@ struct StepSync {
     return block;
   }
 
-  void post(const Plan& plan, const torch::Device& device) {
+  // Records `ready` and keeps what wait() needs: each head slot's segment (or -1) and length.
+  // With removes = false the step removes nothing (every head keeps its length).
+  void post_slots(const int64_t* segment_of_slot, const int64_t* length_of_slot, int64_t slots,
+                  int64_t layer_count, int64_t segment_count, bool removes,
+                  const torch::Device& device) {
     ready.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
-    const int64_t* slot = plan.head_info.data_ptr<int64_t>();
-    slot_segment.assign(slot, slot + plan.slots);
-    slot_length.assign(slot + plan.slots, slot + 2 * plan.slots);
-    layers = plan.layers;
-    heads = plan.slots / plan.layers;
-    segments = plan.segments;
+    slot_segment.assign(segment_of_slot, segment_of_slot + slots);
+    slot_length.assign(length_of_slot, length_of_slot + slots);
+    layers = layer_count;
+    heads = slots / layer_count;
+    segments = segment_count;
+    subtract = removes;
     pending = true;
+  }
+
+  void post(const Plan& plan, const torch::Device& device, bool removes = true) {
+    const int64_t* slot = plan.head_info.data_ptr<int64_t>();
+    post_slots(slot, slot + plan.slots, plan.slots, plan.layers, plan.segments, removes, device);
   }
 
   // Waits for the selection, refuses non-finite scores (scoring.py:292-293's message), and
@@ -371,7 +388,7 @@ struct StepSync {
       for (int64_t h = 0; h < heads; ++h) {
         const int64_t slot = l * heads + h;
         const int64_t s = slot_segment[slot];
-        const int64_t n = slot_length[slot] - (s >= 0 ? info[s] : 0);
+        const int64_t n = slot_length[slot] - (subtract && s >= 0 ? info[s] : 0);
         lengths[h] = py::int_(n);
         row += n;
       }
@@ -382,14 +399,19 @@ struct StepSync {
   }
 };
 
-// One whole audit step on the device (controller.py:140-159 without the lazy queue order):
-// plan, one metadata upload, fused scores, Pool7, the removal sets of the allocation-preserving
-// selection and the compaction of every layer, all enqueued on `stream` from here (no Python
-// between the launches). Returns (plan block, meta, segment_info, head_info, scores [2*total]
-// (raw then pooled), info i64 [S+1] (quotas, then the non-finite score count as i32),
-// quotas, offsets, removed positions, changed, out keys, out values, out positions, the block
-// on the device, the selection workspace (for the queue order, lr_select_refine_queue)). count is
-// clamped to [0, total]; with count 0 nothing is selected and the layers are copied as they are.
+// One whole audit step on the device (controller.py:140-159): plan, one metadata upload, fused
+// scores, Pool7, the removal sets of the allocation-preserving selection and the compaction of
+// every layer, all enqueued on `stream` from here (no Python between the launches). Returns
+// (plan block, meta, segment_info, head_info, scores [2*total] (raw then pooled), info i64
+// [S+1] (quotas, then the non-finite score count as i32), quotas, offsets, removed positions,
+// changed, out keys, out values, out positions, the block on the device, the selection
+// workspace (for the queue order, lr_select_refine_queue), queue). count is clamped to
+// [0, total]; with count 0 nothing is selected and the layers are copied as they are.
+// immediate < 0 or >= count removes every selected slot (queue None). 0 <= immediate < count is
+// the lazy form: the queue order is computed on `stream`, only its first `immediate` slots are
+// removed (none: the out tensors are undefined and the layers stay as they are), and queue =
+// (values f32 [count], segments then positions i64 [2 * count], rank i32 [count]) is the device
+// state lr_queue_evict_plan needs for the rest (with quotas, offsets and removed positions).
 // `mark` (None or a callable) is called with a stage name after each stage's launches and with
 // "start" before the first (then the scorer is launched stage by stage), for event timing.
 // `sync` (or None) receives the quota copy and its event between the selection and the
@@ -403,9 +425,9 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        const std::vector<std::vector<int64_t>>& head_lens,
                        const std::vector<std::optional<std::vector<int64_t>>>& prompt_lens,
                        int64_t protect_recent, const torch::Tensor& query_positions,
-                       const torch::Tensor& margin, int64_t count, int64_t pool_kernel,
-                       double epsilon, int64_t stream_handle, const py::object& mark,
-                       StepSync* sync) {
+                       const torch::Tensor& margin, int64_t count, int64_t immediate,
+                       int64_t pool_kernel, double epsilon, int64_t stream_handle,
+                       const py::object& mark, StepSync* sync) {
   require(library.score_segments != nullptr, "library entry points are not bound");
   require(pool_kernel > 0 && pool_kernel % 2 == 1, "pool kernel must be a positive odd integer");
   // with a StepSync the block goes through its staging buffer, so it need not be pinned
@@ -426,6 +448,8 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                                         : plan.block.to(device, /*non_blocking=*/true);
   const int64_t* words = block.data_ptr<int64_t>();
   count = std::min(std::max<int64_t>(count, 0), plan.total);
+  // controller.py:151-153: the selection must cover the slots the budget removes now
+  require(immediate <= count, "Not enough unprotected candidates to enforce the budget");
 
   // quotas (written for every segment by the selection) and the non-finite count (cleared by
   // the first scorer kernel) come back in one small copy
@@ -457,13 +481,64 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                           pool_kernel, pooled, stream));
   stage("pool");
 
-  const int64_t out_rows = plan.rows_total - count;
+  // The lazy form: only the queue's first `immediate` slots leave now, the rest stay queued
+  // (controller.py:148-158). It needs the queue order before the compaction.
+  const bool lazy = count > 0 && immediate >= 0 && immediate < count;
+  const int64_t out_rows = plan.rows_total - (lazy ? immediate : count);
   const auto kv = on_device.dtype(keys[0].scalar_type());
-  torch::Tensor out_keys = torch::empty({out_rows, plan.dim}, kv);
-  torch::Tensor out_values = torch::empty({out_rows, plan.dim}, kv);
-  torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
+  torch::Tensor out_keys, out_values, out_positions;
+  if (!lazy || immediate > 0) {
+    out_keys = torch::empty({out_rows, plan.dim}, kv);
+    out_values = torch::empty({out_rows, plan.dim}, kv);
+    out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
+  }
   torch::Tensor sets, quotas, offsets, removed, changed, select_ws;
-  if (count > 0) {
+  torch::Tensor queue_values, queue_order, queue_rank, batch;
+  if (lazy) {
+    const size_t select_bytes = library.select_workspace_bytes(plan.total, S, count);
+    select_ws = torch::empty({static_cast<int64_t>(select_bytes)}, on_device.dtype(torch::kUInt8));
+    sets = torch::empty({count + 2 * S + 1}, on_device.dtype(torch::kInt64));
+    quotas = info.narrow(0, 0, S);
+    removed = sets.narrow(0, 0, count);
+    offsets = sets.narrow(0, count, S + 1);
+    changed = sets.narrow(0, count + S + 1, S);
+    queue_values = torch::empty({count}, on_device.dtype(torch::kFloat32));
+    queue_order = torch::empty({2 * count}, on_device.dtype(torch::kInt64));
+    queue_rank = torch::empty({count}, on_device.dtype(torch::kInt32));
+    batch = torch::empty({count + S}, on_device.dtype(torch::kInt64));
+    int64_t* host = sync != nullptr ? sync->info_buffer(S + 1) : nullptr;
+    check_call(library.select_refine_sets(
+        raw, pooled, plan.total, words + plan.ends_at(), words + plan.starts_at(), S, count,
+        dptr(select_ws), select_bytes, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+        removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(), host, nonfinite, stream));
+    int64_t* queue_segments = queue_order.data_ptr<int64_t>();
+    int64_t* queue_positions = queue_segments + count;
+    check_call(library.select_refine_queue(
+        words + plan.starts_at(), plan.total, S, count, dptr(select_ws), select_bytes,
+        quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(), queue_values.data_ptr<float>(),
+        queue_segments, queue_positions, stream));
+    check_call(library.queue_index(queue_segments, queue_positions, count,
+                                   quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+                                   removed.data_ptr<int64_t>(), S, queue_rank.data_ptr<int32_t>(),
+                                   stream));
+    int64_t* batch_positions = batch.data_ptr<int64_t>();
+    int64_t* batch_quotas = batch_positions + count;
+    if (immediate > 0)
+      check_call(library.queue_evict_plan(
+          quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(), removed.data_ptr<int64_t>(),
+          queue_rank.data_ptr<int32_t>(), S, 0, immediate, batch_quotas, batch_positions, host,
+          stream));
+    stage("select");
+    if (sync != nullptr) sync->post(plan, device, /*removes=*/immediate > 0);
+    if (immediate > 0) {  // with nothing to remove now the layers stay as they are
+      check_call(library.compact_heads(
+          words + plan.heads_at(), plan.slots, batch_quotas, offsets.data_ptr<int64_t>(),
+          batch_positions, plan.dim, static_cast<int>(keys[0].element_size()),
+          plan.max_head_length, out_rows, dptr(out_keys), dptr(out_values),
+          out_positions.data_ptr<float>(), stream));
+      stage("compact");
+    }
+  } else if (count > 0) {
     const size_t select_bytes = library.select_workspace_bytes(plan.total, S, count);
     select_ws = torch::empty({static_cast<int64_t>(select_bytes)}, on_device.dtype(torch::kUInt8));
     sets = torch::empty({count + 2 * S + 1}, on_device.dtype(torch::kInt64));
@@ -497,9 +572,141 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
     out_values.copy_(torch::cat(values));
     out_positions.copy_(torch::cat(flat_positions));
   }
+  py::object queue = py::none();
+  if (lazy) queue = py::make_tuple(queue_values, queue_order, queue_rank);
   return py::make_tuple(plan.block, plan.meta(), plan.segment_info, plan.head_info, scores, info,
                         quotas, offsets, removed, changed, out_keys, out_values, out_positions,
-                        block, select_ws);
+                        block, select_ws, queue);
+}
+
+// One evict_prefix batch (controller.py:57-70) on the device: removes the queued slots
+// [begin, end) of an audit's lazy queue from the layers as they are now (the audit's own
+// removals done, tokens appended since at the end of each head). The queue state is the
+// audit's (quotas, offsets, removed positions, rank; lr_queue_evict_plan) plus a host copy of
+// the queue's segment ids (`segments_host`, CPU int64 [count], queue order), from which the
+// batch's per-segment counts and so the new layout are known here without waiting for the
+// device. slot_segment maps each (layer, head) slot to its score segment or -1, as at the audit.
+// Enqueues on `stream`: the head-table upload (sync's staging buffer), the plan (remapped
+// positions) and one compaction of every layer; nothing here waits for them. Returns (out keys,
+// out values, out positions, rows kept per head [L][H], row offset of each layer [L + 1]).
+py::tuple queue_evict_launch(const std::vector<torch::Tensor>& keys,
+                             const std::vector<torch::Tensor>& values,
+                             const std::vector<torch::Tensor>& positions,
+                             const std::vector<std::vector<int64_t>>& head_lens,
+                             const std::vector<int64_t>& slot_segment, const torch::Tensor& quotas,
+                             const torch::Tensor& offsets, const torch::Tensor& removed,
+                             const torch::Tensor& rank, const torch::Tensor& segments_host,
+                             int64_t begin, int64_t end, int64_t stream_handle, StepSync* sync,
+                             const std::vector<int64_t>& packed_offsets) {
+  require(library.queue_evict_plan != nullptr, "library entry points are not bound");
+  require(sync != nullptr, "an evict_prefix batch needs a StepSync");
+  // Packed form (an audit's or a batch's own output): one K, V and positions tensor holding
+  // every layer, layer l at rows [packed_offsets[l], packed_offsets[l + 1]).
+  const bool packed = !packed_offsets.empty();
+  const size_t layers = packed ? packed_offsets.size() - 1 : keys.size();
+  require(layers > 0 && head_lens.size() == layers &&
+              (packed ? keys.size() == 1 && values.size() == 1 && positions.size() == 1
+                      : values.size() == layers && positions.size() == layers),
+          "Layer lists differ in length");
+  const int64_t heads = static_cast<int64_t>(head_lens[0].size());
+  const int64_t slots = static_cast<int64_t>(layers) * heads;
+  require(heads > 0 && static_cast<int64_t>(slot_segment.size()) == slots,
+          "The queue belongs to a cache of another shape");
+  const int64_t S = quotas.numel();
+  const torch::Device device = keys[0].device();
+  for (const torch::Tensor* t : {&quotas, &offsets, &removed})
+    require(t->is_cuda() && t->device() == device && t->is_contiguous() &&
+                t->scalar_type() == torch::kInt64,
+            "Invalid queue state");
+  require(rank.is_cuda() && rank.device() == device && rank.is_contiguous() &&
+              rank.scalar_type() == torch::kInt32 && rank.numel() == removed.numel() &&
+              offsets.numel() == S + 1,
+          "Invalid queue state");
+  require(!segments_host.is_cuda() && segments_host.is_contiguous() &&
+              segments_host.scalar_type() == torch::kInt64 &&
+              segments_host.numel() == removed.numel(),
+          "Invalid queue state");
+  require(0 <= begin && begin <= end && end <= removed.numel(), "Discard queue underflow");
+  // the batch's slots per segment, from the host copy of the queue order
+  std::vector<int64_t> leaving(static_cast<size_t>(S), 0);
+  const int64_t* queue_segments = segments_host.data_ptr<int64_t>();
+  for (int64_t j = begin; j < end; ++j) {
+    const int64_t segment = queue_segments[j];
+    require(segment >= 0 && segment < S, "Invalid queue state");
+    ++leaving[segment];
+  }
+  const int64_t dim = keys[0].dim() == 2 ? keys[0].size(1) : 0;
+  const auto dtype = keys[0].scalar_type();
+  torch::Tensor table = torch::empty({slots * LR_HEAD_WORDS}, torch::TensorOptions().dtype(torch::kInt64));
+  int64_t* rows = table.data_ptr<int64_t>();
+  py::list kept(layers), layer_offsets(layers + 1);
+  layer_offsets[0] = py::int_(0);
+  int64_t rows_total = 0, out_rows = 0, max_length = 0;
+  for (size_t l = 0; l < layers; ++l) {
+    const size_t t_index = packed ? 0 : l;
+    const torch::Tensor &k = keys[t_index], &v = values[t_index], &p = positions[t_index];
+    if (!packed || l == 0) {
+      for (const torch::Tensor* t : {&k, &v, &p})
+        require(t->is_cuda() && t->is_contiguous() && t->device() == device,
+                "Expected contiguous CUDA tensor");
+      require(k.dim() == 2 && k.sizes() == v.sizes() && k.size(1) == dim && dim > 0 &&
+                  k.scalar_type() == dtype && v.scalar_type() == dtype,
+              "Invalid KV layout");
+      require(p.scalar_type() == torch::kFloat32 && p.numel() == k.size(0), "Invalid positions");
+    }
+    const int64_t first_row = packed ? packed_offsets[l] : 0;
+    const int64_t layer_rows = packed ? packed_offsets[l + 1] - first_row : k.size(0);
+    require(first_row >= 0 && layer_rows >= 0 && first_row + layer_rows <= k.size(0),
+            "Position/KV lengths differ");
+    require(static_cast<int64_t>(head_lens[l].size()) == heads,
+            "Every layer must have the same number of KV heads");
+    py::list lengths(heads);
+    int64_t base = first_row;
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t n = head_lens[l][h];
+      require(n >= 0, "Position/KV lengths differ");
+      const int64_t slot = static_cast<int64_t>(l) * heads + h;
+      const int64_t segment = slot_segment[slot];
+      require(segment >= -1 && segment < S, "The queue belongs to a cache of another shape");
+      const int64_t gone = segment >= 0 ? leaving[segment] : 0;
+      require(gone <= n, "The queue belongs to a cache of another shape");
+      int64_t* row = rows + slot * LR_HEAD_WORDS;
+      row[0] = ptr(k) + base * dim * static_cast<int64_t>(k.element_size());
+      row[1] = ptr(v) + base * dim * static_cast<int64_t>(v.element_size());
+      row[2] = ptr(p) + base * 4;
+      row[3] = n;
+      row[4] = segment;
+      row[5] = 0;
+      lengths[h] = py::int_(n - gone);
+      out_rows += n - gone;
+      base += n;
+      max_length = std::max(max_length, n);
+    }
+    require(base == first_row + layer_rows, "Position/KV lengths differ");
+    rows_total += layer_rows;
+    kept[l] = lengths;
+    layer_offsets[l + 1] = py::int_(out_rows);
+  }
+  void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
+  const auto on_device = torch::TensorOptions().device(device);
+  torch::Tensor head_table = sync->upload(table, device, stream);
+  const int64_t count = removed.numel();
+  torch::Tensor batch = torch::empty({count + S}, on_device.dtype(torch::kInt64));
+  int64_t* batch_positions = batch.data_ptr<int64_t>();
+  int64_t* batch_quotas = batch_positions + count;
+  check_call(library.queue_evict_plan(quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+                                      removed.data_ptr<int64_t>(), rank.data_ptr<int32_t>(), S,
+                                      begin, end, batch_quotas, batch_positions, nullptr, stream));
+  const auto kv = on_device.dtype(dtype);
+  torch::Tensor out_keys = torch::empty({out_rows, dim}, kv);
+  torch::Tensor out_values = torch::empty({out_rows, dim}, kv);
+  torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
+  check_call(library.compact_heads(head_table.data_ptr<int64_t>(), slots, batch_quotas,
+                                   offsets.data_ptr<int64_t>(), batch_positions, dim,
+                                   static_cast<int>(keys[0].element_size()), max_length, out_rows,
+                                   dptr(out_keys), dptr(out_values), out_positions.data_ptr<float>(),
+                                   stream));
+  return py::make_tuple(out_keys, out_values, out_positions, kept, layer_offsets);
 }
 
 // The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,
@@ -570,6 +777,8 @@ PYBIND11_MODULE(_plan, module) {
       .def("wait", &StepSync::wait, py::arg("check_finite"),
            "Wait for the selection of the pending step; returns (kept [L][H], layer offsets)");
   module.def("audit_launch", &audit_launch, "Enqueue one whole audit step");
+  module.def("queue_evict_launch", &queue_evict_launch,
+             "Enqueue one evict_prefix batch of an audit's lazy queue");
   module.def("plan_batch_append", &plan_batch_append,
              "Validate a batch and upload its batch_append descriptors");
   module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;

@@ -242,6 +242,29 @@ int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* qu
                      int elem_bytes, int64_t max_length, int64_t total_out_rows,
                      void* out_keys, void* out_values, float* out_positions, void* stream);
 
+/* The lazy eviction queue (src/lazy_recall/controller.py:140-159 keeps references[immediate:]
+ * after removing the first `immediate`; controller.py:57-70 evict_prefix removes the next
+ * batches). State: the selection's per-segment position-sorted picks (quotas, offsets,
+ * removed_positions of lr_select_refine) and, per pick, its queue slot `rank` (device i32
+ * [count], laid out like removed_positions).
+ * lr_queue_index fills `rank` from the queue order (queue_segments/queue_positions [count] i64,
+ * lr_select_refine_queue's out_segments/out_positions); every entry is written.
+ * lr_queue_evict_plan plans the removal of queue slots [begin, end), given that slots
+ * [0, begin) are already removed: per segment s, batch_quotas[s] = its slots in the range and
+ * batch_positions[offsets[s] ...] = their positions ascending, each minus the number of slots
+ * of s removed earlier at a lower position (the searchsorted(removed_at_audit, positions)
+ * remap). (batch_quotas, offsets, batch_positions) is then what lr_compact_heads takes.
+ * host_quotas (may be NULL): host-coherent memory (lr_staging_alloc) of `segments` words that
+ * also receives batch_quotas. */
+int lr_queue_index(const int64_t* queue_segments, const int64_t* queue_positions, int64_t count,
+                   const int64_t* quotas, const int64_t* offsets,
+                   const int64_t* removed_positions, int64_t segments, int32_t* rank,
+                   void* stream);
+int lr_queue_evict_plan(const int64_t* quotas, const int64_t* offsets,
+                        const int64_t* removed_positions, const int32_t* rank, int64_t segments,
+                        int64_t begin, int64_t end, int64_t* batch_quotas,
+                        int64_t* batch_positions, int64_t* host_quotas, void* stream);
+
 /* Staging of the fused step's metadata block (no reference counterpart: the reference copies
  * each per-layer index list to the device with its own blocking copy). lr_staging_alloc gives
  * `bytes` of pinned, host-coherent memory that kernels may read directly; lr_staging_free
