@@ -42,6 +42,8 @@ SIGNATURES = {
     "lr_merge": [_P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I, _P, _P, _P, _P],
     "lr_pack": [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _I64, _P, _P, _P],
     "lr_batch_append": [_P, _I64, _P, _P, _I64, _I, _I64, _P, _P, _P, _P],
+    "lr_pack_layers": [_P, _I64, _P, _I64, _I64, _P, _P, _P],
+    "lr_group_mean_queries": [_P, _I64, _I64, _I64, _I64, _I, _P, _P],
     "lr_append_flattened_cache": [_P, _I64, _P, _I64, _I64, _I64, _I, _P, _P, _P, _P],
     "lr_compact_flattened_kv": [_P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P],
     "lr_decision_risk_scores": [_P, _P, _I, _P, _P, _I64, _I64, _I64, _D, _D, _P, _P],

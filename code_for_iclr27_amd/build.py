@@ -1,6 +1,7 @@
 """Build liblazyrecall_hip.so (gfx950) from csrc/*.hip with hipcc, the host planner module
-_plan from csrc/host_plan.cpp with g++ against torch's headers, and the recall archive
-liblazyrecall_archive.so from csrc/archive.cpp with g++.
+_plan from csrc/host_plan.cpp with g++ against torch's headers, the recall archive
+liblazyrecall_archive.so from csrc/archive.cpp with g++, and the recall transport's ring
+liblazyrecall_recall.so from csrc/recall_ring.cpp with g++ against the HIP runtime API.
 
 Run as ``python -m code_for_iclr27_amd.build``. Each translation unit is compiled in parallel,
 then linked into ``code_for_iclr27_amd/liblazyrecall_hip.so`` next to this file; the planner
@@ -100,6 +101,33 @@ def build_archive(verbose: bool = False) -> Path:
     return ARCHIVE
 
 
+RECALL = PACKAGE_DIR / "liblazyrecall_recall.so"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+
+def build_recall(verbose: bool = False) -> Path:
+    """The recall transport's ring (host C++ against the HIP runtime API, no GPU code):
+    liblazyrecall_recall.so, linked to liblazyrecall_archive.so next to it."""
+    temporary = RECALL.with_suffix(".so.tmp")
+    command = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-pthread", "-Wall",
+               "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
+               f"-I{PACKAGE_DIR.parent / 'include'}", str(SOURCE_DIR / "recall_ring.cpp"),
+               "-o", str(temporary), f"-L{PACKAGE_DIR}", "-llazyrecall_archive",
+               "-Wl,-rpath,$ORIGIN", f"-L{ROCM / 'lib'}", "-lamdhip64",
+               f"-Wl,-rpath,{ROCM / 'lib'}"]
+    if verbose:
+        print(" ".join(command), flush=True)
+    _run(command)
+    os.replace(temporary, RECALL)
+    return RECALL
+
+
+def build_host_libraries(verbose: bool = False) -> None:
+    """The archive, then the ring that links it."""
+    build_archive(verbose)
+    build_recall(verbose)
+
+
 def build(verbose: bool = False) -> Path:
     hipcc = _hipcc()
     sources = sorted(SOURCE_DIR.glob("*.hip"))
@@ -119,7 +147,7 @@ def build(verbose: bool = False) -> Path:
     workers = min(len(sources) + 1, max(1, (os.cpu_count() or 4)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         planner = pool.submit(build_host_plan, verbose)
-        archive = pool.submit(build_archive, verbose)
+        archive = pool.submit(build_host_libraries, verbose)
         list(pool.map(compile_one, zip(sources, objects)))
         planner.result()
         archive.result()

@@ -1,369 +1,404 @@
-"""The recall transport: evicted KV rows stream to a CPU-owned exact-MIPS archive, periodic
-per-(layer, head) queries search it, and the results come back to HBM for reinsertion.
+"""The recall transport: eviction batches out to the host archive, search results back to HBM
+(the drop-in for RecallTransport, src/lazy_recall/recall/transport.py:46-361, and its CPU worker,
+recall/cpu_worker.py:136-182).
 
-Drop-in for ``RecallTransport`` of src/lazy_recall/recall/transport.py:46-361: same
-constructor, methods (record_evicted, pump, ready_result, release_result, retire_finished,
-remove_admitted, wait_pending, step, finish, close), slot states, counters and errors. The
-layout differs where this pool differs from the reference's:
+What a caller sees is the reference's: the constructor arguments, record_evicted / step /
+ready_result / release_result / retire_finished / remove_admitted / wait_pending / finish /
+close, the per-slot state names ("free", "copying", "worker"; "free", "copying_query",
+"worker", "copying_result", "retiring"), the counter keys and the stats.
 
-- staging buffers are pinned host allocations (``pin_memory=True``, hipHostMalloc) instead of
-  shared-memory segments pinned with hipHostRegister (refused here for existing memory);
-- the archive (code_for_iclr27_amd.archive, host C++) runs on a worker thread of this process
-  instead of a spawned process fed through queues: its calls release the GIL, so the decode
-  loop keeps running while it adds or searches; commands and replies keep the reference's
-  message kinds;
-- rows are gathered into the staging slot by the HIP ``pack`` kernel (code_for_iclr27_amd._C)
-  and copied device-to-host / host-to-device on a side stream of default priority, ordered by
-  events, as the reference does.
+How it works is this package's own:
+  * the native ring (liblazyrecall_recall.so, csrc/recall_ring.cpp) owns the slot states, two
+    default-priority copy streams (one per direction) with their events, the exact-MIPS archive
+    (csrc/archive.cpp) and one worker thread. The worker takes archive batches, searches and
+    removals in submission order, waits for each job's copy event itself, calls the archive and
+    enqueues the results' copy into device staging. Nothing here polls or forwards messages: a
+    method only reads states, and the worker moves them;
+  * an eviction batch is one pinned upload of a (layer, head, row) descriptor list with the
+    layers' pointer table and one packing launch for every layer (lr_pack_layers); a search's
+    queries are one launch averaging every layer's group queries (lr_group_mean_queries);
+  * the buffers are torch's: pinned host staging (``host``), device staging, allocated once.
 """
 
 from __future__ import annotations
 
-import queue
-import resource
-import threading
-import time
-from collections import deque
+import ctypes
+import os
+from pathlib import Path
 
 import numpy as np
 import torch
 
-from . import _C
-from .archive import ArchiveIndex
+from . import _lib
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "liblazyrecall_recall.so"
+
+_P, _I64, _I, _D = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double
+_IP = ctypes.POINTER(ctypes.c_int)
+SIGNATURES = {
+    "lrr_last_error": ([], ctypes.c_char_p),
+    "lrr_create": ([_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I] + [_P] * 10, _P),
+    "lrr_destroy": ([_P], None),
+    "lrr_acquire_archive": ([_P, _D, _IP, _IP], _I),
+    "lrr_abandon_archive": ([_P, _I], _I),
+    "lrr_commit_archive": ([_P, _I, _I64, _P], _I),
+    "lrr_acquire_query": ([_P, _IP], _I),
+    "lrr_abandon_query": ([_P, _I], _I),
+    "lrr_commit_query": ([_P, _I, _I64, _P], _I),
+    "lrr_result_ready": ([_P, _I], _I),
+    "lrr_release_result": ([_P, _I, _P], _I),
+    "lrr_drop_result": ([_P, _I], _I),
+    "lrr_retire": ([_P], _I),
+    "lrr_remove": ([_P, _P, _I64], _I),
+    "lrr_wait_pending": ([_P, _D], _I),
+    "lrr_flush": ([_P, _D], _I),
+    "lrr_archive_state": ([_P, _I], _I),
+    "lrr_query_state": ([_P, _I], _I),
+    "lrr_query_step": ([_P, _I], _I64),
+    "lrr_result_count": ([_P, _I], _I64),
+    "lrr_counters": ([_P, _P], _I),
+    "lrr_worker_alive": ([_P], _I),
+    "lrr_check": ([_P], _I),
+}
+ARCHIVE_STATES = ("free", "filling", "copying", "worker")
+QUERY_STATES = ("free", "filling", "copying_query", "worker", "copying_result", "retiring")
+RESULT_STATE = 4
+# the counter keys the ring's worker keeps, in lrr_counters order
+WORKER_COUNTERS = ("indexed_vectors", "capacity_drops", "searches_completed", "retrieved_vectors",
+                   "h2d_bytes", "cpu_peak_rss_kib")
+_TIMEOUT = 3
+_library = None
 
 
-def _worker(index, topk, views, commands, replies):
-    """cpu_worker.py:136-182 as a thread: the same commands and replies."""
-    try:
-        while True:
-            message = commands.get()
-            kind, slot = message["kind"], message.get("slot")
-            started = time.perf_counter_ns()
-            if kind == "stop":
-                return
-            if kind == "archive":
-                count = message["count"]
-                index.add(views["archive_meta"][slot, :count], views["archive_kv"][slot, :count])
-                reply = dict(kind="archived", slot=slot, count=count)
-            elif kind == "remove":
-                index.remove(message["metadata"])
-                continue
-            elif kind == "search":
-                metadata, payload = index.search(views["queries"][slot], topk)
-                count = len(metadata)
-                views["result_meta"][slot, :count] = metadata
-                views["result_kv"][slot, :count] = payload
-                reply = dict(kind="searched", slot=slot, count=count, query_step=message["step"])
-            elif kind == "flush":
-                reply = dict(kind="flushed")
-            else:
-                raise ValueError(f"Unknown worker command: {kind}")
-            reply.update(indexed=index.size, capacity_drops=index.dropped, start_ns=started,
-                         end_ns=time.perf_counter_ns(),
-                         cpu_peak_rss_kib=resource.getrusage(resource.RUSAGE_SELF).ru_maxrss)
-            replies.put(reply)
-    except BaseException:  # reported to the owner like the reference's worker errors
-        import traceback
+def load() -> ctypes.CDLL:
+    """liblazyrecall_recall.so, opened once after torch (one HIP runtime per process)."""
+    global _library
+    if _library is None:
+        if not LIBRARY_PATH.exists():
+            raise _lib.LazyRecallLibraryError(
+                f"{LIBRARY_PATH.name} is not built; run `python -m code_for_iclr27_amd.build`")
+        library = ctypes.CDLL(os.fspath(LIBRARY_PATH))
+        for name, (argtypes, restype) in SIGNATURES.items():
+            function = getattr(library, name)
+            function.argtypes, function.restype = argtypes, restype
+        _library = library
+    return _library
 
-        replies.put(dict(kind="error", traceback=traceback.format_exc()))
+
+def _check(status: int) -> None:
+    if status == 0:
+        return
+    message = load().lrr_last_error().decode()
+    if status == _TIMEOUT:
+        raise TimeoutError(message)
+    raise RuntimeError(message)
+
+
+class _WorkerView:
+    """The ring's worker thread as seen from Python (``is_alive``)."""
+
+    name = "LazyRecall-CPU-archive"
+
+    def __init__(self, transport):
+        self._transport = transport
+
+    def is_alive(self) -> bool:
+        ring = self._transport._ring
+        return bool(ring) and bool(load().lrr_worker_alive(ring))
 
 
 class RecallTransport:
-    def __init__(self, layers, heads, query_heads, dimension, search_interval=32,
-                 topk=4, archive_buffers=16, cpu_threads=2, evict_interval=8,
+    def __init__(self, layers, heads, query_heads, dimension, search_interval=32, topk=4,
+                 archive_buffers=16, cpu_threads=2, evict_interval=8,
                  archive_capacity_per_head=32768, timeout_seconds=60.0):
-        if query_heads % heads or min(layers, heads, dimension, search_interval, topk,
-                                      archive_buffers, cpu_threads) <= 0:
+        if (query_heads % heads or min(layers, heads, dimension, search_interval, topk,
+                                        archive_buffers, cpu_threads) <= 0):
             raise ValueError("Invalid recall configuration")
-        self.layers, self.heads, self.groups = layers, heads, query_heads // heads
-        self.dimension = dimension
-        self.search_interval = search_interval
+        self.layers, self.heads, self.dimension = int(layers), int(heads), int(dimension)
+        self.groups = query_heads // heads
+        self.search_interval, self.topk = int(search_interval), int(topk)
         self.capacity = max(evict_interval, topk) * layers * heads
         self.result_capacity = topk * layers * heads
-        self.timeout = timeout_seconds
+        self.timeout = float(timeout_seconds)
         self.closed = False
-        self.thread = None
-        self.copy_stream = torch.cuda.Stream()
-        self.archive_states = ["free"] * archive_buffers
-        self.query_states = ["free"] * 2
-        self.archive_jobs, self.query_jobs, self.events = {}, {}, deque(maxlen=32)
-        self.counters = dict(archived_vectors=0, archive_batches=0, indexed_vectors=0,
-                             submitted_queries=0, searches_completed=0, skipped_busy_queries=0,
-                             retrieved_vectors=0, spliced_vectors=0, splices=0,
-                             d2h_bytes=0, h2d_bytes=0, archive_overflows=0,
-                             cpu_peak_rss_kib=0, query_age_tokens_max=0,
-                             archive_backpressure=0, capacity_drops=0, superseded_results=0)
-        specs = dict(archive_kv=((archive_buffers, self.capacity, 2, dimension), torch.int16),
-                     archive_meta=((archive_buffers, self.capacity, 3), torch.int64),
-                     queries=((2, layers, heads, dimension), torch.float32),
-                     result_kv=((2, self.result_capacity, 2, dimension), torch.int16),
-                     result_meta=((2, self.result_capacity, 3), torch.int64))
-        self.host = {name: torch.empty(shape, dtype=dtype, pin_memory=True)
-                     for name, (shape, dtype) in specs.items()}
-        views = {name: tensor.numpy() for name, tensor in self.host.items()}
-        views["archive_kv"] = views["archive_kv"].view(np.uint16)
-        views["result_kv"] = views["result_kv"].view(np.uint16)
-        self.views = views
-        self.archive_gpu = torch.empty(specs["archive_kv"][0], device="cuda", dtype=torch.bfloat16)
-        self.archive_meta_gpu = torch.empty(specs["archive_meta"][0], device="cuda", dtype=torch.int64)
-        self.query_gpu = torch.empty(specs["queries"][0], device="cuda", dtype=torch.float32)
-        self.result_gpu = torch.empty(specs["result_kv"][0], device="cuda", dtype=torch.bfloat16)
-        self.result_meta_gpu = torch.empty(specs["result_meta"][0], device="cuda", dtype=torch.int64)
+        self._ring = None
+        self.counters = dict.fromkeys(
+            ("archived_vectors", "archive_batches", "indexed_vectors", "submitted_queries",
+             "searches_completed", "skipped_busy_queries", "retrieved_vectors", "spliced_vectors",
+             "splices", "d2h_bytes", "h2d_bytes", "archive_overflows", "cpu_peak_rss_kib",
+             "query_age_tokens_max", "archive_backpressure", "capacity_drops",
+             "superseded_results"), 0)
         self.config = dict(layers=layers, heads=heads, dimension=dimension, topk=topk,
                            cpu_threads=cpu_threads,
                            archive_capacity_per_head=archive_capacity_per_head)
-        self.index = ArchiveIndex(layers, heads, dimension, cpu_threads, archive_capacity_per_head)
-        self.commands = queue.Queue(maxsize=archive_buffers + 6)
-        self.replies = queue.Queue()
-        self.thread = threading.Thread(target=_worker, name="LazyRecall-CPU-archive", daemon=True,
-                                       args=(self.index, topk, views, self.commands, self.replies))
-        self.thread.start()
-        self.worker_info = dict(kind="ready", thread=self.thread.name, archive="exact-MIPS C++")
+        L, H, d, B = self.layers, self.heads, self.dimension, int(archive_buffers)
+        shapes = dict(archive_kv=((B, self.capacity, 2, d), torch.int16),
+                      archive_meta=((B, self.capacity, 3), torch.int64),
+                      queries=((2, L, H, d), torch.float32),
+                      result_kv=((2, self.result_capacity, 2, d), torch.int16),
+                      result_meta=((2, self.result_capacity, 3), torch.int64))
+        self.host = {name: torch.empty(shape, dtype=dtype, pin_memory=True)
+                     for name, (shape, dtype) in shapes.items()}
+        device = torch.device("cuda", torch.cuda.current_device())
+        self.device = device
+        self.archive_gpu = torch.empty(shapes["archive_kv"][0], dtype=torch.bfloat16, device=device)
+        self.archive_meta_gpu = torch.empty(shapes["archive_meta"][0], dtype=torch.int64, device=device)
+        self.query_gpu = torch.empty(shapes["queries"][0], dtype=torch.float32, device=device)
+        self.result_gpu = torch.empty(shapes["result_kv"][0], dtype=torch.bfloat16, device=device)
+        self.result_meta_gpu = torch.empty(shapes["result_meta"][0], dtype=torch.int64, device=device)
+        ring = load().lrr_create(
+            L, H, d, self.topk, B, self.capacity, self.result_capacity,
+            int(archive_capacity_per_head), int(cpu_threads), device.index,
+            *(self.host[name].data_ptr() for name in shapes),
+            *(t.data_ptr() for t in (self.archive_gpu, self.archive_meta_gpu, self.query_gpu,
+                                     self.result_gpu, self.result_meta_gpu)))
+        if not ring:
+            raise ValueError(load().lrr_last_error().decode())
+        self._ring = ring
+        self.thread = _WorkerView(self)
+        self.worker_info = dict(kind="ready", thread=_WorkerView.name, pid=os.getpid(),
+                                archive="exact-MIPS (host C++)")
 
-    def _send(self, message):
-        try:
-            self.commands.put(message, timeout=self.timeout)
-        except queue.Full as error:
-            raise RuntimeError("Recall command queue backpressure exceeded timeout") from error
+    # ---- states --------------------------------------------------------------------------
+    @property
+    def archive_states(self):
+        library = load()
+        return [ARCHIVE_STATES[library.lrr_archive_state(self._ring, s)]
+                for s in range(self.host["archive_kv"].shape[0])]
 
-    def _copy_out(self, pairs):
-        packed = torch.cuda.Event()
-        packed.record(torch.cuda.current_stream())
-        done = torch.cuda.Event()
-        with torch.cuda.stream(self.copy_stream):
-            self.copy_stream.wait_event(packed)
-            for destination, source in pairs:
-                destination.copy_(source, non_blocking=True)
-                self.counters["d2h_bytes"] += source.numel() * source.element_size()
-            done.record(self.copy_stream)
-        return done
+    @property
+    def query_states(self):
+        library = load()
+        return [QUERY_STATES[library.lrr_query_state(self._ring, s)] for s in range(2)]
+
+    def pump(self):
+        """Reports a worker failure and refreshes the worker's counters (the worker advances
+        the slots by itself; there is nothing to forward)."""
+        if self.closed:
+            return
+        library = load()
+        if not library.lrr_worker_alive(self._ring):
+            raise RuntimeError("CPU recall worker exited unexpectedly")
+        _check(library.lrr_check(self._ring))
+        values = (ctypes.c_int64 * len(WORKER_COUNTERS))()
+        _check(library.lrr_counters(self._ring, values))
+        for key, value in zip(WORKER_COUNTERS, values):
+            self.counters[key] = int(value)
+
+    # ---- eviction batches ----------------------------------------------------------------
+    @staticmethod
+    def _batch(removals):
+        """(layer, head, position) of every distinct removed slot, in (layer, head, position)
+        order: the order the reference packs and archives them (transport.py:141-167)."""
+        keys = sorted(removals)
+        parts = [np.asarray(removals[key], dtype=np.int64).reshape(-1) for key in keys]
+        sizes = np.fromiter((len(p) for p in parts), dtype=np.int64, count=len(parts))
+        if not sizes.sum():
+            return np.empty((0, 3), np.int64)
+        coordinates = np.asarray(keys, dtype=np.int64).reshape(-1, 2)
+        segment = np.repeat(np.arange(len(keys), dtype=np.int64), sizes)
+        positions = np.concatenate(parts)
+        order = np.lexsort((positions, segment))
+        segment, positions = segment[order], positions[order]
+        keep = np.ones(len(positions), dtype=bool)
+        keep[1:] = (segment[1:] != segment[:-1]) | (positions[1:] != positions[:-1])
+        segment, positions = segment[keep], positions[keep]
+        return np.column_stack((coordinates[segment, 0], coordinates[segment, 1], positions))
 
     @torch.no_grad()
     def record_evicted(self, cache, removals):
-        """transport.py:130-177: gather {(layer, head): positions} into a free staging slot with
-        the pack kernel and start its copy to host memory."""
+        """transport.py:129-177: pack the evicted rows of every layer into a free archive slot,
+        copy them out and archive them (the latter two by the ring, in the background)."""
         self.pump()
-        count = sum(len(set(positions)) for positions in removals.values())
+        batch = self._batch(removals)
+        count = len(batch)
         if count == 0:
             return
         if count > self.capacity:
             self.counters["archive_overflows"] += 1
             raise RuntimeError("Eviction batch exceeds configured archive staging capacity")
-        started = time.perf_counter()
-        if "free" not in self.archive_states:
+        library = load()
+        slot, waited = ctypes.c_int(-1), ctypes.c_int(0)
+        status = library.lrr_acquire_archive(self._ring, self.timeout, ctypes.byref(slot),
+                                             ctypes.byref(waited))
+        if waited.value:
             self.counters["archive_backpressure"] += 1
-        while "free" not in self.archive_states:
-            if time.perf_counter() - started > self.timeout:
-                raise TimeoutError("CPU archive backpressure exceeded timeout")
-            self.pump()
-            time.sleep(0.001)
-        slot = self.archive_states.index("free")
-        # Every layer's absolute rows and head ids in one host array, uploaded with one
-        # non-blocking copy from pinned memory (the reference uploads two tensors per layer).
-        plan = []
-        rows_all, heads_all = [], []
-        for layer in sorted({layer for layer, _ in removals}):
-            bounds = np.concatenate(([0], np.cumsum(cache.metadata_list[layer].head_lens_cpu)))
-            start = len(rows_all)
-            for (record_layer, head), positions in sorted(removals.items()):
-                if record_layer == layer:
-                    selected = sorted(set(int(position) for position in positions))
-                    rows_all.extend(int(bounds[head]) + position for position in selected)
-                    heads_all.extend([head] * len(selected))
-            if len(rows_all) > start:
-                plan.append((layer, start, len(rows_all)))
-        table = torch.tensor([rows_all, heads_all], dtype=torch.int64).pin_memory()
-        table = table.to("cuda", non_blocking=True)
-        cursor = 0
-        for layer, start, end in plan:
-            _C.pack(cache.key_cache[layer].contiguous(), cache.value_cache[layer].contiguous(),
-                    cache.position_cache[layer].contiguous(), table[0, start:end],
-                    table[1, start:end], layer, self.archive_gpu[slot, start:end],
-                    self.archive_meta_gpu[slot, start:end])
-            cursor = end
-        if cursor != count:
-            raise AssertionError("Archive packing count mismatch")
-        done = self._copy_out([
-            (self.host["archive_kv"][slot, :count].view(torch.bfloat16), self.archive_gpu[slot, :count]),
-            (self.host["archive_meta"][slot, :count], self.archive_meta_gpu[slot, :count]),
-        ])
-        self.archive_states[slot] = "copying"
-        self.archive_jobs[slot] = dict(event=done, count=count)
+        _check(status)
+        slot = slot.value
+        try:
+            self._pack(cache, batch, slot)
+            _check(library.lrr_commit_archive(self._ring, slot, count,
+                                              torch.cuda.current_stream(self.device).cuda_stream))
+        except BaseException:
+            library.lrr_abandon_archive(self._ring, slot)
+            raise
         self.counters["archived_vectors"] += count
         self.counters["archive_batches"] += 1
+        self.counters["d2h_bytes"] += count * (2 * self.dimension * 2 + 3 * 8)
 
-    @torch.no_grad()
-    def pump(self):
-        """transport.py:180-229: advance every slot whose copy or worker job has finished."""
-        if self.closed:
-            return
-        if not self.thread.is_alive():
-            raise RuntimeError("CPU recall worker exited unexpectedly")
-        for slot, job in list(self.archive_jobs.items()):
-            if self.archive_states[slot] == "copying" and job["event"].query():
-                self._send(dict(kind="archive", slot=slot, count=job["count"]))
-                self.archive_states[slot] = "worker"
-        for slot, job in list(self.query_jobs.items()):
-            if self.query_states[slot] == "copying_query" and job["event"].query():
-                self._send(dict(kind="search", slot=slot, step=job["step"]))
-                self.query_states[slot] = "worker"
-        while True:
-            try:
-                message = self.replies.get_nowait()
-            except queue.Empty:
-                break
-            kind, slot = message["kind"], message.get("slot")
-            if kind == "error":
-                raise RuntimeError(message["traceback"])
-            if kind not in ("archived", "searched", "flushed"):
-                raise RuntimeError(f"Unexpected CPU reply: {message}")
-            self.events.append(dict(kind=kind, start_ns=message["start_ns"], end_ns=message["end_ns"]))
-            self.counters["indexed_vectors"] = message["indexed"]
-            self.counters["capacity_drops"] = message.get("capacity_drops", 0)
-            self.counters["cpu_peak_rss_kib"] = max(self.counters["cpu_peak_rss_kib"],
-                                                    message["cpu_peak_rss_kib"])
-            if kind == "flushed":
-                self._flushed = True
-            elif kind == "archived":
-                del self.archive_jobs[slot]
-                self.archive_states[slot] = "free"
-            else:
-                self.counters["searches_completed"] += 1
-                self.counters["retrieved_vectors"] += message["count"]
-                job = self.query_jobs[slot]
-                job.update(count=message["count"], indexed=message["indexed"])
-                if not message["count"]:
-                    del self.query_jobs[slot]
-                    self.query_states[slot] = "free"
-                    continue
-                count = job["count"]
-                done = torch.cuda.Event()
-                with torch.cuda.stream(self.copy_stream):
-                    self.result_gpu[slot, :count].copy_(
-                        self.host["result_kv"][slot, :count].view(torch.bfloat16), non_blocking=True)
-                    self.result_meta_gpu[slot, :count].copy_(self.host["result_meta"][slot, :count],
-                                                             non_blocking=True)
-                    done.record(self.copy_stream)
-                self.counters["h2d_bytes"] += count * (2 * self.dimension * 2 + 3 * 8)
-                job["event"] = done
-                self.query_states[slot] = "copying_result"
+    def _pack(self, cache, batch, slot):
+        """One upload (layer pointer table + row descriptors) and one lr_pack_layers launch."""
+        L, count = self.layers, len(batch)
+        block = torch.empty((4 * L + 3 * count,), dtype=torch.int64, pin_memory=True)
+        words = block.numpy()
+        table = words[:4 * L].reshape(L, 4)
+        table[:] = 0
+        rows = words[4 * L:].reshape(count, 3)
+        rows[:, :2] = batch[:, :2]
+        for layer in np.unique(batch[:, 0]).tolist():
+            keys, values = cache.key_cache[layer], cache.value_cache[layer]
+            positions = cache.position_cache[layer]
+            if not (keys.is_cuda and keys.is_contiguous() and values.is_contiguous()
+                    and positions.is_contiguous() and keys.dtype in (torch.bfloat16, torch.float16)
+                    and values.dtype == keys.dtype and positions.dtype == torch.float32
+                    and keys.shape == values.shape and positions.numel() == keys.shape[0]
+                    and keys.shape[1] == self.dimension):
+                raise RuntimeError("Expected contiguous CUDA tensor")
+            if keys.data_ptr() % 16 or values.data_ptr() % 16:
+                raise RuntimeError("Cache rows must be aligned to the row granule")
+            starts = np.concatenate(([0], np.cumsum(cache.metadata_list[layer].head_lens_cpu)))
+            selected = batch[:, 0] == layer
+            rows[selected, 2] = starts[batch[selected, 1]] + batch[selected, 2]
+            table[layer] = (keys.data_ptr(), values.data_ptr(), positions.data_ptr(), keys.shape[0])
+        device_block = block.to(self.device, non_blocking=True)
+        _lib.call("lr_pack_layers", device_block.data_ptr(), L,
+                  device_block.data_ptr() + 8 * 4 * L, count, self.dimension,
+                  self.archive_gpu[slot].data_ptr(), self.archive_meta_gpu[slot].data_ptr(),
+                  torch.cuda.current_stream(self.device).cuda_stream)
 
-    def release_result(self, slot):
-        complete = torch.cuda.Event()
-        complete.record(torch.cuda.current_stream())
-        self.query_jobs[slot]["event"] = complete
-        self.query_states[slot] = "retiring"
-
-    def retire_finished(self):
-        for slot, job in list(self.query_jobs.items()):
-            if self.query_states[slot] == "retiring" and job["event"].query():
-                del self.query_jobs[slot]
-                self.query_states[slot] = "free"
-
-    def ready_result(self):
-        """transport.py:243-258: the newest search result resident in HBM, older ones released:
-        (slot, step, payload [n, 2, d] bf16, metadata [n, 3] i64 on the device, metadata host)."""
-        self.pump()
-        self.retire_finished()
-        candidates = [(job["step"], slot) for slot, job in self.query_jobs.items()
-                      if self.query_states[slot] == "copying_result" and job["event"].query()]
-        if not candidates:
-            return None
-        _, chosen = max(candidates)
-        for _, slot in candidates:
-            if slot != chosen:
-                self.release_result(slot)
-                self.counters["superseded_results"] += 1
-        job = self.query_jobs[chosen]
-        return (chosen, job["step"], self.result_gpu[chosen, :job["count"]],
-                self.result_meta_gpu[chosen, :job["count"]],
-                self.views["result_meta"][chosen, :job["count"]].copy())
-
-    def remove_admitted(self, metadata):
-        self._send(dict(kind="remove", metadata=np.asarray(metadata, dtype=np.int64).tolist()))
-
-    def wait_pending(self):
-        started = time.perf_counter()
-        while self.archive_jobs or any(
-            self.query_states[slot] in ("copying_query", "worker")
-            or (self.query_states[slot] == "copying_result" and not job["event"].query())
-            for slot, job in self.query_jobs.items()
-        ):
-            if time.perf_counter() - started > self.timeout:
-                raise TimeoutError("Recall diagnostic wait exceeded timeout")
-            self.pump()
-            self.retire_finished()
-            time.sleep(0.001)
-
+    # ---- searches ------------------------------------------------------------------------
     @torch.no_grad()
     def step(self, model, cache, step):
-        """transport.py:277-301: every search_interval steps, submit one query per (layer, KV
-        head): the mean over its query group of the last decode query."""
-        del cache
+        """transport.py:276-301: every search_interval decode steps, the group-mean decode
+        queries of every layer go to the archive; the newest results come back to HBM."""
         self.pump()
         self.retire_finished()
         if step % self.search_interval or not self.counters["archived_vectors"]:
             return
-        if "free" not in self.query_states:
-            ready = [(job["step"], slot) for slot, job in self.query_jobs.items()
-                     if self.query_states[slot] == "copying_result" and job["event"].query()]
+        library = load()
+        slot = ctypes.c_int(-1)
+        _check(library.lrr_acquire_query(self._ring, ctypes.byref(slot)))
+        if slot.value < 0:  # both slots busy: drop the older finished result nobody took
+            ready = [(library.lrr_query_step(self._ring, s), s) for s in range(2)
+                     if library.lrr_result_ready(self._ring, s)]
             if ready:
-                _, oldest = min(ready)
-                del self.query_jobs[oldest]
-                self.query_states[oldest] = "free"
+                _check(library.lrr_drop_result(self._ring, min(ready)[1]))
                 self.counters["superseded_results"] += 1
-        if "free" not in self.query_states:
+                _check(library.lrr_acquire_query(self._ring, ctypes.byref(slot)))
+        if slot.value < 0:
             self.counters["skipped_busy_queries"] += 1
             return
-        slot = self.query_states.index("free")
-        for layer, block in enumerate(model.model.layers):
-            query = block.self_attn._last_query_states.detach()[0, :, 0]
-            self.query_gpu[slot, layer].copy_(
-                query.view(self.heads, self.groups, self.dimension).float().mean(dim=1))
-        done = self._copy_out([(self.host["queries"][slot], self.query_gpu[slot])])
-        self.query_jobs[slot] = dict(event=done, step=step)
-        self.query_states[slot] = "copying_query"
+        slot = slot.value
+        try:
+            self._query_means(model, slot)
+            _check(library.lrr_commit_query(self._ring, slot, int(step),
+                                            torch.cuda.current_stream(self.device).cuda_stream))
+        except BaseException:
+            library.lrr_abandon_query(self._ring, slot)
+            raise
         self.counters["submitted_queries"] += 1
+        self.counters["d2h_bytes"] += self.layers * self.heads * self.dimension * 4
+
+    def _query_means(self, model, slot):
+        blocks = model.model.layers
+        if len(blocks) != self.layers:
+            raise RuntimeError("Model layer count differs from the recall configuration")
+        table = torch.empty((self.layers, 2), dtype=torch.int64, pin_memory=True)
+        words = table.numpy()
+        dtype = None
+        for layer, block in enumerate(blocks):
+            query = block.self_attn._last_query_states.detach()[0, :, 0]  # [Hq, d]
+            if (not query.is_cuda or query.shape != (self.heads * self.groups, self.dimension)
+                    or query.stride(1) != 1):
+                raise RuntimeError("Historical query-head count changed")
+            if dtype is None:
+                dtype = query.dtype
+            elif query.dtype != dtype:
+                raise RuntimeError("Query dtypes differ between layers")
+            words[layer] = (query.data_ptr(), query.stride(0))
+        _lib.call("lr_group_mean_queries", table.to(self.device, non_blocking=True).data_ptr(),
+                  self.layers, self.heads, self.groups, self.dimension, _lib.DTYPE_CODES[dtype],
+                  self.query_gpu[slot].data_ptr(), torch.cuda.current_stream(self.device).cuda_stream)
+
+    def ready_result(self):
+        """transport.py:263-280: the newest search whose results are in HBM, as (slot, step,
+        payload [n, 2, d] bf16, metadata [n, 3] i64 on the device, metadata on the host); older
+        finished results are released."""
+        self.pump()
+        self.retire_finished()
+        library = load()
+        ready = [(library.lrr_query_step(self._ring, s), s) for s in range(2)
+                 if library.lrr_result_ready(self._ring, s)]
+        if not ready:
+            return None
+        step, chosen = max(ready)
+        for _, slot in ready:
+            if slot != chosen:
+                self.release_result(slot)
+                self.counters["superseded_results"] += 1
+        count = int(library.lrr_result_count(self._ring, chosen))
+        return (chosen, int(step), self.result_gpu[chosen, :count],
+                self.result_meta_gpu[chosen, :count],
+                self.host["result_meta"][chosen, :count].numpy().copy())
+
+    def release_result(self, slot):
+        """The consumer's work on the current stream is the slot's last use (transport.py:
+        231-235)."""
+        _check(load().lrr_release_result(self._ring, int(slot),
+                                         torch.cuda.current_stream(self.device).cuda_stream))
+
+    def retire_finished(self):
+        if self._ring:
+            _check(load().lrr_retire(self._ring))
+
+    def remove_admitted(self, metadata):
+        metadata = np.ascontiguousarray(np.asarray(metadata, dtype=np.int64).reshape(-1, 3))
+        _check(load().lrr_remove(self._ring, metadata.ctypes.data, len(metadata)))
+
+    def wait_pending(self):
+        """Every archive batch archived, every search answered and its results in HBM."""
+        _check(load().lrr_wait_pending(self._ring, self.timeout))
+        self.pump()
 
     def finish(self):
+        """transport.py:328-343: results nobody took are released, the consumer's stream is
+        drained, and every queued job (removals included) has run."""
         self.wait_pending()
-        for slot in list(self.query_jobs):
-            if self.query_states[slot] == "copying_result":
+        library = load()
+        for slot in range(2):
+            if library.lrr_query_state(self._ring, slot) == RESULT_STATE:
                 self.release_result(slot)
-        torch.cuda.current_stream().synchronize()
+        torch.cuda.current_stream(self.device).synchronize()
         self.retire_finished()
-        self._flushed = False
-        self._send(dict(kind="flush"))
-        started = time.perf_counter()
-        while not self._flushed:
-            if time.perf_counter() - started > self.timeout:
-                raise TimeoutError("CPU archive flush exceeded timeout")
-            self.pump()
-            time.sleep(0.001)
+        _check(library.lrr_flush(self._ring, self.timeout))
+        self.pump()
 
     @property
     def stats(self):
         if hasattr(self, "_closed_stats"):
             return dict(self._closed_stats)
+        device = (self.archive_gpu, self.archive_meta_gpu, self.query_gpu, self.result_gpu,
+                  self.result_meta_gpu)
         return dict(self.counters, worker=self.worker_info,
-                    pinned_host_bytes=sum(t.numel() * t.element_size() for t in self.host.values()),
-                    gpu_staging_bytes=sum(t.numel() * t.element_size() for t in
-                                          (self.archive_gpu, self.archive_meta_gpu, self.query_gpu,
-                                           self.result_gpu, self.result_meta_gpu)))
+                    registered_shared_bytes=sum(t.numel() * t.element_size()
+                                                for t in self.host.values()),
+                    gpu_staging_bytes=sum(t.numel() * t.element_size() for t in device))
 
     def close(self, abort=False):
+        """Stops the worker (after the jobs already queued) and releases the ring; the
+        staging buffers go with this object."""
         if self.closed:
             return
-        self._closed_stats = self.stats
-        self.closed = True
-        if self.thread is not None and self.thread.is_alive():
-            try:
-                self.commands.put(dict(kind="stop"), timeout=5)
-            except queue.Full:
-                pass
+        if self._ring:
             if not abort:
-                self.thread.join(timeout=self.timeout)
-        torch.cuda.synchronize()
-        for name in ("archive_gpu", "archive_meta_gpu", "query_gpu", "result_gpu", "result_meta_gpu"):
-            if hasattr(self, name):
-                delattr(self, name)
+                self.pump()
+            self._closed_stats = self.stats
+            load().lrr_destroy(self._ring)
+            self._ring = None
+        self.closed = True
+        torch.cuda.synchronize(self.device)
+
+    def __del__(self):
+        if getattr(self, "_ring", None) and _library is not None:
+            _library.lrr_destroy(self._ring)
+            self._ring = None

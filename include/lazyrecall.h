@@ -105,6 +105,24 @@ int lr_batch_append(const int64_t* descriptors, int64_t segments, const void* ne
                     const void* new_values, int64_t dim, int elem_bytes, int64_t max_rows,
                     void* out_keys, void* out_values, float* out_positions, void* stream);
 
+/* All-layer pack of one eviction batch: the per-layer _C.pack calls of record_evicted
+ * (src/lazy_recall/recall/transport.py:150-167, csrc/recall.cu:30-47) in one launch.
+ * layer_table: DEVICE [layers, 4] i64 = (keys ptr, values ptr, positions ptr (f32), rows) per
+ * layer; rows: DEVICE [count, 3] i64 = (layer, head, row within the layer). Writes payload
+ * [count, 2, dim] (key row, value row; 2-byte elements) and metadata [count, 3] i64 = (layer,
+ * head, int64(position)). dim * 2 a multiple of 16; payload and every key/value buffer 16-byte
+ * aligned. A descriptor whose layer or row is out of range leaves its output row unwritten. */
+int lr_pack_layers(const int64_t* layer_table, int64_t layers, const int64_t* rows,
+                   int64_t count, int64_t dim, void* payload, int64_t* metadata, void* stream);
+
+/* Group-mean decode queries of every layer (src/lazy_recall/recall/transport.py:293-296: the
+ * last decode query [Hq, d] of each layer viewed as [H, G, d] and averaged over G in f32).
+ * query_table: DEVICE [layers, 2] i64 = (queries ptr, query-head stride in elements);
+ * queries of `dtype` (BF16/F16/F32), dim contiguous. out f32 [layers, heads, dim]: the G values
+ * summed in order, divided by G. */
+int lr_group_mean_queries(const int64_t* query_table, int64_t layers, int64_t heads,
+                          int64_t groups, int64_t dim, int dtype, float* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Module lazy_recall._legacy_C (csrc/cache_legacy.cu:304-308)
  * ------------------------------------------------------------------------------------- */
