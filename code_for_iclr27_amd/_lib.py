@@ -19,6 +19,8 @@ LR_OK = 0
 LR_DTYPE_F32, LR_DTYPE_F64, LR_DTYPE_F16, LR_DTYPE_BF16 = 0, 1, 2, 3
 LR_SEG_WORDS = 12
 LR_HEAD_WORDS = 6
+LR_REINSERT_WORDS = 8
+LR_REINSERT_MAX_PER_HEAD = 4096
 LR_HISTORY_MAX_LAYERS = 128
 
 _P = ctypes.c_void_p
@@ -60,6 +62,9 @@ SIGNATURES = {
                               _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
+    "lr_reinsert_plan": [_P, _I64, _P, _I64, _P, _P, _P, _P],
+    "lr_reinsert_resident": [_P, _I64, _P, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
+    "lr_reinsert_recalled": [_P, _I64, _P, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_queue_index": [_P, _P, _I64, _P, _P, _P, _I64, _P, _P],
     "lr_queue_evict_plan": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P],
     "lr_history_append": [_P, _I64, _I64, _I64, _I, _I64, _I64, _P, _I64, _P, _P],

@@ -709,6 +709,115 @@ py::tuple queue_evict_launch(const std::vector<torch::Tensor>& keys,
   return py::make_tuple(out_keys, out_values, out_positions, kept, layer_offsets);
 }
 
+// Host planning of a reinsertion (insert_payload, cache.py:201-253, for every layer): checks the
+// layers and the recalled identities, counts each (layer, head)'s recalled rows (which fixes
+// the new layout without any device read), and writes one pinned int64 block: the reinsert table
+// (LR_REINSERT_WORDS per slot, lr_reinsert_plan), then the recalled positions grouped by slot
+// (each slot's run in input order) and the input index of each grouped entry. Layers
+// come as per-layer tensors, or packed: one tensor each plus the first row of every layer
+// (packed_offsets, layers + 1 entries). Returns (block, new head lengths [L][H], first row of
+// each merged layer [L + 1], output rows, longest resident head).
+py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
+                           const std::vector<torch::Tensor>& values,
+                           const std::vector<torch::Tensor>& positions,
+                           const std::vector<std::vector<int64_t>>& head_lens,
+                           const std::vector<int64_t>& packed_offsets,
+                           const torch::Tensor& metadata) {
+  const bool packed = !packed_offsets.empty();
+  const size_t layers = head_lens.size();
+  require(layers > 0 && (packed ? packed_offsets.size() == layers + 1 && keys.size() == 1 &&
+                                      values.size() == 1 && positions.size() == 1
+                                : keys.size() == layers && values.size() == layers &&
+                                      positions.size() == layers),
+          "Layer lists differ in length");
+  const int64_t heads = static_cast<int64_t>(head_lens[0].size());
+  require(heads > 0, "Invalid KV layout");
+  require(!metadata.is_cuda() && metadata.is_contiguous() &&
+              metadata.scalar_type() == torch::kInt64 && metadata.dim() == 2 &&
+              metadata.size(1) == 3,
+          "Recall metadata must be a contiguous int64 [count, 3] host array");
+  const int64_t count = metadata.size(0);
+  const int64_t slots = static_cast<int64_t>(layers) * heads;
+  std::vector<int64_t> counts(static_cast<size_t>(slots), 0);
+  const int64_t* meta = metadata.data_ptr<int64_t>();
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t layer = meta[3 * i], head = meta[3 * i + 1], position = meta[3 * i + 2];
+    require(layer >= 0 && layer < static_cast<int64_t>(layers) && head >= 0 && head < heads &&
+                position >= 0 && position < (int64_t{1} << 31),
+            "Invalid recall identity");
+    ++counts[layer * heads + head];
+  }
+  const torch::Tensor& k0 = keys[0];
+  require(k0.dim() == 2 && k0.size(1) > 0, "Invalid KV layout");
+  const int64_t dim = k0.size(1);
+  const auto dtype = k0.scalar_type();
+  const torch::Device device = k0.device();
+  const int64_t row_bytes = dim * static_cast<int64_t>(k0.element_size());
+  for (size_t t = 0; t < keys.size(); ++t) {
+    const torch::Tensor &k = keys[t], &v = values[t], &p = positions[t];
+    for (const torch::Tensor* x : {&k, &v, &p})
+      require(x->is_cuda() && x->is_contiguous() && x->device() == device,
+              "Expected contiguous CUDA tensor");
+    require(k.dim() == 2 && k.sizes() == v.sizes() && k.size(1) == dim &&
+                k.scalar_type() == dtype && v.scalar_type() == dtype,
+            "Expected contiguous CUDA tensor");
+    require(p.scalar_type() == torch::kFloat32 && p.numel() == k.size(0),
+            "Position lengths do not match metadata");
+  }
+  torch::Tensor block = torch::empty({slots * LR_REINSERT_WORDS + 2 * count},
+                                     torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
+  int64_t* table = block.data_ptr<int64_t>();
+  py::list new_lens(layers), offsets(layers + 1);
+  offsets[0] = py::int_(0);
+  int64_t run = 0, out_row = 0, max_length = 0;
+  for (size_t l = 0; l < layers; ++l) {
+    require(static_cast<int64_t>(head_lens[l].size()) == heads,
+            "Every layer must have the same number of KV heads");
+    const size_t t = packed ? 0 : l;
+    const int64_t first = packed ? packed_offsets[l] : 0;
+    const int64_t layer_rows = packed ? packed_offsets[l + 1] - first : keys[t].size(0);
+    require(first >= 0 && layer_rows >= 0 && first + layer_rows <= keys[t].size(0),
+            "Position lengths do not match metadata");
+    const int64_t kp = ptr(keys[t]), vp = ptr(values[t]), pp = ptr(positions[t]);
+    py::list lengths(heads);
+    int64_t base = first;
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t n = head_lens[l][h];
+      require(n >= 0, "Position lengths do not match metadata");
+      const int64_t slot = static_cast<int64_t>(l) * heads + h;
+      int64_t* row = table + slot * LR_REINSERT_WORDS;
+      row[0] = kp + base * row_bytes;
+      row[1] = vp + base * row_bytes;
+      row[2] = pp + base * 4;
+      row[3] = n;
+      row[4] = run;
+      row[5] = counts[slot];
+      row[6] = out_row;
+      row[7] = 0;
+      require(counts[slot] <= LR_REINSERT_MAX_PER_HEAD, "Too many recalled rows for one head");
+      run += counts[slot];
+      out_row += n + counts[slot];
+      lengths[h] = py::int_(n + counts[slot]);
+      base += n;
+      max_length = std::max(max_length, n);
+    }
+    require(base == first + layer_rows, "Position lengths do not match metadata");
+    new_lens[l] = lengths;
+    offsets[l + 1] = py::int_(out_row);
+  }
+  // group by slot: entry i goes to the next place of its slot's run
+  int64_t* grouped_position = table + slots * LR_REINSERT_WORDS;
+  int64_t* grouped_source = grouped_position + count;
+  std::vector<int64_t> cursor(static_cast<size_t>(slots));
+  for (int64_t slot = 0; slot < slots; ++slot) cursor[slot] = table[slot * LR_REINSERT_WORDS + 4];
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t at = cursor[meta[3 * i] * heads + meta[3 * i + 1]]++;
+    grouped_position[at] = meta[3 * i + 2];
+    grouped_source[at] = i;
+  }
+  return py::make_tuple(block, new_lens, offsets, out_row, max_length);
+}
+
 // The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,
 // head): [keys ptr, values ptr, positions ptr, first source row, old length, destination row,
 // logical position]; same checks, order and messages as the reference's host loop. Returns
@@ -779,6 +888,8 @@ PYBIND11_MODULE(_plan, module) {
   module.def("audit_launch", &audit_launch, "Enqueue one whole audit step");
   module.def("queue_evict_launch", &queue_evict_launch,
              "Enqueue one evict_prefix batch of an audit's lazy queue");
+  module.def("reinsert_prepare", &reinsert_prepare,
+             "Check a reinsertion and build its pinned table + metadata block");
   module.def("plan_batch_append", &plan_batch_append,
              "Validate a batch and upload its batch_append descriptors");
   module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;

@@ -454,6 +454,175 @@ __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
                    d0, n, out_start, layout, out_keys, out_values, out_positions);
 }
 
+// ---------------------------------------------------------------------------------------
+// Reinsertion of recalled rows into every layer at once (insert_payload, src/lazy_recall/
+// cache.py:201-253, with merge_plan, recall/planning.py:34-52, and _C.merge, csrc/recall.cu:
+// 7-28). A head's resident positions ascend (the cache keeps them so), its recalled positions
+// come in any order; the merged head holds both, ascending. Instead of a per-row source mapping
+// the rows are scattered: resident row j of a head goes to j + (recalled positions below it),
+// recalled row k (k-th smallest) to k + (resident positions below it). So the resident rows,
+// almost every byte, need only the recalled positions, not the recalled payload, and can move
+// while the payload is still being copied in.
+//
+// Reinsert table, LR_REINSERT_WORDS i64 per (layer, KV head) slot:
+//   [0] keys ptr, [1] values ptr, [2] positions ptr (f32) of the head's first resident row,
+//   [3] resident rows, [4] first entry of the head's recalled run, [5] recalled rows of the
+//   head, [6] first output row of the merged head, [7] unused (0).
+constexpr int kReinsertMax = LR_REINSERT_MAX_PER_HEAD;  // recalled rows of one head (sorted in LDS)
+
+// One workgroup per slot: its recalled entries sorted by position in LDS (bitonic), each one's
+// insertion point among the resident positions (binary search), duplicates flagged (bit 1);
+// writes the sorted run back with each entry's absolute output row, and each input entry's row
+// within its merged head.
+__global__ __launch_bounds__(kThreads) void reinsert_plan_kernel(
+    const int64_t* __restrict__ table, const int64_t* __restrict__ grouped,
+    int64_t* __restrict__ sorted_position, int64_t* __restrict__ sorted_source,
+    int64_t* __restrict__ sorted_destination, int64_t* __restrict__ recalled_rows, int64_t count,
+    int32_t* __restrict__ flag) {
+  __shared__ int64_t key[kReinsertMax];
+  __shared__ int64_t value[kReinsertMax];
+  const int64_t* entry = table + static_cast<int64_t>(blockIdx.x) * LR_REINSERT_WORDS;
+  const int64_t first = entry[4], r = entry[5];
+  if (r == 0) return;
+  if (r > kReinsertMax) {
+    if (threadIdx.x == 0) atomicOr(flag, 8);
+    return;
+  }
+  int n2 = 1;
+  while (n2 < r) n2 <<= 1;
+  for (int k = threadIdx.x; k < n2; k += kThreads) {
+    key[k] = k < r ? grouped[first + k] : INT64_MAX;
+    value[k] = k < r ? grouped[count + first + k] : -1;
+  }
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int k = threadIdx.x; k < n2; k += kThreads) {
+        const int other = k ^ stride;
+        if (other > k) {
+          const bool ascending = (k & size) == 0;
+          // ties (only between duplicates, which are refused) by source index
+          const bool greater = key[k] > key[other] || (key[k] == key[other] && value[k] > value[other]);
+          if (greater == ascending) {
+            const int64_t tk = key[k], tv = value[k];
+            key[k] = key[other];
+            value[k] = value[other];
+            key[other] = tk;
+            value[other] = tv;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const float* resident = reinterpret_cast<const float*>(entry[2]);
+  const int64_t n = entry[3], out_first = entry[6];
+  for (int k = threadIdx.x; k < r; k += kThreads) {
+    const int64_t position = key[k];
+    int64_t lo = 0, hi = n;  // resident positions below `position`
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (static_cast<int64_t>(resident[mid]) < position) lo = mid + 1;
+      else hi = mid;
+    }
+    const bool duplicate = (lo < n && static_cast<int64_t>(resident[lo]) == position) ||
+                           (k > 0 && key[k - 1] == position);
+    if (duplicate) atomicOr(flag, 1);
+    const int64_t row = lo + k;
+    sorted_position[first + k] = position;
+    sorted_source[first + k] = value[k];
+    sorted_destination[first + k] = out_first + row;
+    if (value[k] >= 0 && value[k] < count) recalled_rows[value[k]] = row;
+  }
+}
+
+// Resident rows: block (x, slot) owns rows [x * kCompactRows, ...) of the slot's head; each
+// thread finds its row's destination by binary search over the head's sorted recalled
+// positions (staged in LDS), then lane groups copy the rows in batches.
+template <int G>
+__global__ __launch_bounds__(kThreads) void reinsert_resident_kernel(
+    const int64_t* __restrict__ table, const int64_t* __restrict__ sorted_position,
+    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions) {
+  __shared__ int32_t recalled[kReinsertMax];  // positions are below 2^31 (host-checked)
+  __shared__ int64_t destination[kCompactRows];
+  const int64_t* entry = table + static_cast<int64_t>(blockIdx.y) * LR_REINSERT_WORDS;
+  const int64_t n = entry[3];
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kCompactRows;
+  if (d0 >= n) return;  // uniform
+  const int64_t first = entry[4], r = entry[5] < kReinsertMax ? entry[5] : kReinsertMax;
+  for (int64_t k = threadIdx.x; k < r; k += kThreads)
+    recalled[k] = static_cast<int32_t>(sorted_position[first + k]);
+  __syncthreads();
+  const int rows = static_cast<int>(n - d0 < kCompactRows ? n - d0 : kCompactRows);
+  const float* positions = reinterpret_cast<const float*>(entry[2]);
+  if (static_cast<int>(threadIdx.x) < rows) {
+    const int64_t j = d0 + threadIdx.x;
+    const float p = positions[j];
+    const int64_t key = static_cast<int64_t>(p);
+    int64_t lo = 0, hi = r;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (recalled[mid] < key) lo = mid + 1;
+      else hi = mid;
+    }
+    const int64_t to = entry[6] + j + lo;
+    destination[threadIdx.x] = to;
+    out_positions[to] = p;
+  }
+  __syncthreads();
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t rb = layout.row_bytes;
+  const uint8_t* keys = reinterpret_cast<const uint8_t*>(entry[0]);
+  const uint8_t* values = reinterpret_cast<const uint8_t*>(entry[1]);
+  for (int r0 = gc.group; r0 < rows; r0 += gc.groups_per_block * kBatch) {
+    RowBatch<true> b;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int row = r0 + u * gc.groups_per_block;
+      const bool ok = row < rows;
+      const int64_t from = ok ? d0 + row : d0;
+      b.ok[u] = ok;
+      b.src[u] = keys + from * rb;
+      b.src2[u] = values + from * rb;
+      const int64_t to = ok ? destination[row] : 0;
+      b.dst[u] = out_keys + to * rb;
+      b.dst2[u] = out_values + to * rb;
+    }
+    copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+  }
+}
+
+// Recalled rows: sorted entry q copies payload row sorted_source[q] (key half, value half) to
+// output row sorted_destination[q], with its position.
+template <int G>
+__global__ __launch_bounds__(kThreads) void reinsert_recalled_kernel(
+    const int64_t* __restrict__ sorted_position, const int64_t* __restrict__ sorted_source,
+    const int64_t* __restrict__ sorted_destination, int64_t count, int64_t out_rows,
+    const uint8_t* __restrict__ payload, RowLayout layout, uint8_t* __restrict__ out_keys,
+    uint8_t* __restrict__ out_values, float* __restrict__ out_positions) {
+  const GroupCoord gc = group_coord(layout.lanes_log2);
+  const int64_t rb = layout.row_bytes;
+  for (int64_t q0 = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * kBatch;
+       q0 < count; q0 += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * kBatch) {
+    RowBatch<true> b;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t q = q0 + u;
+      const int64_t source = q < count ? sorted_source[q] : -1;
+      const int64_t to = q < count ? sorted_destination[q] : -1;
+      const bool ok = source >= 0 && source < count && to >= 0 && to < out_rows;
+      b.ok[u] = ok;
+      b.src[u] = payload + (ok ? 2 * source : 0) * rb;
+      b.src2[u] = payload + (ok ? 2 * source + 1 : 0) * rb;
+      b.dst[u] = out_keys + (ok ? to : 0) * rb;
+      b.dst2[u] = out_values + (ok ? to : 0) * rb;
+      if (ok && gc.lane == 0) out_positions[to] = static_cast<float>(sorted_position[q]);
+    }
+    copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+  }
+}
+
 inline const uint8_t* bytes(const void* p) { return static_cast<const uint8_t*>(p); }
 inline uint8_t* bytes(void* p) { return static_cast<uint8_t*>(p); }
 
@@ -672,5 +841,69 @@ extern "C" int lr_compact_heads(const int64_t* head_table, int64_t heads, const 
         head_table, quotas, offsets, removed_positions, layout, bytes(out_keys),
         bytes(out_values), out_positions);
     return check_launch("compact_heads");
+  });
+}
+
+extern "C" int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64_t* grouped,
+                                int64_t count, int64_t* workspace, int64_t* recalled_rows,
+                                int32_t* flag, void* stream) {
+  clear_error();
+  LR_REQUIRE(slots > 0 && slots <= (int64_t{1} << 31) - 1 && count >= 0 &&
+                 count < (int64_t{1} << 40),
+             "Invalid reinsert layout");
+  LR_REQUIRE(table && flag && (count == 0 || (grouped && workspace && recalled_rows)),
+             "Expected contiguous CUDA tensor");
+  if (count == 0) return LR_OK;
+  reinsert_plan_kernel<<<static_cast<unsigned>(slots), kThreads, 0, as_stream(stream)>>>(
+      table, grouped, workspace, workspace + count, workspace + 2 * count, recalled_rows, count,
+      flag);
+  return check_launch("reinsert_plan");
+}
+
+extern "C" int lr_reinsert_resident(const int64_t* table, int64_t slots, const int64_t* workspace,
+                                    int64_t count, int64_t max_length, int64_t dim,
+                                    int elem_bytes, int64_t out_rows, void* out_keys,
+                                    void* out_values, float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Invalid KV layout");
+  LR_REQUIRE(slots > 0 && slots <= 65535 && max_length >= 0 && count >= 0, "Invalid reinsert layout");
+  if (out_rows == 0 || max_length == 0) return LR_OK;
+  LR_REQUIRE(table && out_keys && out_values && out_positions && (count == 0 || workspace),
+             "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {out_keys, out_values});
+  LR_REQUIRE(max_length < (int64_t{1} << 31), "Invalid reinsert layout");
+  const RowLayout layout = make_layout(row_bytes, g, out_rows, 8);
+  const int64_t bx = ceil_div(max_length, kCompactRows);
+  LR_REQUIRE(bx <= 65535, "Invalid reinsert layout");
+  dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(slots));
+  return dispatch_granule(g, [&]<int G>() {
+    reinsert_resident_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+        table, workspace, layout, bytes(out_keys), bytes(out_values), out_positions);
+    return check_launch("reinsert_resident");
+  });
+}
+
+extern "C" int lr_reinsert_recalled(const int64_t* workspace, int64_t count, const void* payload,
+                                    int64_t dim, int elem_bytes, int64_t out_rows,
+                                    void* out_keys, void* out_values, float* out_positions,
+                                    void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0 && count >= 0 && out_rows >= 0,
+             "Invalid KV layout");
+  if (count == 0 || out_rows == 0) return LR_OK;
+  LR_REQUIRE(workspace && payload && out_keys && out_values && out_positions,
+             "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  const int g = granule_for(row_bytes, {payload, out_keys, out_values});
+  const RowLayout layout = make_layout(row_bytes, g, count, kBatch);
+  const int64_t groups_per_block = kThreads >> layout.lanes_log2;
+  int64_t blocks = ceil_div(ceil_div(count, kBatch), groups_per_block);
+  if (blocks > kMaxGridX) blocks = kMaxGridX;
+  return dispatch_granule(g, [&]<int G>() {
+    reinsert_recalled_kernel<G><<<static_cast<unsigned>(blocks), kThreads, 0, as_stream(stream)>>>(
+        workspace, workspace + count, workspace + 2 * count, count, out_rows, bytes(payload),
+        layout, bytes(out_keys), bytes(out_values), out_positions);
+    return check_launch("reinsert_recalled");
   });
 }

@@ -283,6 +283,39 @@ int lr_queue_evict_plan(const int64_t* quotas, const int64_t* offsets,
                         int64_t begin, int64_t end, int64_t* batch_quotas,
                         int64_t* batch_positions, int64_t* host_quotas, void* stream);
 
+/* Reinsertion of recalled rows into every layer at once (insert_payload, src/lazy_recall/
+ * cache.py:201-253, with merge_plan, recall/planning.py:34-52, and merge, csrc/recall.cu:7-28;
+ * no single reference counterpart). Per (layer, KV head) slot, its resident rows (positions
+ * ascending, as the cache keeps them) and its recalled rows (any order) merge into one head
+ * ordered by position, all heads packed in slot order into one output. Device table of `slots`
+ * rows of LR_REINSERT_WORDS i64 (written by the caller):
+ *   [0] keys ptr, [1] values ptr, [2] positions ptr (f32) of the head's first resident row,
+ *   [3] resident rows, [4] first entry of the head's run (exclusive prefix of [5]), [5] recalled
+ *   rows of the head (at most LR_REINSERT_MAX_PER_HEAD), [6] first output row of the merged
+ *   head, [7] 0.
+ * lr_reinsert_plan: grouped = DEVICE i64 [2 * count]: the recalled positions grouped by slot
+ * (slot s's run at [4] of its row, any order within the run), then at [count + j] the index in
+ * the payload of grouped entry j. Sorts each run by position and finds each entry's output
+ * row. workspace: device i64 [3 * count]. recalled_rows [count] i64: the row of each payload
+ * entry within its merged head. flag (device i32, zeroed by the caller): bit 0 = a recalled
+ * position equals a resident or another recalled one of its head (merge_plan's "duplicate
+ * physical KV identities"), bit 3 = a slot with more than LR_REINSERT_MAX_PER_HEAD rows.
+ * lr_reinsert_resident: the resident rows of every slot (needs only the plan: may run while
+ * the payload is still being copied in). max_length = longest resident run.
+ * lr_reinsert_recalled: the recalled rows, from payload [count, 2, dim] (K at [i, 0], V at
+ * [i, 1]). */
+#define LR_REINSERT_WORDS 8
+#define LR_REINSERT_MAX_PER_HEAD 4096
+int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64_t* grouped, int64_t count,
+                     int64_t* workspace, int64_t* recalled_rows, int32_t* flag, void* stream);
+int lr_reinsert_resident(const int64_t* table, int64_t slots, const int64_t* workspace,
+                         int64_t count, int64_t max_length, int64_t dim, int elem_bytes,
+                         int64_t out_rows, void* out_keys, void* out_values, float* out_positions,
+                         void* stream);
+int lr_reinsert_recalled(const int64_t* workspace, int64_t count, const void* payload,
+                         int64_t dim, int elem_bytes, int64_t out_rows, void* out_keys,
+                         void* out_values, float* out_positions, void* stream);
+
 /* Staging of the fused step's metadata block (no reference counterpart: the reference copies
  * each per-layer index list to the device with its own blocking copy). lr_staging_alloc gives
  * `bytes` of pinned, host-coherent memory that kernels may read directly; lr_staging_free
