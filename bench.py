@@ -353,24 +353,35 @@ def ops_bench(torch, seed, reps=5):
         return device, float(np.median(walls))
 
     out = {}
-    keys = [randn(rows, d) for _ in range(2)]
-    values = [randn(rows, d) for _ in range(2)]
+    # every layer has its own K/V (32 x 18.4 MB, beyond the 256 MB Infinity Cache), as in a
+    # decode step, so no call reads rows another call left in the cache
+    keys = [randn(rows, d) for _ in range(L)]
+    values = [randn(rows, d) for _ in range(L)]
     positions = torch.arange(T, dtype=torch.float32, device=dev).repeat(H)[:, None].contiguous()
     cumulative = torch.arange(0, rows + 1, T, dtype=torch.int32, device=dev)
     new_k, new_v = randn(1, H, 1, d), randn(1, H, 1, d)
 
     # a10 append: one token per head into every layer (cache.py:33-52)
     device, wall = measure(lambda: [
-        (lambda l=l: _C.append(keys[l % 2], values[l % 2], positions, new_k, new_v, cumulative,
+        (lambda l=l: _C.append(keys[l], values[l], positions, new_k, new_v, cumulative,
                                T, T)) for l in range(L)], L)
     nbytes = 2 * rows * d * 2 + 2 * (rows + H) * d * 2 + rows * 4 + (rows + H) * 4 + 2 * H * d * 2
     out["append"] = _op_line("cfg1 layer: 8 heads x 2250 rows + 1 token per head, bf16 d128", L,
                              device, nbytes, wall)
 
+    # the same decode step's appends of all 32 layers in one launch (packed outputs)
+    device, wall = measure(lambda: [
+        (lambda: _C.append_layers(keys, values, [positions] * L, [new_k] * L,
+                                  [new_v] * L, [cumulative] * L, [T] * L, T))
+        for _ in range(4)], 1)
+    out["append_layers"] = _op_line("cfg1 decode step: all 32 layers' appends in one launch", 1,
+                                    device, L * nbytes, wall)
+
     # a11 append_flattened_cache: K and V of every layer (cache_legacy.cu:145-197)
     head_lens = torch.full((H,), T, dtype=torch.int32, device=dev)
     device, wall = measure(lambda: [
-        (lambda l=l: _legacy_C.append_flattened_cache(keys[l % 2], new_k, head_lens, cumulative))
+        (lambda l=l: _legacy_C.append_flattened_cache((keys if l < L else values)[l % L], new_k,
+                                                       head_lens, cumulative))
         for l in range(2 * L)], 2 * L)
     nbytes = rows * d * 2 + (rows + H) * d * 2 + H * d * 2
     out["append_flattened_cache"] = _op_line("cfg1 layer K (or V): 8 heads x 2250 rows + 1 token",
@@ -386,7 +397,7 @@ def ops_bench(torch, seed, reps=5):
 
     # a9 compact, per layer (scoring.cu:294-314)
     device, wall = measure(lambda: [
-        (lambda l=l: _C.compact(keys[l % 2], values[l % 2], positions, removed_d))
+        (lambda l=l: _C.compact(keys[l], values[l], positions, removed_d))
         for l in range(L)], L)
     nbytes = 2 * kept * d * 2 * 2 + kept * 4 * 2 + removed.size * 8
     out["compact"] = _op_line("cfg1 layer: remove 250 of 2250 rows per head", L, device, nbytes,
@@ -394,7 +405,7 @@ def ops_bench(torch, seed, reps=5):
 
     # a12 compact_flattened_kv (cache_legacy.cu:199-242)
     device, wall = measure(lambda: [
-        (lambda l=l: _legacy_C.compact_flattened_kv(keys[l % 2], values[l % 2], keep_d))
+        (lambda l=l: _legacy_C.compact_flattened_kv(keys[l], values[l], keep_d))
         for l in range(L)], L)
     nbytes = 2 * kept * d * 2 * 2 + kept * 8
     out["compact_flattened_kv"] = _op_line("cfg1 layer: keep 2000 of 2250 rows per head", L,
@@ -405,7 +416,7 @@ def ops_bench(torch, seed, reps=5):
     payload = torch.empty((removed.size, 2, d), dtype=bf16, device=dev)
     meta = torch.empty((removed.size, 3), dtype=torch.int64, device=dev)
     device, wall = measure(lambda: [
-        (lambda l=l: _C.pack(keys[l % 2], values[l % 2], positions, removed_d, heads_d, l,
+        (lambda l=l: _C.pack(keys[l], values[l], positions, removed_d, heads_d, l,
                              payload, meta)) for l in range(L)], L)
     nbytes = removed.size * (2 * d * 2 * 2 + 4 + 8 + 8 + 3 * 8)
     out["pack"] = _op_line("cfg1 layer: 2000 evicted rows -> [2000, 2, 128] payload", L, device,
@@ -416,14 +427,14 @@ def ops_bench(torch, seed, reps=5):
     R = 8
     lengths = [[int(x) for x in rng.integers(1500, 2251, H)] for _ in range(R)]
     totals = [sum(l) for l in lengths]
-    req_k = [[randn(n, d) for n in totals] for _ in range(2)]
-    req_v = [[randn(n, d) for n in totals] for _ in range(2)]
+    req_k = [[randn(n, d) for n in totals] for _ in range(L)]  # every layer its own caches
+    req_v = [[randn(n, d) for n in totals] for _ in range(L)]
     req_p = [torch.cat([torch.arange(n, dtype=torch.float32, device=dev) for n in l])[:, None]
              for l in lengths]
     nk, nv = randn(R, H, 1, d), randn(R, H, 1, d)
     logical = [max(l) for l in lengths]
     device, wall = measure(lambda: [
-        (lambda l=l: _C.batch_append(req_k[l % 2], req_v[l % 2], req_p, nk, nv, lengths, logical))
+        (lambda l=l: _C.batch_append(req_k[l], req_v[l], req_p, nk, nv, lengths, logical))
         for l in range(L)], L)
     n = sum(totals)
     nbytes = 2 * n * d * 2 + 2 * (n + R * H) * d * 2 + n * 4 + (n + R * H) * 4 + 2 * R * H * d * 2

@@ -82,64 +82,51 @@ def temporal_risk(probabilities, output_projection, projected_values, margin, fi
     return result
 
 
-def _check_cache(keys, values, positions):
-    # csrc/scoring.cu:257-262
-    for tensor in (keys, values, positions):
-        _check_cuda(tensor, keys)
-    _check(keys.dim() == 2 and keys.size(1) > 0 and keys.shape == values.shape
-           and keys.dtype == values.dtype, "Invalid KV layout")
-    _check(positions.dtype == torch.float32 and positions.numel() == keys.size(0),
-           "Invalid positions")
+_bound_native = False
+
+
+def _native():
+    """The C++ host module with lr_append / lr_compact bound (once): the per-layer decode-time
+    ops run their checks, allocate their outputs and launch from C++ on torch's current stream."""
+    global _bound_native
+    from .scoring import _planner
+    planner = _planner()
+    if not _bound_native:
+        import ctypes
+        library = _lib.load()
+        address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
+        planner.bind_data_movement(address("lr_append"), address("lr_compact"),
+                                   address("lr_append_layers"))
+        _bound_native = True
+    return planner
 
 
 def append(keys, values, positions, new_keys, new_values, cumulative, logical_start,
            maximum_length):
-    """csrc/scoring.cu:264-292 -> [keys, values, positions [N,1], cumulative i32, lengths i32]."""
-    _check_cache(keys, values, positions)
-    for tensor in (new_keys, new_values, cumulative):
-        _check_cuda(tensor, keys)
-    _check(new_keys.dim() == 4 and new_keys.size(0) == 1 and new_keys.shape == new_values.shape
-           and new_keys.dtype == keys.dtype and new_values.dtype == keys.dtype,
-           "Invalid appended KV")
-    heads, added, dimension = new_keys.size(1), new_keys.size(2), keys.size(1)
-    _check(heads > 0 and added > 0 and new_keys.size(3) == dimension and maximum_length >= 0,
-           "Invalid appended shape")
-    _check(cumulative.dtype == torch.int32 and cumulative.numel() == heads + 1,
-           "Invalid cumulative lengths")
-    elem = _elem_bytes(keys, "lazy_recall_append")
-    rows = keys.size(0) + heads * added
-    with torch.cuda.device(keys.device):
-        output_keys = torch.empty((rows, dimension), dtype=keys.dtype, device=keys.device)
-        output_values = torch.empty_like(output_keys)
-        output_positions = torch.empty((rows, 1), dtype=positions.dtype, device=keys.device)
-        output_cumulative = torch.empty_like(cumulative)
-        output_lengths = torch.empty((heads,), dtype=cumulative.dtype, device=keys.device)
-        _lib.call("lr_append", _lib.ptr(keys), _lib.ptr(values), _lib.ptr(positions), keys.size(0),
-                  new_keys.data_ptr(), new_values.data_ptr(), cumulative.data_ptr(), heads, added,
-                  dimension, elem, int(logical_start), int(maximum_length),
-                  output_keys.data_ptr(), output_values.data_ptr(), output_positions.data_ptr(),
-                  output_cumulative.data_ptr(), output_lengths.data_ptr(), _lib.stream_of(keys))
-    return [output_keys, output_values, output_positions, output_cumulative, output_lengths]
+    """csrc/scoring.cu:264-292 -> [keys, values, positions [N,1], cumulative i32, lengths i32].
+    Checks (csrc/scoring.cu:257-283, same order and messages), allocation and launch are made by
+    the C++ host module (csrc/host_plan.cpp append_launch)."""
+    return _native().append(keys, values, positions, new_keys, new_values, cumulative,
+                            int(logical_start), int(maximum_length))
+
+
+def append_layers(keys, values, positions, new_keys, new_values, cumulative, logical_starts,
+                  maximum_length):
+    """One decode step's ``append`` into every layer in one launch (an extra export: the
+    reference makes one append call per layer, cache.py:33-52). Each argument except
+    ``maximum_length`` is a per-layer list, with ``append``'s meaning. Returns [keys, values,
+    positions [rows, 1], cumulative i32 [L, H + 1], lengths i32 [L, H], first row of each layer
+    [L + 1]]: every layer's rows packed into one buffer, layer l at rows
+    [first[l], first[l + 1])."""
+    return list(_native().append_layers(list(keys), list(values), list(positions),
+                                        list(new_keys), list(new_values), list(cumulative),
+                                        [int(v) for v in logical_starts], int(maximum_length)))
 
 
 def compact(keys, values, positions, removed):
-    """csrc/scoring.cu:294-314 -> [keys, values, positions [N-E,1]]; removed sorted, unique."""
-    _check_cache(keys, values, positions)
-    _check_cuda(removed, keys)
-    _check(removed.dtype == torch.int64 and removed.dim() == 1
-           and removed.numel() <= keys.size(0), "Invalid removals")
-    elem = _elem_bytes(keys, "lazy_recall_compact")
-    rows, dimension = keys.size(0) - removed.numel(), keys.size(1)
-    with torch.cuda.device(keys.device):
-        output_keys = torch.empty((rows, dimension), dtype=keys.dtype, device=keys.device)
-        output_values = torch.empty_like(output_keys)
-        output_positions = torch.empty((rows, 1), dtype=positions.dtype, device=keys.device)
-        if rows > 0:
-            _lib.call("lr_compact", keys.data_ptr(), values.data_ptr(), positions.data_ptr(),
-                      keys.size(0), dimension, elem, _lib.ptr(removed), removed.numel(),
-                      output_keys.data_ptr(), output_values.data_ptr(),
-                      output_positions.data_ptr(), _lib.stream_of(keys))
-    return [output_keys, output_values, output_positions]
+    """csrc/scoring.cu:294-314 -> [keys, values, positions [N-E,1]]; removed sorted, unique.
+    Checks, allocation and launch in the C++ host module (csrc/host_plan.cpp compact_launch)."""
+    return _native().compact(keys, values, positions, removed)
 
 
 def pool(scores, bounds, maximum_count, width):

@@ -20,6 +20,7 @@ LR_DTYPE_F32, LR_DTYPE_F64, LR_DTYPE_F16, LR_DTYPE_BF16 = 0, 1, 2, 3
 LR_SEG_WORDS = 12
 LR_HEAD_WORDS = 6
 LR_REINSERT_WORDS = 8
+LR_APPEND_WORDS = 12
 LR_REINSERT_MAX_PER_HEAD = 4096
 LR_HISTORY_MAX_LAYERS = 128
 
@@ -39,6 +40,7 @@ SIGNATURES = {
     "lr_temporal_risk": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D, _P, _P],
     "lr_append": [_P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I, _I64, _I64, _P, _P, _P, _P,
                   _P, _P],
+    "lr_append_layers": [_P, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P, _P, _P],
     "lr_compact": [_P, _P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P, _P],
     "lr_pool": [_P, _I64, _P, _I64, _I64, _I64, _P, _P],
     "lr_merge": [_P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I, _P, _P, _P, _P],

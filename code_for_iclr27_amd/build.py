@@ -60,7 +60,8 @@ def _run(command: list[str]) -> None:
 
 
 def build_host_plan(verbose: bool = False) -> Path:
-    """The CPU-side planner (a CPython extension; no GPU code)."""
+    """The host-side planner and launcher (a CPython extension; no GPU code: it calls the
+    library's entry points on torch's current HIP stream)."""
     import sysconfig
 
     import torch
@@ -68,17 +69,20 @@ def build_host_plan(verbose: bool = False) -> Path:
 
     target = PACKAGE_DIR / ("_plan" + sysconfig.get_config_var("EXT_SUFFIX"))
     temporary = target.with_name(target.name + ".tmp")
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
     includes = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"],
-                str(PACKAGE_DIR.parent / "include")]
+                str(PACKAGE_DIR.parent / "include"), str(rocm / "include")]
     library_dirs = cpp_extension.library_paths()
     command = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function",
                f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+               "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
                "-DTORCH_EXTENSION_NAME=_plan", str(SOURCE_DIR / "host_plan.cpp"),
                "-o", str(temporary)]
     command += [f"-I{path}" for path in includes]
     command += [f"-L{path}" for path in library_dirs]
     command += [f"-Wl,-rpath,{path}" for path in library_dirs]
-    command += ["-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+    command += ["-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+                f"-L{rocm / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{rocm / 'lib'}"]
     if verbose:
         print(" ".join(command), flush=True)
     _run(command)

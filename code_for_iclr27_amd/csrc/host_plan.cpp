@@ -8,6 +8,7 @@
 // offsets and the mapped query heads) and of remove_positions (src/lazy_recall/cache.py:
 // 113-147: absolute rows of every head). Done from Python it costs ~27 tensor attribute
 // reads per layer at ~0.2 us each; here the whole 32-layer plan takes a few microseconds.
+#include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
 #include <algorithm>
@@ -229,6 +230,9 @@ struct Library {
   decltype(&lr_queue_index) queue_index = nullptr;
   decltype(&lr_queue_evict_plan) queue_evict_plan = nullptr;
   decltype(&lr_compact_heads) compact_heads = nullptr;
+  decltype(&lr_append) append = nullptr;
+  decltype(&lr_compact) compact = nullptr;
+  decltype(&lr_append_layers) append_layers = nullptr;
   decltype(&lr_last_error) last_error = nullptr;
   decltype(&lr_staging_alloc) staging_alloc = nullptr;
   decltype(&lr_staging_free) staging_free = nullptr;
@@ -260,6 +264,12 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
   bind_one(library.staging_alloc, staging_alloc);
   bind_one(library.staging_free, staging_free);
   bind_one(library.copy_words, copy_words);
+}
+
+void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers) {
+  bind_one(library.append, append);
+  bind_one(library.compact, compact);
+  bind_one(library.append_layers, append_layers);
 }
 
 void check_call(int status) {
@@ -818,6 +828,179 @@ py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
   return py::make_tuple(block, new_lens, offsets, out_row, max_length);
 }
 
+// ---------------------------------------------------------------------------------------
+// The per-layer drop-ins _C.append and _C.compact with their checks, output allocation and
+// launch in C++ (a decode step makes one append per layer; from Python each call cost ~20 us of
+// host time in tensor checks, five allocations and the ctypes call). Same checks, order and
+// messages as the Python mirror of csrc/scoring.cu:257-314.
+
+void check_cuda(const torch::Tensor& t, const torch::Tensor& reference) {
+  require(t.is_cuda() && t.is_contiguous(), "Expected contiguous CUDA tensor");
+  require(t.device() == reference.device(), "CUDA devices differ");
+}
+
+void check_cache(const torch::Tensor& keys, const torch::Tensor& values,
+                 const torch::Tensor& positions) {
+  for (const torch::Tensor* t : {&keys, &values, &positions}) check_cuda(*t, keys);
+  require(keys.dim() == 2 && keys.size(1) > 0 && keys.sizes() == values.sizes() &&
+              keys.scalar_type() == values.scalar_type(),
+          "Invalid KV layout");
+  require(positions.scalar_type() == torch::kFloat32 && positions.numel() == keys.size(0),
+          "Invalid positions");
+}
+
+int elem_bytes(const torch::Tensor& t, const char* op) {
+  const auto type = t.scalar_type();
+  if (type != torch::kFloat32 && type != torch::kFloat64 && type != torch::kFloat16 &&
+      type != torch::kBFloat16)
+    throw std::runtime_error(std::string("\"") + op + "\" not implemented for '" +
+                             std::string(c10::toString(type)) + "'");
+  return static_cast<int>(t.element_size());
+}
+
+void* current_stream(const torch::Device& device) {
+  return c10::hip::getCurrentHIPStream(device.index()).stream();
+}
+
+std::vector<torch::Tensor> append_launch(const torch::Tensor& keys, const torch::Tensor& values,
+                                         const torch::Tensor& positions,
+                                         const torch::Tensor& new_keys,
+                                         const torch::Tensor& new_values,
+                                         const torch::Tensor& cumulative, int64_t logical_start,
+                                         int64_t maximum_length) {
+  require(library.append != nullptr, "library entry points are not bound");
+  check_cache(keys, values, positions);
+  for (const torch::Tensor* t : {&new_keys, &new_values, &cumulative}) check_cuda(*t, keys);
+  require(new_keys.dim() == 4 && new_keys.size(0) == 1 && new_keys.sizes() == new_values.sizes() &&
+              new_keys.scalar_type() == keys.scalar_type() &&
+              new_values.scalar_type() == keys.scalar_type(),
+          "Invalid appended KV");
+  const int64_t heads = new_keys.size(1), added = new_keys.size(2), dim = keys.size(1);
+  require(heads > 0 && added > 0 && new_keys.size(3) == dim && maximum_length >= 0,
+          "Invalid appended shape");
+  require(cumulative.scalar_type() == torch::kInt32 && cumulative.numel() == heads + 1,
+          "Invalid cumulative lengths");
+  const int elem = elem_bytes(keys, "lazy_recall_append");
+  const c10::DeviceGuard guard(keys.device());
+  const int64_t rows = keys.size(0) + heads * added;
+  const auto options = keys.options();
+  torch::Tensor out_keys = torch::empty({rows, dim}, options);
+  torch::Tensor out_values = torch::empty({rows, dim}, options);
+  torch::Tensor out_positions = torch::empty({rows, 1}, positions.options());
+  torch::Tensor out_cumulative = torch::empty_like(cumulative);
+  torch::Tensor out_lengths = torch::empty({heads}, cumulative.options());
+  check_call(library.append(
+      keys.numel() ? keys.data_ptr() : nullptr, values.numel() ? values.data_ptr() : nullptr,
+      positions.numel() ? positions.data_ptr<float>() : nullptr, keys.size(0),
+      new_keys.data_ptr(), new_values.data_ptr(), cumulative.data_ptr<int32_t>(), heads, added,
+      dim, elem, logical_start, maximum_length, out_keys.data_ptr(), out_values.data_ptr(),
+      out_positions.data_ptr<float>(), out_cumulative.data_ptr<int32_t>(),
+      out_lengths.data_ptr<int32_t>(), current_stream(keys.device())));
+  return {out_keys, out_values, out_positions, out_cumulative, out_lengths};
+}
+
+std::vector<torch::Tensor> compact_launch(const torch::Tensor& keys, const torch::Tensor& values,
+                                          const torch::Tensor& positions,
+                                          const torch::Tensor& removed) {
+  require(library.compact != nullptr, "library entry points are not bound");
+  check_cache(keys, values, positions);
+  check_cuda(removed, keys);
+  require(removed.scalar_type() == torch::kInt64 && removed.dim() == 1 &&
+              removed.numel() <= keys.size(0),
+          "Invalid removals");
+  const int elem = elem_bytes(keys, "lazy_recall_compact");
+  const c10::DeviceGuard guard(keys.device());
+  const int64_t rows = keys.size(0) - removed.numel(), dim = keys.size(1);
+  torch::Tensor out_keys = torch::empty({rows, dim}, keys.options());
+  torch::Tensor out_values = torch::empty({rows, dim}, keys.options());
+  torch::Tensor out_positions = torch::empty({rows, 1}, positions.options());
+  if (rows > 0)
+    check_call(library.compact(keys.data_ptr(), values.data_ptr(), positions.data_ptr<float>(),
+                               keys.size(0), dim, elem,
+                               removed.numel() ? removed.data_ptr<int64_t>() : nullptr,
+                               removed.numel(), out_keys.data_ptr(), out_values.data_ptr(),
+                               out_positions.data_ptr<float>(), current_stream(keys.device())));
+  return {out_keys, out_values, out_positions};
+}
+
+// One decode step's append into every layer (lr_append_layers): the per-layer checks of
+// append_launch for each layer, one pinned table uploaded without blocking, packed outputs and
+// one launch. Returns (keys, values, positions [rows, 1], cumulative [L, H + 1] i32, lengths
+// [L, H] i32, first output row of each layer [L + 1]).
+py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
+                               const std::vector<torch::Tensor>& values,
+                               const std::vector<torch::Tensor>& positions,
+                               const std::vector<torch::Tensor>& new_keys,
+                               const std::vector<torch::Tensor>& new_values,
+                               const std::vector<torch::Tensor>& cumulative,
+                               const std::vector<int64_t>& logical_starts,
+                               int64_t maximum_length) {
+  require(library.append_layers != nullptr, "library entry points are not bound");
+  const size_t layers = keys.size();
+  require(layers > 0 && values.size() == layers && positions.size() == layers &&
+              new_keys.size() == layers && new_values.size() == layers &&
+              cumulative.size() == layers && logical_starts.size() == layers,
+          "Layer lists differ in length");
+  const torch::Tensor& k0 = keys[0];
+  int64_t heads = 0, added = 0, dim = 0;
+  torch::Tensor table = torch::empty({static_cast<int64_t>(layers) * LR_APPEND_WORDS},
+                                     torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
+  int64_t* rows = table.data_ptr<int64_t>();
+  py::list firsts(layers + 1);
+  int64_t total = 0;
+  int elem = 0;
+  for (size_t l = 0; l < layers; ++l) {
+    const torch::Tensor &k = keys[l], &v = values[l], &p = positions[l];
+    check_cache(k, v, p);
+    check_cuda(k, k0);
+    for (const torch::Tensor* t : {&new_keys[l], &new_values[l], &cumulative[l]}) check_cuda(*t, k0);
+    const torch::Tensor &nk = new_keys[l], &nv = new_values[l];
+    require(nk.dim() == 4 && nk.size(0) == 1 && nk.sizes() == nv.sizes() &&
+                nk.scalar_type() == k0.scalar_type() && nv.scalar_type() == k0.scalar_type() &&
+                k.scalar_type() == k0.scalar_type(),
+            "Invalid appended KV");
+    if (l == 0) {
+      heads = nk.size(1);
+      added = nk.size(2);
+      dim = k0.size(1);
+      elem = elem_bytes(k0, "lazy_recall_append");
+    }
+    require(heads > 0 && added > 0 && nk.size(1) == heads && nk.size(2) == added &&
+                nk.size(3) == dim && k.size(1) == dim && maximum_length >= 0,
+            "Invalid appended shape");
+    require(cumulative[l].scalar_type() == torch::kInt32 && cumulative[l].numel() == heads + 1,
+            "Invalid cumulative lengths");
+    int64_t* row = rows + l * LR_APPEND_WORDS;
+    row[0] = k.numel() ? ptr(k) : 0;
+    row[1] = v.numel() ? ptr(v) : 0;
+    row[2] = p.numel() ? ptr(p) : 0;
+    row[3] = k.size(0);
+    row[4] = ptr(cumulative[l]);
+    row[5] = ptr(nk);
+    row[6] = ptr(nv);
+    row[7] = logical_starts[l];
+    row[8] = total;
+    row[9] = row[10] = row[11] = 0;
+    firsts[l] = py::int_(total);
+    total += k.size(0) + heads * added;
+  }
+  firsts[layers] = py::int_(total);
+  const c10::DeviceGuard guard(k0.device());
+  torch::Tensor device_table = table.to(k0.device(), /*non_blocking=*/true);
+  torch::Tensor out_keys = torch::empty({total, dim}, k0.options());
+  torch::Tensor out_values = torch::empty({total, dim}, k0.options());
+  torch::Tensor out_positions = torch::empty({total, 1}, positions[0].options());
+  const auto i32 = cumulative[0].options();
+  torch::Tensor out_cumulative = torch::empty({static_cast<int64_t>(layers), heads + 1}, i32);
+  torch::Tensor out_lengths = torch::empty({static_cast<int64_t>(layers), heads}, i32);
+  check_call(library.append_layers(device_table.data_ptr<int64_t>(), static_cast<int64_t>(layers),
+                                   heads, added, dim, elem, maximum_length, out_keys.data_ptr(),
+                                   out_values.data_ptr(), out_positions.data_ptr<float>(),
+                                   out_cumulative.data_ptr<int32_t>(),
+                                   out_lengths.data_ptr<int32_t>(), current_stream(k0.device())));
+  return py::make_tuple(out_keys, out_values, out_positions, out_cumulative, out_lengths, firsts);
+}
+
 // The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,
 // head): [keys ptr, values ptr, positions ptr, first source row, old length, destination row,
 // logical position]; same checks, order and messages as the reference's host loop. Returns
@@ -881,6 +1064,11 @@ py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
 PYBIND11_MODULE(_plan, module) {
   module.def("plan_audit", &plan_audit, "Validate layers and build the audit metadata block");
   module.def("bind_library", &bind_library, "Bind the entry points of liblazyrecall_hip.so");
+  module.def("bind_data_movement", &bind_data_movement,
+             "Bind lr_append and lr_compact of liblazyrecall_hip.so");
+  module.def("append", &append_launch, "_C.append (csrc/scoring.cu:264-292)");
+  module.def("compact", &compact_launch, "_C.compact (csrc/scoring.cu:294-314)");
+  module.def("append_layers", &append_layers_launch, "One decode step's append into every layer");
   py::class_<StepSync>(module, "StepSync")
       .def(py::init<>())
       .def("wait", &StepSync::wait, py::arg("check_finite"),

@@ -200,12 +200,12 @@ __global__ __launch_bounds__(kThreads) void compact_kernel(
 // old rows move from src_start(h) to dst_start(h) = src_start(h) + h * added, followed by
 // `added` new rows. blockIdx.y = head; rows of a head are covered up to `covered_rows`.
 template <int G, bool kWithPositions>
-__global__ __launch_bounds__(kThreads) void head_append_kernel(
+__device__ __forceinline__ void head_append(
     const uint8_t* __restrict__ cache_keys, const uint8_t* __restrict__ cache_values,
     const float* __restrict__ positions, int64_t rows_in, const uint8_t* __restrict__ new_keys,
     const uint8_t* __restrict__ new_values, const int32_t* __restrict__ starts,
     const int32_t* __restrict__ lengths_or_next, int lengths_are_cumulative, int64_t heads,
-    int64_t added, int64_t covered_rows, int64_t logical_start, RowLayout layout,
+    int64_t added, int64_t covered_rows, int64_t logical_start, const RowLayout& layout,
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
     int32_t* __restrict__ out_lengths) {
@@ -270,6 +270,46 @@ __global__ __launch_bounds__(kThreads) void head_append_kernel(
       }
     }
   }
+}
+
+template <int G, bool kWithPositions>
+__global__ __launch_bounds__(kThreads) void head_append_kernel(
+    const uint8_t* __restrict__ cache_keys, const uint8_t* __restrict__ cache_values,
+    const float* __restrict__ positions, int64_t rows_in, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, const int32_t* __restrict__ starts,
+    const int32_t* __restrict__ lengths_or_next, int lengths_are_cumulative, int64_t heads,
+    int64_t added, int64_t covered_rows, int64_t logical_start, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
+    int32_t* __restrict__ out_lengths) {
+  head_append<G, kWithPositions>(cache_keys, cache_values, positions, rows_in, new_keys,
+                                 new_values, starts, lengths_or_next, lengths_are_cumulative,
+                                 heads, added, covered_rows, logical_start, layout, out_keys,
+                                 out_values, out_positions, out_cumulative, out_lengths);
+}
+
+// One decode step's append into every layer (blockIdx.z = layer): the per-layer append above
+// with its arguments from a table of LR_APPEND_WORDS i64 per layer, all layers' outputs packed
+// into one K, V and positions buffer (layer l from its output row [8]) and one [L, heads + 1]
+// cumulative / [L, heads] lengths pair.
+template <int G>
+__global__ __launch_bounds__(kThreads) void append_layers_kernel(
+    const int64_t* __restrict__ table, int64_t heads, int64_t added, int64_t covered_rows,
+    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
+    int32_t* __restrict__ out_lengths) {
+  const int64_t layer = blockIdx.z;
+  const int64_t* row = table + layer * LR_APPEND_WORDS;
+  const int64_t first = row[8];
+  const int32_t* cumulative = reinterpret_cast<const int32_t*>(row[4]);
+  head_append<G, true>(reinterpret_cast<const uint8_t*>(row[0]),
+                       reinterpret_cast<const uint8_t*>(row[1]),
+                       reinterpret_cast<const float*>(row[2]), row[3],
+                       reinterpret_cast<const uint8_t*>(row[5]),
+                       reinterpret_cast<const uint8_t*>(row[6]), cumulative, cumulative, 1, heads,
+                       added, covered_rows, row[7], layout, out_keys + first * layout.row_bytes,
+                       out_values + first * layout.row_bytes, out_positions + first,
+                       out_cumulative + layer * (heads + 1), out_lengths + layer * heads);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -905,5 +945,34 @@ extern "C" int lr_reinsert_recalled(const int64_t* workspace, int64_t count, con
         workspace, workspace + count, workspace + 2 * count, count, out_rows, bytes(payload),
         layout, bytes(out_keys), bytes(out_values), out_positions);
     return check_launch("reinsert_recalled");
+  });
+}
+
+extern "C" int lr_append_layers(const int64_t* table, int64_t layers, int64_t heads,
+                                int64_t added, int64_t dim, int elem_bytes, int64_t max_length,
+                                void* out_keys, void* out_values, float* out_positions,
+                                int32_t* out_cumulative, int32_t* out_lengths, void* stream) {
+  clear_error();
+  LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Invalid KV layout");
+  LR_REQUIRE(layers > 0 && layers <= 65535 && heads > 0 && heads <= 65535 && added > 0 &&
+                 max_length >= 0,
+             "Invalid appended shape");
+  LR_REQUIRE(table && out_keys && out_values && out_positions && out_cumulative && out_lengths,
+             "Expected contiguous CUDA tensor");
+  const int64_t row_bytes = dim * elem_bytes;
+  // every layer's rows are whole rows of its (16-byte aligned) allocation; the outputs bound
+  // the granule
+  const int g = granule_for(row_bytes, {out_keys, out_values});
+  const int64_t covered = max_length + added;
+  const RowLayout layout = make_layout(row_bytes, g, covered * heads * layers, 8);
+  int64_t bx = ceil_div(ceil_div(covered, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  if (bx < 1) bx = 1;
+  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads),
+            static_cast<unsigned>(layers));
+  return dispatch_granule(g, [&]<int G>() {
+    append_layers_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+        table, heads, added, covered, layout, bytes(out_keys), bytes(out_values), out_positions,
+        out_cumulative, out_lengths);
+    return check_launch("append_layers");
   });
 }

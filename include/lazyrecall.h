@@ -72,6 +72,23 @@ int lr_append(const void* keys, const void* values, const float* positions, int6
               int64_t max_length, void* out_keys, void* out_values, float* out_positions,
               int32_t* out_cumulative, int32_t* out_lengths, void* stream);
 
+/* One decode step's append into every layer in one launch (the per-layer append calls of
+ * LazyRecallCache.update, src/lazy_recall/cache.py:33-52, for all layers; no single reference
+ * counterpart). Device table of `layers` rows of LR_APPEND_WORDS i64:
+ *   [0] keys ptr, [1] values ptr, [2] positions ptr (f32), [3] rows, [4] cumulative ptr (i32
+ *   [heads + 1]), [5] new keys ptr, [6] new values ptr ([1, heads, added, dim]), [7] logical
+ *   start, [8] first output row of the layer (exclusive prefix of rows + heads * added),
+ *   [9..11] 0.
+ * Each layer as lr_append; outputs packed: keys/values [sum of rows + layers*heads*added, dim],
+ * positions [same] f32, cumulative [layers, heads + 1] i32, lengths [layers, heads] i32.
+ * max_length = the longest head of any layer. Every key/value row must be 16-byte aligned when
+ * dim * elem_bytes is a multiple of 16 (the output alignment picks the copy granule). */
+#define LR_APPEND_WORDS 12
+int lr_append_layers(const int64_t* table, int64_t layers, int64_t heads, int64_t added,
+                     int64_t dim, int elem_bytes, int64_t max_length, void* out_keys,
+                     void* out_values, float* out_positions, int32_t* out_cumulative,
+                     int32_t* out_lengths, void* stream);
+
 /* compact (csrc/scoring.cu:164-188, 294-314). removed [removed_count] i64, sorted, unique.
  * Outputs [rows - removed_count, dim] and positions [rows - removed_count]. */
 int lr_compact(const void* keys, const void* values, const float* positions, int64_t rows,

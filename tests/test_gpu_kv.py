@@ -128,6 +128,46 @@ def test_append(device, dtype, added, dim):
     np.testing.assert_array_equal(got[4].cpu().numpy(), expect[4])
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("added,dim", [(1, 128), (3, 64), (2, 3)])
+def test_append_layers_matches_per_layer_append(device, dtype, added, dim):
+    """One launch for every layer (packed outputs) equals the oracle's per-layer append, with
+    per-layer lengths (an empty layer and empty heads included) and logical starts."""
+    heads = 8
+    layer_lengths = [[7, 0, 300, 1, 64, 2, 9, 33], [0] * heads, [250] * heads,
+                     [1, 2, 3, 4, 5, 6, 7, 8]]
+    args = {name: [] for name in ("keys", "values", "positions", "new_k", "new_v", "cumulative")}
+    starts = [4242, 4241, 17, 0]
+    for l, lengths in enumerate(layer_lengths):
+        rows = sum(lengths)
+        args["keys"].append(rand((rows, dim), dtype, device, 20 + l))
+        args["values"].append(rand((rows, dim), dtype, device, 40 + l))
+        args["positions"].append(torch.arange(rows).float().to(device)[:, None] * 2 + l)
+        args["new_k"].append(rand((1, heads, added, dim), dtype, device, 60 + l))
+        args["new_v"].append(rand((1, heads, added, dim), dtype, device, 80 + l))
+        args["cumulative"].append(torch.tensor(np.concatenate(([0], np.cumsum(lengths))),
+                                               dtype=torch.int32, device=device))
+    maximum = max(max(lengths) for lengths in layer_lengths)
+    keys, values, positions, cumulative, lengths_out, first = _C.append_layers(
+        args["keys"], args["values"], args["positions"], args["new_k"], args["new_v"],
+        args["cumulative"], starts, maximum)
+    for l in range(len(layer_lengths)):
+        expect = kv_ops.append(bits(args["keys"][l]), bits(args["values"][l]),
+                               bits(args["positions"][l]).view(np.float32), bits(args["new_k"][l]),
+                               bits(args["new_v"][l]), args["cumulative"][l].cpu().numpy(),
+                               starts[l], maximum)
+        rows = slice(first[l], first[l + 1])
+        np.testing.assert_array_equal(bits(keys[rows]), expect[0])
+        np.testing.assert_array_equal(bits(values[rows]), expect[1])
+        np.testing.assert_array_equal(positions[rows].cpu().numpy(), expect[2])
+        np.testing.assert_array_equal(cumulative[l].cpu().numpy(), expect[3])
+        np.testing.assert_array_equal(lengths_out[l].cpu().numpy(), expect[4])
+    with pytest.raises(RuntimeError, match="Invalid cumulative lengths"):
+        _C.append_layers(args["keys"], args["values"], args["positions"], args["new_k"],
+                         args["new_v"], args["cumulative"][:-1] + [args["cumulative"][0][:3]],
+                         starts, maximum)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(1, 8, 1, 1), (2, 4, 3, 128), (1, 8, 2, 64)])
 def test_append_flattened_cache(device, dtype, shape):
