@@ -604,9 +604,9 @@ def ops_bench(torch, seed, reps=5):
 
 
 def copy_probe(torch, gib=4, reps=5):
-    """What a plain device copy (torch's copy kernel, bf16) reaches on this part at a size far
-    beyond the 256 MB Infinity Cache: the practical ceiling of the read+write row kernels
-    (compaction, merge), next to the 8 TB/s peak."""
+    """What a plain device-to-device copy (torch copy_, carried out by the HIP runtime's copy
+    kernel) reaches on this part at a size far beyond the 256 MB Infinity Cache: the practical
+    ceiling of the read+write row kernels (compaction, merge), next to the 8 TB/s peak."""
     import numpy as np
 
     source = torch.empty((gib << 29,), dtype=torch.bfloat16, device="cuda")
