@@ -356,9 +356,10 @@ __device__ __forceinline__ void dma_rows(const __bf16* matrix, int row0, int las
 // workgroup streams all key tiles of its segment through LDS (double buffered).
 // Output per row (g, w): {-m*log2(e), S, eps*S, op} with m the masked row max, S the sum of
 // exp(z - m) and op = sum exp(z - m) * pv / S; {NaN x4} for a fully masked row.
-// Three waves per SIMD (at most 168 VGPRs) measure faster here than two without spills.
+// Three waves per SIMD (at most 168 VGPRs) measure faster here than two without spills for
+// d <= 128; d = 256 runs two (at most 256 VGPRs; its 74 KB of LDS also fit two workgroups per CU).
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 3 : 1))) void row_stats_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 3 : 2))) void row_stats_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, float scale, float epsilon,
     int64_t wg_per_segment, const float* __restrict__ pv, float4* __restrict__ stats) {
@@ -563,8 +564,10 @@ __device__ __forceinline__ int red_slot(int source_lane) {
   return source_lane * kRedStride + 16 * ((source_lane >> 4) & 3);
 }
 
+// Waves per SIMD the register budget is held to: two with two key tiles (d = 128) and for
+// d = 256 (its 64 KB of LDS also fit two workgroups per CU), three for d = 64.
 template <int D>
-constexpr int column_waves_per_simd() { return column_key_tiles<D>() == 2 ? 2 : D <= 128 ? 3 : 1; }
+constexpr int column_waves_per_simd() { return column_key_tiles<D>() == 2 ? 2 : D <= 128 ? 3 : 2; }
 
 // Units per barrier-separated stage: two for d = 128, where the LDS of a second query tile
 // fits the two workgroups per CU that the registers allow (halving the barriers per unit;
@@ -730,6 +733,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
 #pragma unroll
     for (int k = 0; k < UP; ++k) {
     if (stage * UP + k >= units) break;  // uniform
+    // A wave whose keys all lie at or past the candidate range's end (the tail of a segment's
+    // last workgroup) only takes part in the copies and barriers.
+    if (wave_key0 >= seg.last) {
+      if (++g == groups) {
+        g = 0;
+        ++qt;
+      }
+      continue;
+    }
     f32x16 acc[KT];
     {
       bf16x8 b[KS];
