@@ -102,6 +102,19 @@ __device__ __forceinline__ float logit_fast(float acc, float scale) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// IEEE 754-2019 minimum / maximum (NaN-propagating, -0 < +0) of three values in one
+// instruction; the compiler forms these only with a repeated operand.
+__device__ __forceinline__ float minimum3(float a, float b, float c) {
+  float r;
+  asm("v_minimum3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float maximum3(float a, float b, float c) {
+  float r;
+  asm("v_maximum3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ f32x16 mfma_tile_zero() {
   f32x16 z;
 #pragma unroll
@@ -789,16 +802,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
           ratio[t][r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
         }
     }
+    // The drops restart with each query tile: its first group writes them, the others add.
     const float* pv_row = pv_lds + g * kKeys + wave * 32 * KT;
+    if (g == 0) {
 #pragma unroll
-    for (int t = 0; t < KT; ++t)
+      for (int t = 0; t < KT; ++t)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 32 * t + 8 * c + 4 * half);
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 32 * t + 8 * c + 4 * half);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          drop[t][4 * c + j] = __builtin_fmaf(ratio[t][4 * c + j], w[j] - st.w, drop[t][4 * c + j]);
-      }
+          for (int j = 0; j < 4; ++j) drop[t][4 * c + j] = ratio[t][4 * c + j] * (w[j] - st.w);
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 32 * t + 8 * c + 4 * half);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            drop[t][4 * c + j] = __builtin_fmaf(ratio[t][4 * c + j], w[j] - st.w, drop[t][4 * c + j]);
+        }
+    }
     if (g == groups - 1) {
       // Min / max of each key tile's drops over the query tile's queries, through this wave's
       // LDS scratch. LDS accesses of one wave complete in order, so the reads see this wave's
@@ -818,10 +843,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
         // NaN-propagating, as torch's amin / amax
         if (valid == 16) {
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            const float x = column[q * kRedStride];
-            tile_lo = __builtin_elementwise_minimum(tile_lo, x);
-            tile_hi = __builtin_elementwise_maximum(tile_hi, x);
+          for (int q = 0; q < 16; q += 2) {  // three-input minimum / maximum
+            const float x0 = column[q * kRedStride], x1 = column[(q + 1) * kRedStride];
+            tile_lo = minimum3(tile_lo, x0, x1);
+            tile_hi = maximum3(tile_hi, x0, x1);
           }
         } else {
 #pragma unroll
@@ -836,8 +861,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-#pragma unroll
-        for (int r = 0; r < 16; ++r) drop[t][r] = 0.0f;
       }
     }
     if (++g == groups) {
