@@ -82,32 +82,32 @@ def temporal_risk(probabilities, output_projection, projected_values, margin, fi
     return result
 
 
-_bound_native = False
+_native_module = None
 
 
 def _native():
     """The C++ host module with lr_append / lr_compact bound (once): the per-layer decode-time
     ops run their checks, allocate their outputs and launch from C++ on torch's current stream."""
-    global _bound_native
-    from .scoring import _planner
-    planner = _planner()
-    if not _bound_native:
+    global _native_module
+    if _native_module is None:
         import ctypes
+        from .scoring import _planner
+        planner = _planner()
         library = _lib.load()
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_data_movement(address("lr_append"), address("lr_compact"),
                                    address("lr_append_layers"))
-        _bound_native = True
-    return planner
+        _native_module = planner
+    return _native_module
 
 
 def append(keys, values, positions, new_keys, new_values, cumulative, logical_start,
            maximum_length):
     """csrc/scoring.cu:264-292 -> [keys, values, positions [N,1], cumulative i32, lengths i32].
     Checks (csrc/scoring.cu:257-283, same order and messages), allocation and launch are made by
-    the C++ host module (csrc/host_plan.cpp append_launch)."""
-    return _native().append(keys, values, positions, new_keys, new_values, cumulative,
-                            int(logical_start), int(maximum_length))
+    the C++ host module (csrc/host_plan.cpp append_launch); the integers are converted there."""
+    return (_native_module or _native()).append(keys, values, positions, new_keys, new_values,
+                                                cumulative, logical_start, maximum_length)
 
 
 def append_layers(keys, values, positions, new_keys, new_values, cumulative, logical_starts,
@@ -126,7 +126,7 @@ def append_layers(keys, values, positions, new_keys, new_values, cumulative, log
 def compact(keys, values, positions, removed):
     """csrc/scoring.cu:294-314 -> [keys, values, positions [N-E,1]]; removed sorted, unique.
     Checks, allocation and launch in the C++ host module (csrc/host_plan.cpp compact_launch)."""
-    return _native().compact(keys, values, positions, removed)
+    return (_native_module or _native()).compact(keys, values, positions, removed)
 
 
 def pool(scores, bounds, maximum_count, width):

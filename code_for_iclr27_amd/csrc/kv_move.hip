@@ -720,11 +720,15 @@ extern "C" int lr_append(const void* keys, const void* values, const float* posi
   const int g = granule_for(row_bytes, {keys, values, new_keys, new_values, out_keys, out_values});
   const int64_t covered = max_length + added;
   const RowLayout layout = make_layout(row_bytes, g, covered * heads, 8);
-  int64_t bx = ceil_div(ceil_div(covered, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  // Two-wave workgroups: one decode step's layer (cfg1: 18 MB) is a single round of copies, and
+  // twice the workgroups of 256 threads spread it evenly over the CUs (measured 13% less device
+  // time per layer than 256-thread workgroups).
+  constexpr int kAppendThreads = 128;
+  int64_t bx = ceil_div(ceil_div(covered, layout.rows_per_group), kAppendThreads >> layout.lanes_log2);
   if (bx < 1) bx = 1;
   dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads));
   return dispatch_granule(g, [&]<int G>() {
-    head_append_kernel<G, true><<<grid, kThreads, 0, as_stream(stream)>>>(
+    head_append_kernel<G, true><<<grid, kAppendThreads, 0, as_stream(stream)>>>(
         bytes(keys), bytes(values), positions, rows, bytes(new_keys), bytes(new_values),
         cumulative, cumulative, 1, heads, added, covered, logical_start, layout,
         bytes(out_keys), bytes(out_values), out_positions, out_cumulative, out_lengths);

@@ -68,9 +68,13 @@ class Reinserter:
         return address
 
     def __del__(self):
+        # at interpreter exit the module globals may already be gone; the process releases
+        # its pinned memory then anyway
+        library = getattr(_lib, "_library", None) if _lib is not None else None
+        if library is None:
+            return
         for address in getattr(self, "flags", {}).values():
-            if _lib._library is not None:
-                _lib._library.lr_staging_free(address)
+            library.lr_staging_free(address)
 
     def run(self, layers: Sequence[LayerState], payload: torch.Tensor, metadata) -> ReinsertOutcome:
         """Inserts payload rows [M, 2, d] (K at [i, 0], V at [i, 1]; pinned host memory or
