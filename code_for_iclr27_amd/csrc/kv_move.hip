@@ -142,7 +142,7 @@ __device__ __forceinline__ void compact_block(const uint8_t* keys, const uint8_t
   __shared__ int64_t source[kCompactRows];
   const bool in_lds = removed_count <= kCompactStaged;
   if (in_lds)
-    for (int64_t i = threadIdx.x; i < removed_count; i += kThreads)
+    for (int64_t i = threadIdx.x; i < removed_count; i += blockDim.x)
       staged[i] = static_cast<int32_t>(removed[i]);
   __syncthreads();
   if (static_cast<int>(threadIdx.x) < n) {
