@@ -37,8 +37,12 @@ typedef unsigned attn_u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = 64 * kAttnWaves;
 // Keys per wave: 12 KB of K rows (and as many V bytes) for d64/d128, 16 KB for d256 (a whole
-// number of 16-key MFMA blocks); small enough for three waves per SIMD.
+// number of 16-key MFMA blocks); small enough for three waves per SIMD. A call whose blocks of
+// that size would not give every CU two workgroups (batch-1 decode: cfg1 has 96) takes one
+// 16-key MFMA block per wave instead, so that its single round of loads spreads over the chip.
 constexpr int wave_keys(int dim) { return dim == 256 ? 32 : 6144 / dim; }
+constexpr int kSmallWaveKeys = 16;
+constexpr int64_t kFewBlocks = 512;
 constexpr int kMergeUnroll = 4;       // partial blocks each merging thread loads at once
 constexpr float kAttnLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -137,14 +141,13 @@ __device__ __forceinline__ void merge_into(MergeState& s, float m, float l, cons
   s.m = mx;
 }
 
-template <typename T, int D, int R>
+template <typename T, int D, int R, int CH>
 __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attention_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "head dim");
   static_assert(R == 4 || R == 8, "rows per tile");
   constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
   constexpr int LPK = D / 8;          // lanes per V row in the P*V phase
   constexpr int KPI = 64 / LPK;       // V rows per wave-wide load
-  constexpr int CH = wave_keys(D);    // keys per wave
   static_assert(CH % 16 == 0, "whole MFMA key blocks");
   constexpr int NB = CH / 16;         // 16-key MFMA blocks per wave
   constexpr int VL = CH / KPI;        // V loads (16 B) per lane
@@ -366,12 +369,12 @@ __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attenti
 // Second launch: one workgroup per (segment, tile) whose keys spanned more than one block merges
 // the blocks' partial states. Thread (part, item) folds blocks part, part + PARTS, ... with the
 // loads of kMergeUnroll blocks in flight at once; the PARTS states then meet in LDS.
-template <typename T, int D, int R>
+template <typename T, int D, int R, int CH>
 __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs a) {
   constexpr int LPK = D / 8;
   constexpr int ITEMS = R * LPK;
   constexpr int PARTS = kAttnThreads / ITEMS;
-  constexpr int64_t kBlockKeys = kAttnWaves * wave_keys(D);
+  constexpr int64_t kBlockKeys = kAttnWaves * CH;
   __shared__ __align__(16) float merge_o[kAttnThreads][8];
   __shared__ float merge_ml[kAttnThreads][2];
   const int tid = threadIdx.x;
@@ -435,12 +438,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs 
 }
 
 struct AttnPlan {
-  int rows_per_tile;
+  int rows_per_tile, wave_keys;
   int64_t tiles, splits, chunk, units;
 };
-
-// Keys one workgroup covers: four waves of wave_keys(dim) keys each.
-int64_t block_keys(int64_t dim) { return kAttnWaves * wave_keys(static_cast<int>(dim)); }
 
 AttnPlan plan_attention(int64_t segments, int64_t groups, int64_t length, int64_t max_keys,
                         int64_t dim) {
@@ -449,8 +449,15 @@ AttnPlan plan_attention(int64_t segments, int64_t groups, int64_t length, int64_
   p.rows_per_tile = rows <= 4 ? 4 : 8;
   p.tiles = ceil_div(rows, p.rows_per_tile);
   p.units = segments * p.tiles;
-  p.chunk = block_keys(dim);
+  // Keys one workgroup covers: four waves of wave_keys keys each.
+  p.wave_keys = wave_keys(static_cast<int>(dim));
+  p.chunk = kAttnWaves * p.wave_keys;
   p.splits = std::max<int64_t>(1, ceil_div(max_keys, p.chunk));
+  if (p.units * p.splits < kFewBlocks && p.splits > 1) {
+    p.wave_keys = kSmallWaveKeys;
+    p.chunk = kAttnWaves * p.wave_keys;
+    p.splits = ceil_div(max_keys, p.chunk);
+  }
   return p;
 }
 
@@ -460,31 +467,38 @@ size_t workspace_bytes(const AttnPlan& p, int64_t dim) {
   return static_cast<size_t>(slots) * static_cast<size_t>(dim + 2) * 4;
 }
 
-template <typename T, int D, int R>
+template <typename T, int D, int R, int CH>
 int launch_attention(const AttnArgs& args, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((packed_attention_kernel<T, D, R>), dim3(static_cast<unsigned>(blocks)),
+  hipLaunchKernelGGL((packed_attention_kernel<T, D, R, CH>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kAttnThreads), 0, stream, args);
   if (int status = check_launch("packed_attention")) return status;
   if (args.splits == 1) return LR_OK;
-  hipLaunchKernelGGL((attention_merge_kernel<T, D, R>),
+  hipLaunchKernelGGL((attention_merge_kernel<T, D, R, CH>),
                      dim3(static_cast<unsigned>(blocks / args.splits)), dim3(kAttnThreads), 0,
                      stream, args);
   return check_launch("packed_attention merge");
 }
 
+template <typename T, int D, int R>
+int launch_keys(const AttnArgs& args, int keys_per_wave, int64_t blocks, hipStream_t stream) {
+  return keys_per_wave == kSmallWaveKeys
+             ? launch_attention<T, D, R, kSmallWaveKeys>(args, blocks, stream)
+             : launch_attention<T, D, R, wave_keys(D)>(args, blocks, stream);
+}
+
 template <typename T, int D>
-int launch_rows(const AttnArgs& args, int rows_per_tile, int64_t blocks, hipStream_t stream) {
-  return rows_per_tile == 4 ? launch_attention<T, D, 4>(args, blocks, stream)
-                            : launch_attention<T, D, 8>(args, blocks, stream);
+int launch_rows(const AttnArgs& args, const AttnPlan& plan, int64_t blocks, hipStream_t stream) {
+  return plan.rows_per_tile == 4 ? launch_keys<T, D, 4>(args, plan.wave_keys, blocks, stream)
+                                 : launch_keys<T, D, 8>(args, plan.wave_keys, blocks, stream);
 }
 
 template <typename T>
-int launch_dim(const AttnArgs& args, int64_t dim, int rows_per_tile, int64_t blocks,
+int launch_dim(const AttnArgs& args, int64_t dim, const AttnPlan& plan, int64_t blocks,
                hipStream_t stream) {
   switch (dim) {
-    case 64: return launch_rows<T, 64>(args, rows_per_tile, blocks, stream);
-    case 128: return launch_rows<T, 128>(args, rows_per_tile, blocks, stream);
-    default: return launch_rows<T, 256>(args, rows_per_tile, blocks, stream);
+    case 64: return launch_rows<T, 64>(args, plan, blocks, stream);
+    case 128: return launch_rows<T, 128>(args, plan, blocks, stream);
+    default: return launch_rows<T, 256>(args, plan, blocks, stream);
   }
 }
 
@@ -565,8 +579,8 @@ int packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head
   }
   const hipStream_t s = as_stream(stream);
   return dtype == LR_DTYPE_BF16
-             ? launch_dim<__bf16>(args, dim, plan.rows_per_tile, blocks, s)
-             : launch_dim<_Float16>(args, dim, plan.rows_per_tile, blocks, s);
+             ? launch_dim<__bf16>(args, dim, plan, blocks, s)
+             : launch_dim<_Float16>(args, dim, plan, blocks, s);
 }
 
 // Workspace of the allocation-free entry point: one fixed array per device, held from the

@@ -233,6 +233,8 @@ struct Library {
   decltype(&lr_append) append = nullptr;
   decltype(&lr_compact) compact = nullptr;
   decltype(&lr_append_layers) append_layers = nullptr;
+  decltype(&lr_packed_attention) packed_attention = nullptr;
+  decltype(&lr_packed_attention_workspace_bytes) attention_workspace_bytes = nullptr;
   decltype(&lr_last_error) last_error = nullptr;
   decltype(&lr_staging_alloc) staging_alloc = nullptr;
   decltype(&lr_staging_free) staging_free = nullptr;
@@ -270,6 +272,11 @@ void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers) 
   bind_one(library.append, append);
   bind_one(library.compact, compact);
   bind_one(library.append_layers, append_layers);
+}
+
+void bind_attention(int64_t packed_attention, int64_t workspace_bytes) {
+  bind_one(library.packed_attention, packed_attention);
+  bind_one(library.attention_workspace_bytes, workspace_bytes);
 }
 
 void check_call(int status) {
@@ -828,6 +835,63 @@ py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
   return py::make_tuple(block, new_lens, offsets, out_row, max_length);
 }
 
+void* current_stream(const torch::Device& device);
+
+// ---------------------------------------------------------------------------------------
+// packed_attention (src/lazy_recall/attention.py:15-35) with its checks, output and workspace
+// allocation and launch in C++: a decode step makes one call per layer, and from Python the
+// checks, the device context and two ctypes calls cost about 20 us of host time per call, more
+// than the kernel. Same checks, order and messages as the Python layer. Returns the output
+// [batch, length, query_heads * dim].
+torch::Tensor attention_launch(const torch::Tensor& queries, const torch::Tensor& keys_in,
+                               const torch::Tensor& values_in, const torch::Tensor& cumulative,
+                               int64_t decoding_count, int64_t max_keys, int64_t length,
+                               int64_t kv_heads) {
+  require(library.packed_attention != nullptr, "library entry points are not bound");
+  require(queries.dim() == 4, "Query length differs from the queries tensor");
+  const int64_t batch = queries.size(0), query_heads = queries.size(1), dim = queries.size(3);
+  require(queries.size(2) == length, "Query length differs from the queries tensor");
+  require(kv_heads > 0 && query_heads % kv_heads == 0,
+          "Number of heads in key/value must divide number of heads in query");
+  const int64_t groups = query_heads / kv_heads;
+  const auto dtype = queries.scalar_type();
+  require(dtype == torch::kHalf || dtype == torch::kBFloat16,
+          "FlashAttention only supports fp16 and bf16 data type");
+  require(keys_in.scalar_type() == dtype && values_in.scalar_type() == dtype,
+          "query and key must have the same dtype");
+  for (const torch::Tensor* t : {&queries, &keys_in, &values_in}) {
+    require(t->is_cuda(), "Expected contiguous CUDA tensor");
+    require(t->device() == queries.device(), "CUDA devices differ");
+  }
+  require(dim == 64 || dim == 128 || dim == 256, "Head dimension must be 64, 128 or 256");
+  require(queries.stride(3) == 1, "Input tensor must have contiguous last dimension");
+  const torch::Tensor keys = keys_in.reshape({-1, dim}), values = values_in.reshape({-1, dim});
+  require(keys.is_contiguous() && values.is_contiguous(), "Expected contiguous CUDA tensor");
+  require(keys.sizes() == values.sizes(), "Keys and values differ in shape");
+  const int64_t segments = batch * kv_heads;
+  require(cumulative.is_cuda() && cumulative.scalar_type() == torch::kInt32 &&
+              cumulative.is_contiguous() && cumulative.numel() == segments + 1,
+          "cu_seqlens_k must have shape (batch_size + 1)");
+  require(cumulative.device() == queries.device(), "CUDA devices differ");
+  require(decoding_count == segments + 1, "cu_seqlens_q must have shape (batch_size + 1)");
+  require(max_keys >= 0, "Invalid max_seqlen_k");
+  const c10::DeviceGuard guard(queries.device());
+  torch::Tensor out = torch::empty({batch, length, query_heads, dim}, queries.options());
+  const size_t size = library.attention_workspace_bytes(segments, groups, length, max_keys, dim);
+  torch::Tensor workspace;
+  if (size)
+    workspace = torch::empty({static_cast<int64_t>(size)},
+                             queries.options().dtype(torch::kUInt8));
+  const float scale = static_cast<float>(std::pow(static_cast<double>(dim), -0.5));
+  check_call(library.packed_attention(
+      queries.data_ptr(), queries.stride(0), queries.stride(1), queries.stride(2),
+      keys.numel() ? keys.data_ptr() : nullptr, values.numel() ? values.data_ptr() : nullptr,
+      keys.size(0), cumulative.data_ptr<int32_t>(), batch, kv_heads, groups, length, dim,
+      dtype == torch::kBFloat16 ? LR_DTYPE_BF16 : LR_DTYPE_F16, max_keys, scale, out.data_ptr(),
+      size ? workspace.data_ptr() : nullptr, size, current_stream(queries.device())));
+  return out.view({batch, length, query_heads * dim});
+}
+
 // ---------------------------------------------------------------------------------------
 // The per-layer drop-ins _C.append and _C.compact with their checks, output allocation and
 // launch in C++ (a decode step makes one append per layer; from Python each call cost ~20 us of
@@ -1076,6 +1140,10 @@ PYBIND11_MODULE(_plan, module) {
   module.def("audit_launch", &audit_launch, "Enqueue one whole audit step");
   module.def("queue_evict_launch", &queue_evict_launch,
              "Enqueue one evict_prefix batch of an audit's lazy queue");
+  module.def("bind_attention", &bind_attention,
+             "Bind lr_packed_attention and its workspace size (addresses from the ctypes handle)");
+  module.def("packed_attention", &attention_launch,
+             "packed_attention: checks, output and workspace allocation and launch from C++");
   module.def("reinsert_prepare", &reinsert_prepare,
              "Check a reinsertion and build its pinned table + metadata block");
   module.def("plan_batch_append", &plan_batch_append,
