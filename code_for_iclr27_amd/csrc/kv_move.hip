@@ -88,6 +88,13 @@ __device__ __forceinline__ GroupCoord group_coord(int lanes_log2) {
 // all its loads of the batch before any store: a load issued under a per-row branch would be
 // waited for before the next one. Rows that are not copied read `src` = a readable fallback
 // row and store nothing.
+//
+// Cache policy of the row copies (measured per kernel on gfx950): the all-layer kernels that
+// move hundreds of MB run faster with nontemporal (`nt`) accesses, which stream past the
+// caches (compaction and reinsertion: loads and stores; the all-layer append: stores only),
+// while the per-layer drop-ins (one layer, tens of MB, often still in the 256 MB Infinity
+// Cache) are slower with them and keep the default forms.
+enum CopyPolicy : int { kCached = 0, kStreamStores = 2, kStreamAll = 3 };
 
 template <bool kTwo>
 struct RowBatch {
@@ -98,7 +105,21 @@ struct RowBatch {
   bool ok[kBatch];
 };
 
-template <int G, bool kTwo>
+template <int P, typename V>
+__device__ __forceinline__ V load_granule(const uint8_t* row, int64_t c) {
+  const auto p = global_ptr(reinterpret_cast<const V*>(row)) + c;
+  if constexpr ((P & 1) != 0) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <int P, typename V>
+__device__ __forceinline__ void store_granule(uint8_t* row, int64_t c, V v) {
+  const auto p = global_ptr(reinterpret_cast<V*>(row)) + c;
+  if constexpr ((P & 2) != 0) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+template <int G, bool kTwo, int P = kCached>
 __device__ __forceinline__ void copy_batch(const RowBatch<kTwo>& b, int64_t chunks, int lane,
                                            int lanes) {
   using V = typename RawGranule<G>::type;
@@ -106,14 +127,14 @@ __device__ __forceinline__ void copy_batch(const RowBatch<kTwo>& b, int64_t chun
     V x[kBatch], y[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      x[u] = global_ptr(reinterpret_cast<const V*>(b.src[u]))[c];
-      if constexpr (kTwo) y[u] = global_ptr(reinterpret_cast<const V*>(b.src2[u]))[c];
+      x[u] = load_granule<P, V>(b.src[u], c);
+      if constexpr (kTwo) y[u] = load_granule<P, V>(b.src2[u], c);
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       if (b.ok[u]) {
-        global_ptr(reinterpret_cast<V*>(b.dst[u]))[c] = x[u];
-        if constexpr (kTwo) global_ptr(reinterpret_cast<V*>(b.dst2[u]))[c] = y[u];
+        store_granule<P, V>(b.dst[u], c, x[u]);
+        if constexpr (kTwo) store_granule<P, V>(b.dst2[u], c, y[u]);
       }
     }
   }
@@ -131,7 +152,7 @@ constexpr int kCompactRows = 128;     // most output rows per block (measured fa
 constexpr int kCompactStaged = 4096;  // removal entries staged in LDS (larger lists: global)
 static_assert(kCompactRows <= kThreads, "one thread maps each output row of a block");
 
-template <int G>
+template <int G, int P>
 __device__ __forceinline__ void compact_block(const uint8_t* keys, const uint8_t* values,
                                               const float* positions, int64_t length,
                                               const int64_t* removed, int64_t removed_count,
@@ -175,7 +196,7 @@ __device__ __forceinline__ void compact_block(const uint8_t* keys, const uint8_t
       b.dst[u] = out_keys + (out_start + d0 + r) * rb;
       b.dst2[u] = out_values + (out_start + d0 + r) * rb;
     }
-    copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+    copy_batch<G, true, P>(b, layout.chunks, gc.lane, gc.lanes);
   }
 }
 
@@ -191,15 +212,15 @@ __global__ __launch_bounds__(kThreads) void compact_kernel(
   const int64_t d0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
   if (d0 >= rows_out) return;  // uniform across the block
   const int n = static_cast<int>(rows_out - d0 < rows_per_block ? rows_out - d0 : rows_per_block);
-  compact_block<G>(keys, values, positions, rows_in, removed, removed_count, d0, n, 0, layout,
-                   out_keys, out_values, out_positions);
+  compact_block<G, kCached>(keys, values, positions, rows_in, removed, removed_count, d0, n, 0,
+                            layout, out_keys, out_values, out_positions);
 }
 
 // ---------------------------------------------------------------------------------------
 // Per-head ragged append (csrc/scoring.cu:130-162 and csrc/cache_legacy.cu:13-40): head h's
 // old rows move from src_start(h) to dst_start(h) = src_start(h) + h * added, followed by
 // `added` new rows. blockIdx.y = head; rows of a head are covered up to `covered_rows`.
-template <int G, bool kWithPositions>
+template <int G, bool kWithPositions, int P>
 __device__ __forceinline__ void head_append(
     const uint8_t* __restrict__ cache_keys, const uint8_t* __restrict__ cache_values,
     const float* __restrict__ positions, int64_t rows_in, const uint8_t* __restrict__ new_keys,
@@ -262,7 +283,7 @@ __device__ __forceinline__ void head_append(
           position[u] = old ? loaded : static_cast<float>(logical_start + (p - old_length));
         }
       }
-      copy_batch<G, kTwo>(b, layout.chunks, gc.lane, gc.lanes);
+      copy_batch<G, kTwo, P>(b, layout.chunks, gc.lane, gc.lanes);
       if (kWithPositions && gc.lane == 0) {
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
@@ -282,10 +303,10 @@ __global__ __launch_bounds__(kThreads) void head_append_kernel(
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
     int32_t* __restrict__ out_lengths) {
-  head_append<G, kWithPositions>(cache_keys, cache_values, positions, rows_in, new_keys,
-                                 new_values, starts, lengths_or_next, lengths_are_cumulative,
-                                 heads, added, covered_rows, logical_start, layout, out_keys,
-                                 out_values, out_positions, out_cumulative, out_lengths);
+  head_append<G, kWithPositions, kCached>(
+      cache_keys, cache_values, positions, rows_in, new_keys, new_values, starts, lengths_or_next,
+      lengths_are_cumulative, heads, added, covered_rows, logical_start, layout, out_keys,
+      out_values, out_positions, out_cumulative, out_lengths);
 }
 
 // One decode step's append into every layer (blockIdx.z = layer): the per-layer append above
@@ -302,14 +323,13 @@ __global__ __launch_bounds__(kThreads) void append_layers_kernel(
   const int64_t* row = table + layer * LR_APPEND_WORDS;
   const int64_t first = row[8];
   const int32_t* cumulative = reinterpret_cast<const int32_t*>(row[4]);
-  head_append<G, true>(reinterpret_cast<const uint8_t*>(row[0]),
-                       reinterpret_cast<const uint8_t*>(row[1]),
-                       reinterpret_cast<const float*>(row[2]), row[3],
-                       reinterpret_cast<const uint8_t*>(row[5]),
-                       reinterpret_cast<const uint8_t*>(row[6]), cumulative, cumulative, 1, heads,
-                       added, covered_rows, row[7], layout, out_keys + first * layout.row_bytes,
-                       out_values + first * layout.row_bytes, out_positions + first,
-                       out_cumulative + layer * (heads + 1), out_lengths + layer * heads);
+  head_append<G, true, kStreamStores>(
+      reinterpret_cast<const uint8_t*>(row[0]), reinterpret_cast<const uint8_t*>(row[1]),
+      reinterpret_cast<const float*>(row[2]), row[3], reinterpret_cast<const uint8_t*>(row[5]),
+      reinterpret_cast<const uint8_t*>(row[6]), cumulative, cumulative, 1, heads, added,
+      covered_rows, row[7], layout, out_keys + first * layout.row_bytes,
+      out_values + first * layout.row_bytes, out_positions + first,
+      out_cumulative + layer * (heads + 1), out_lengths + layer * heads);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -488,10 +508,11 @@ __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
   int64_t out_start = 0;
   for (int w = 0; w < kThreads / 64; ++w) out_start += partial[w];
   const int n = static_cast<int>(rows_out - d0 < kCompactRows ? rows_out - d0 : kCompactRows);
-  compact_block<G>(reinterpret_cast<const uint8_t*>(row[0]), reinterpret_cast<const uint8_t*>(row[1]),
-                   reinterpret_cast<const float*>(row[2]), length,
-                   segment >= 0 ? removed_positions + offsets[segment] : nullptr, removed_count,
-                   d0, n, out_start, layout, out_keys, out_values, out_positions);
+  compact_block<G, kStreamAll>(
+      reinterpret_cast<const uint8_t*>(row[0]), reinterpret_cast<const uint8_t*>(row[1]),
+      reinterpret_cast<const float*>(row[2]), length,
+      segment >= 0 ? removed_positions + offsets[segment] : nullptr, removed_count, d0, n,
+      out_start, layout, out_keys, out_values, out_positions);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -629,7 +650,7 @@ __global__ __launch_bounds__(kThreads) void reinsert_resident_kernel(
       b.dst[u] = out_keys + to * rb;
       b.dst2[u] = out_values + to * rb;
     }
-    copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
+    copy_batch<G, true, kStreamAll>(b, layout.chunks, gc.lane, gc.lanes);
   }
 }
 

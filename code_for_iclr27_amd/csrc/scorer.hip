@@ -42,6 +42,12 @@ template <typename T>
 __device__ __forceinline__ T gload(const void* p) {
   return *(const __attribute__((address_space(1))) T*)p;
 }
+// The same with a nontemporal load, for data read exactly once (V in the projected-values
+// pass: measured faster than the default load on gfx950).
+template <typename T>
+__device__ __forceinline__ T gload_stream(const void* p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) T*)p);
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxGroups = 16;
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __
       const int t = base + k * RPB;
 #pragma unroll
       for (int e = 0; e < 8; ++e) raw[k][e] = static_cast<__bf16>(0.0f);
-      if (t < length) raw[k] = gload<bf16x8>(seg.values + static_cast<int64_t>(t) * D + 8 * lane);
+      if (t < length) raw[k] = gload_stream<bf16x8>(seg.values + static_cast<int64_t>(t) * D + 8 * lane);
     }
   };
   auto reduce = [&](int first, const bf16x8 (&raw)[kRows]) {
