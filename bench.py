@@ -604,29 +604,42 @@ def ops_bench(torch, seed, reps=5):
 
 
 def copy_probe(torch, gib=4, reps=5):
-    """What a plain device-to-device copy (torch copy_, carried out by the HIP runtime's copy
-    kernel) reaches on this part at a size far beyond the 256 MB Infinity Cache: the practical
-    ceiling of the read+write row kernels (compaction, merge), next to the 8 TB/s peak."""
+    """What a plain device-to-device copy reaches on this part at a size far beyond the 256 MB
+    Infinity Cache, next to the 8 TB/s peak: torch's copy_ (the HIP runtime's copy kernel), and
+    the library's calibration copy lr_stream_copy (the nontemporal 16-byte loads and stores of
+    the all-layer row kernels), the practical ceiling of the read+write row kernels."""
     import numpy as np
+
+    from code_for_iclr27_amd import _lib
 
     source = torch.empty((gib << 29,), dtype=torch.bfloat16, device="cuda")
     source.fill_(1.0)
     target = torch.empty_like(source)
-    times = []
-    for _ in range(reps + 1):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        target.copy_(source)
-        b.record()
-        torch.cuda.synchronize()
-        times.append(a.elapsed_time(b))
-    ms = float(np.median(times[1:]))
     nbytes = 2 * source.numel() * 2
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def timed(copy):
+        times = []
+        for _ in range(reps + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            copy()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b))
+        ms = float(np.median(times[1:]))
+        return {"ms": round(ms, 3), "GBps": round(nbytes / (ms / 1e3) / 1e9, 1),
+                "hbm_fraction": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+    runtime = timed(lambda: target.copy_(source))
+    target.zero_()
+    streamed = timed(lambda: _lib.call("lr_stream_copy", source.data_ptr(), target.data_ptr(),
+                                       nbytes // 2, stream))
+    if not torch.equal(target, source):
+        raise RuntimeError("stream copy probe: the copy differs from its source")
     del source, target
     torch.cuda.empty_cache()
-    return {"bytes_read_plus_written": nbytes, "ms": round(ms, 3),
-            "GBps": round(nbytes / (ms / 1e3) / 1e9, 1),
-            "hbm_fraction": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    return {"bytes_read_plus_written": nbytes, **runtime, "stream_copy": streamed}
 
 
 def lazy_window_bench(torch, layers, qpos, margin, cfg, reps=5):

@@ -73,6 +73,7 @@ SIGNATURES = {
     "lr_staging_alloc": [_SZ, _P],
     "lr_staging_free": [_P],
     "lr_copy_words": [_P, _P, _I64, _P],
+    "lr_stream_copy": [_P, _P, _I64, _P],
     "lr_packed_attention_workspace_bytes": [_I64, _I64, _I64, _I64, _I64],
     "lr_packed_attention": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
                             _I, _I64, _F, _P, _P, _SZ, _P],

@@ -88,6 +88,28 @@ __global__ __launch_bounds__(256) void copy_words_kernel(const int64_t* __restri
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < words) destination[i] = source[i];
 }
+
+// Device-to-device copy of 16-byte granules with nontemporal loads and stores, four granules
+// per thread in flight, one pass (no grid-stride loop): the form of the all-layer row kernels,
+// on a plain copy.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kStreamUnroll = 4;
+__global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4* __restrict__ source,
+                                                          u32x4* __restrict__ destination,
+                                                          int64_t granules) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * kStreamUnroll + threadIdx.x;
+  u32x4 v[kStreamUnroll];
+#pragma unroll
+  for (int u = 0; u < kStreamUnroll; ++u) {
+    const int64_t i = base + static_cast<int64_t>(u) * 256;
+    if (i < granules) v[u] = __builtin_nontemporal_load(source + i);
+  }
+#pragma unroll
+  for (int u = 0; u < kStreamUnroll; ++u) {
+    const int64_t i = base + static_cast<int64_t>(u) * 256;
+    if (i < granules) __builtin_nontemporal_store(v[u], destination + i);
+  }
+}
 }  // namespace
 }  // namespace lr
 
@@ -100,4 +122,20 @@ extern "C" int lr_copy_words(const int64_t* source, int64_t* destination, int64_
   const unsigned blocks = static_cast<unsigned>((words + 255) / 256);
   lr::copy_words_kernel<<<blocks, 256, 0, lr::as_stream(stream)>>>(source, destination, words);
   return lr::check_launch("copy_words");
+}
+
+extern "C" int lr_stream_copy(const void* source, void* destination, int64_t bytes, void* stream) {
+  lr::clear_error();
+  LR_REQUIRE(bytes >= 0 && bytes % 16 == 0, "Copy size must be a multiple of 16 bytes");
+  if (bytes == 0) return LR_OK;
+  LR_REQUIRE(source != nullptr && destination != nullptr, "Expected non-null buffers");
+  LR_REQUIRE((reinterpret_cast<uintptr_t>(source) & 15) == 0 &&
+                 (reinterpret_cast<uintptr_t>(destination) & 15) == 0,
+             "Copy buffers must be 16-byte aligned");
+  const int64_t granules = bytes / 16;
+  const int64_t blocks = (granules + 256 * lr::kStreamUnroll - 1) / (256 * lr::kStreamUnroll);
+  LR_REQUIRE(blocks < (int64_t{1} << 31), "Copy too large");
+  lr::stream_copy_kernel<<<static_cast<unsigned>(blocks), 256, 0, lr::as_stream(stream)>>>(
+      static_cast<const lr::u32x4*>(source), static_cast<lr::u32x4*>(destination), granules);
+  return lr::check_launch("stream_copy");
 }

@@ -344,6 +344,12 @@ int lr_staging_alloc(size_t bytes, void** host);
 int lr_staging_free(void* host);
 int lr_copy_words(const int64_t* source, int64_t* destination, int64_t words, void* stream);
 
+/* Calibration copy (no reference counterpart): copies `bytes` (a multiple of 16; both buffers
+ * 16-byte aligned device memory) with the nontemporal 16-byte loads and stores that the
+ * all-layer row kernels use, on `stream`. Timed on a copy far beyond the caches, it gives the
+ * practical read+write ceiling those kernels are measured against. */
+int lr_stream_copy(const void* source, void* destination, int64_t bytes, void* stream);
+
 /* Device-resident query history (replaces the per-layer deques and the per-audit torch.cat of
  * src/lazy_recall/history.py:21-38,51-63). `ring` is [layers, heads, 2 * window, dim] elements
  * of elem_bytes (2 or 4) and ring_positions [2 * window] i64, both device memory. Writes query l

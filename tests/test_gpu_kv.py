@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from code_for_iclr27_amd import _C, _legacy_C
+from code_for_iclr27_amd import _C, _legacy_C, _lib
 from oracle import kv_ops
 
 pytestmark = pytest.mark.gpu
@@ -337,3 +337,18 @@ def test_validation_messages(device):
     with pytest.raises(RuntimeError, match="Mapping must be int64"):
         _C.merge(keys, keys, positions, torch.zeros((1, 2, 8), dtype=torch.bfloat16, device=device),
                  torch.zeros(1, device=device), torch.zeros(5, dtype=torch.int32, device=device))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nbytes", [16, 16 * 1023, 16 * 1024, 16 * 4097 + 16 * 3, 37 << 20])
+def test_stream_copy(device, nbytes):
+    """The calibration copy (nontemporal loads and stores) is an exact byte copy, including a
+    partial last block, and leaves the bytes after the range alone."""
+    generator = torch.Generator(device="cpu").manual_seed(nbytes)
+    source = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=generator).to(device)
+    target = torch.zeros((nbytes + 64,), dtype=torch.uint8, device=device)
+    _lib.call("lr_stream_copy", source.data_ptr(), target.data_ptr(), nbytes,
+              torch.cuda.current_stream(device).cuda_stream)
+    torch.cuda.synchronize(device)
+    assert torch.equal(target[:nbytes], source)
+    assert int(target[nbytes:].count_nonzero()) == 0

@@ -48,6 +48,15 @@ def test_noalloc_attention_size_check_needs_no_gpu():
     assert status == 1 and "holds at most 16777216 bytes" in _lib.last_error()
 
 
+def test_stream_copy_checks_size_and_alignment_on_host():
+    library = _lib.load()
+    assert library.lr_stream_copy(None, None, 0, None) == 0
+    assert library.lr_stream_copy(None, None, 24, None) == 1
+    assert "multiple of 16" in _lib.last_error()
+    assert library.lr_stream_copy(8, 16, 32, None) == 1
+    assert "16-byte aligned" in _lib.last_error()
+
+
 def test_pre_gradient_layers_width_bound_matches_per_layer_check():
     library = _lib.load()
     status = library.lr_pre_gradient_layers(None, 2, 16, 8200, _lib.LR_DTYPE_BF16, None, 0, None)
