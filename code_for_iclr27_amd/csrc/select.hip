@@ -19,6 +19,7 @@ namespace lr {
 namespace {
 
 constexpr int kSegThreads = 256;   // per-segment workgroups
+constexpr int kLoadBatch = 8;      // global loads per thread issued together
 constexpr int kPickThreads = 512;  // segment_pick workgroups (measured faster than 256:
                                    // cfg1 selection 50 -> 47 us, cfg4 108 -> 79 us)
 
@@ -395,10 +396,23 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
   const int64_t begin = s == 0 ? 0 : ends[s - 1], end = ends[s];
   const uint32_t threshold = st.prefix;
   uint32_t less = 0, equal = 0;
-  for (int64_t i = begin + threadIdx.x; i < end; i += kSegThreads) {
-    const uint32_t key = float_key(scores[i]);
-    less += key < threshold;
-    equal += key == threshold;
+  // kLoadBatch loads per thread in flight at once (a loop of single loads pays the memory
+  // latency once per element)
+  for (int64_t base = begin + threadIdx.x; base < end; base += kSegThreads * kLoadBatch) {
+    float v[kLoadBatch];
+#pragma unroll
+    for (int u = 0; u < kLoadBatch; ++u) {
+      const int64_t i = base + u * kSegThreads;
+      v[u] = i < end ? scores[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kLoadBatch; ++u) {
+      if (base + u * kSegThreads < end) {
+        const uint32_t key = float_key(v[u]);
+        less += key < threshold;
+        equal += key == threshold;
+      }
+    }
   }
   uint32_t bl, be, total_less, total_equal;
   block_scan_pair<kSegThreads>(less, equal, wave_sums, bl, be, total_less, total_equal);
@@ -442,7 +456,8 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
 
 // Radix select inside one workgroup: the k-th smallest (1-based) of the n keys key_at(i), by
 // three LDS-histogram passes (11, 11, 10 bits). Returns the key and how many keys equal to it
-// belong to the bottom k.
+// belong to the bottom k. Each thread reads kLoadBatch keys before it counts them, so keys in
+// global memory are read with that many loads in flight.
 template <typename KeyAt>
 __device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_at, uint32_t* hist,
                                              uint32_t (*wave_sums)[2], uint32_t* found,
@@ -454,9 +469,17 @@ __device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_a
     constexpr int BINS = 1 << shape.bits;
     for (int i = threadIdx.x; i < BINS; i += kPickThreads) hist[i] = 0;
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += kPickThreads) {
-      const uint32_t key = key_at(i);
-      if ((key & st.mask) == st.prefix) atomicAdd(&hist[(key >> shape.shift) & (BINS - 1)], 1u);
+    for (uint32_t base = threadIdx.x; base < n; base += kPickThreads * kLoadBatch) {
+      uint32_t keys[kLoadBatch];
+#pragma unroll
+      for (int u = 0; u < kLoadBatch; ++u) {
+        const uint32_t i = base + u * kPickThreads;
+        keys[u] = i < n ? key_at(i) : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kLoadBatch; ++u)
+        if (base + u * kPickThreads < n && (keys[u] & st.mask) == st.prefix)
+          atomicAdd(&hist[(keys[u] >> shape.shift) & (BINS - 1)], 1u);
     }
     __syncthreads();
     uint32_t digit, below;
@@ -473,16 +496,41 @@ __device__ __forceinline__ void block_select(uint32_t n, uint32_t k, KeyAt key_a
 }
 
 // ---------------------------------------------------------------------------------------
-// Removal sets. One workgroup per segment with a non-zero quota. Each thread owns one
-// contiguous run of the segment, so an ordered (index-order) compaction costs one block scan:
+// Removal sets. One workgroup per segment with a non-zero quota:
 //   raw picks:    key < T, or key == T among the first take_equal such keys in index order;
 //   pooled picks: the same rule against the segment's own pooled threshold (bottom-quota).
 // Writes the raw picks' keys (index order, for the queue), the pooled picks (index order:
 // removal positions ascending, their keys and local indexes for the queue), and the count of
-// pooled picks that are not raw picks. Segments of up to kPickStaged candidates are read from
-// global memory once, with coalesced loads, into LDS keys that every later pass reads; longer
-// segments read global memory in each pass.
+// pooled picks that are not raw picks. The segment's keys go through LDS in chunks of
+// kPickStaged (read with coalesced loads, kLoadBatch per thread in flight); a segment of one
+// chunk is read once for every pass. Within a chunk each thread owns one contiguous run, so the
+// ordered (index-order) compaction costs one block scan per chunk, and the counts of earlier
+// chunks carry over.
 constexpr uint32_t kPickStaged = 4096;
+
+// Keys [c0, c0 + m) of both score arrays of a segment into LDS. All threads call it.
+__device__ __forceinline__ void stage_pick_keys(const float* __restrict__ raw,
+                                                const float* __restrict__ pooled, int64_t begin,
+                                                uint32_t c0, uint32_t m, uint32_t* raw_keys,
+                                                uint32_t* pooled_keys) {
+  for (uint32_t base = threadIdx.x; base < m; base += kPickThreads * kLoadBatch) {
+    float r[kLoadBatch], q[kLoadBatch];
+#pragma unroll
+    for (int u = 0; u < kLoadBatch; ++u) {
+      const uint32_t i = base + u * kPickThreads;
+      r[u] = i < m ? raw[begin + c0 + i] : 0.0f;
+      q[u] = i < m ? pooled[begin + c0 + i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kLoadBatch; ++u) {
+      const uint32_t i = base + u * kPickThreads;
+      if (i < m) {
+        raw_keys[i] = float_key(r[u]);
+        pooled_keys[i] = float_key(q[u]);
+      }
+    }
+  }
+}
 
 __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
     const float* __restrict__ raw, const float* __restrict__ pooled,
@@ -507,72 +555,109 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
   const uint32_t n = static_cast<uint32_t>(end - begin);
   const int64_t offset = offsets[s];
   const int64_t position_start = position_starts[s];
-  const uint32_t per = (n + kPickThreads - 1) / kPickThreads;
-  const uint32_t lo = min(n, threadIdx.x * per), hi = min(n, lo + per);
-  const bool staged = n <= kPickStaged;  // uniform
-  if (staged) {
-    for (uint32_t i = threadIdx.x; i < n; i += kPickThreads) {
-      const float r = raw[begin + i], q = pooled[begin + i];
-      raw_keys[i] = float_key(r);
-      pooled_keys[i] = float_key(q);
-    }
+  const bool single = n <= kPickStaged;  // uniform: one chunk, staged once for every pass
+  if (single) {
+    stage_pick_keys(raw, pooled, begin, 0, n, raw_keys, pooled_keys);
     __syncthreads();
   }
-  auto raw_key = [&](uint32_t i) { return staged ? raw_keys[i] : float_key(raw[begin + i]); };
-  auto pooled_key = [&](uint32_t i) {
-    return staged ? pooled_keys[i] : float_key(pooled[begin + i]);
+  // The thread's run [lo, hi) of a chunk of m keys.
+  auto run_of = [](uint32_t m, uint32_t& lo, uint32_t& hi) {
+    const uint32_t per = (m + kPickThreads - 1) / kPickThreads;
+    lo = min(m, threadIdx.x * per);
+    hi = min(m, lo + per);
   };
 
   // raw picks in index order
   const uint32_t threshold = states[3].prefix, take = take_equal[s];
-  uint32_t raw_seen;  // keys equal to the threshold before this thread's run
   {
-    uint32_t lt = 0, eq = 0;
-    for (uint32_t i = lo; i < hi; ++i) {
-      const uint32_t key = raw_key(i);
-      lt += key < threshold;
-      eq += key == threshold;
-    }
-    uint32_t lt_before, eq_before, lt_total, eq_total;
-    block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
-    uint32_t rank = lt_before + min(take, eq_before);
-    uint32_t seen = eq_before;
-    raw_seen = eq_before;
-    for (uint32_t i = lo; i < hi; ++i) {
-      const uint32_t key = raw_key(i);
-      bool picked = key < threshold;
-      if (key == threshold) picked = seen++ < take;
-      if (picked) run_keys[offset + rank++] = key;
+    uint32_t carry_equal = 0, carry_rank = 0;
+    for (uint32_t c0 = 0; c0 < n; c0 += kPickStaged) {
+      const uint32_t m = min(n - c0, kPickStaged);
+      if (!single) {
+        __syncthreads();  // the previous chunk's readers are done
+        stage_pick_keys(raw, pooled, begin, c0, m, raw_keys, pooled_keys);
+        __syncthreads();
+      }
+      uint32_t lo, hi;
+      run_of(m, lo, hi);
+      uint32_t lt = 0, eq = 0;
+      for (uint32_t i = lo; i < hi; ++i) {
+        const uint32_t key = raw_keys[i];
+        lt += key < threshold;
+        eq += key == threshold;
+      }
+      uint32_t lt_before, eq_before, lt_total, eq_total;
+      block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
+      const uint32_t take_left = take > carry_equal ? take - carry_equal : 0u;
+      uint32_t rank = carry_rank + lt_before + min(take_left, eq_before);
+      uint32_t seen = eq_before;
+      for (uint32_t i = lo; i < hi; ++i) {
+        const uint32_t key = raw_keys[i];
+        bool picked = key < threshold;
+        if (key == threshold) picked = seen++ < take_left;
+        if (picked) run_keys[offset + rank++] = key;
+      }
+      carry_rank += lt_total + min(take_left, eq_total);
+      carry_equal += eq_total;
     }
   }
 
   // pooled picks: bottom-quota of the segment's pooled keys, in index order
   uint32_t pthreshold, ptake;
-  block_select(n, quota, pooled_key, hist, wave_sums, found, pthreshold, ptake);
-  uint32_t lt = 0, eq = 0;
-  for (uint32_t i = lo; i < hi; ++i) {
-    const uint32_t key = pooled_key(i);
-    lt += key < pthreshold;
-    eq += key == pthreshold;
+  if (single) {
+    block_select(n, quota, [&](uint32_t i) { return pooled_keys[i]; }, hist, wave_sums, found,
+                 pthreshold, ptake);
+  } else {
+    block_select(n, quota, [&](uint32_t i) { return float_key(pooled[begin + i]); }, hist,
+                 wave_sums, found, pthreshold, ptake);
   }
-  uint32_t lt_before, eq_before, lt_total, eq_total;
-  block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
-  uint32_t rank = lt_before + min(ptake, eq_before);
-  uint32_t seen = eq_before, moved = 0;
-  for (uint32_t i = lo; i < hi; ++i) {
-    // the raw rule again, in the same order as above, tells whether slot i was a raw pick
-    const uint32_t rkey = raw_key(i);
-    bool raw_picked = rkey < threshold;
-    if (rkey == threshold) raw_picked = raw_seen++ < take;
-    const uint32_t key = pooled_key(i);
-    bool picked = key < pthreshold;
-    if (key == pthreshold) picked = seen++ < ptake;
-    if (picked) {
-      refined_keys[offset + rank] = key;
-      refined_local[offset + rank] = i;
-      removed_positions[offset + rank] = position_start + i;
-      ++rank;
-      moved += raw_picked ? 0u : 1u;
+  uint32_t moved = 0;
+  {
+    uint32_t carry_equal = 0, carry_rank = 0, carry_raw_equal = 0;
+    for (uint32_t c0 = 0; c0 < n; c0 += kPickStaged) {
+      const uint32_t m = min(n - c0, kPickStaged);
+      if (!single) {
+        __syncthreads();
+        stage_pick_keys(raw, pooled, begin, c0, m, raw_keys, pooled_keys);
+        __syncthreads();
+      }
+      uint32_t lo, hi;
+      run_of(m, lo, hi);
+      uint32_t lt = 0, eq = 0, raw_eq = 0;
+      for (uint32_t i = lo; i < hi; ++i) {
+        const uint32_t key = pooled_keys[i];
+        lt += key < pthreshold;
+        eq += key == pthreshold;
+        raw_eq += raw_keys[i] == threshold;
+      }
+      uint32_t lt_before, eq_before, lt_total, eq_total;
+      block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
+      uint32_t raw_eq_before, unused, raw_eq_total, unused_total;
+      block_scan_pair<kPickThreads>(raw_eq, 0u, wave_sums, raw_eq_before, unused, raw_eq_total,
+                                    unused_total);
+      const uint32_t take_left = ptake > carry_equal ? ptake - carry_equal : 0u;
+      const uint32_t raw_take_left = take > carry_raw_equal ? take - carry_raw_equal : 0u;
+      uint32_t rank = carry_rank + lt_before + min(take_left, eq_before);
+      uint32_t seen = eq_before, raw_seen = raw_eq_before;
+      for (uint32_t i = lo; i < hi; ++i) {
+        // the raw rule again, in index order, tells whether slot i was a raw pick
+        const uint32_t rkey = raw_keys[i];
+        bool raw_picked = rkey < threshold;
+        if (rkey == threshold) raw_picked = raw_seen++ < raw_take_left;
+        const uint32_t key = pooled_keys[i];
+        bool picked = key < pthreshold;
+        if (key == pthreshold) picked = seen++ < take_left;
+        if (picked) {
+          refined_keys[offset + rank] = key;
+          refined_local[offset + rank] = c0 + i;
+          removed_positions[offset + rank] = position_start + c0 + i;
+          ++rank;
+          moved += raw_picked ? 0u : 1u;
+        }
+      }
+      carry_rank += lt_total + min(take_left, eq_total);
+      carry_equal += eq_total;
+      carry_raw_equal += raw_eq_total;
     }
   }
   uint32_t moved_before, unused, moved_total, unused_total;

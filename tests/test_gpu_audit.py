@@ -71,6 +71,21 @@ def test_select_matches_oracle(device, ties, fraction):
         np.testing.assert_array_equal(result.quotas.cpu().numpy(), reference.quotas)
 
 
+@pytest.mark.parametrize("fraction", [0.02, 0.3, 0.97])
+def test_select_long_segments_across_chunks(device, fraction):
+    """Segments longer than one LDS chunk of the per-segment pick (4096 candidates: exactly
+    one, one more, several and a ragged last chunk), with many tied values, so the threshold's
+    tie group and the pooled tie group both span chunk boundaries: identical to the oracle."""
+    rng = np.random.default_rng(int(fraction * 100) + 7)
+    lengths = [4096, 4097, 12345, 9000, 33]
+    raw, pooled, ends = tables(rng, lengths, ties=True)
+    starts = rng.integers(0, 40, len(lengths))
+    count = max(1, int(fraction * raw.size))
+    result = run_select(device, raw, pooled, ends, starts, count)
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+    compare(result, expect, ends)
+
+
 def test_select_many_segments_and_side_stream(device):
     """More segments than one plan workgroup covers (1024), runs of 0..60 candidates, and the
     queue half on a side stream: identical to the one-stream call and to the oracle."""
