@@ -106,6 +106,22 @@ __device__ __forceinline__ float logit_fast(float acc, float scale) {
   return bf16_round_fast(bf16_round_fast(acc) * scale);
 }
 
+// What the scorer passes work on. With a power-of-two scale (1/sqrt(d) for d = 64 and 256) the
+// second rounding is exact (bf16(x) * 2^k is a bf16 value), so the passes work on u = bf16(acc)
+// and fold the scale into the constant that converts logits to exp2 arguments: every use is
+// z * log2(e) = u * (scale * log2(e)) with scale * log2(e) exact, in an FMA that rounds once,
+// and max(z) = scale * max(u). One conversion per logit instead of two and a multiply.
+template <bool P2>
+__device__ __forceinline__ float logit_input(float acc, float scale) {
+  if constexpr (P2) return bf16_round_fast(acc);
+  else return logit_fast(acc, scale);
+}
+template <bool P2>
+__device__ __forceinline__ float log2e_per_input(float scale) {
+  if constexpr (P2) return scale * kLog2e;
+  else return kLog2e;
+}
+
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // IEEE 754-2019 minimum / maximum (NaN-propagating, -0 < +0) of three values in one
@@ -377,7 +393,7 @@ __device__ __forceinline__ void dma_rows(const __bf16* matrix, int row0, int las
 // exp(z - m) and op = sum exp(z - m) * pv / S; {NaN x4} for a fully masked row.
 // Three waves per SIMD (at most 168 VGPRs) measure faster here than two without spills for
 // d <= 128; d = 256 runs two (at most 256 VGPRs; its 74 KB of LDS also fit two workgroups per CU).
-template <int D>
+template <int D, bool P2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 3 : 2))) void row_stats_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, float scale, float epsilon,
@@ -461,6 +477,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       kpos_lds[buf][threadIdx.x] = INFINITY;
   };
 
+  // (log2e_per_input is called at each use: a copy held across the loop cost a register at
+  // d = 128 and three waves per SIMD, where the kernel sits at the 168-register limit.)
   float m_run = -INFINITY, S = 0.0f, A = 0.0f;
   // One 64-key stage: 32 logits of this lane (two 32-key tiles, keys acc_key(r, half)).
   auto stage = [&](int buf, auto masked) {
@@ -478,7 +496,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       for (int ks = 0; ks < KS; ++ks)
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], qop[ks], acc, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) z[16 * t + r] = logit_fast(acc[r], scale);
+      for (int r = 0; r < 16; ++r) z[16 * t + r] = logit_input<P2>(acc[r], scale);
     }
     if constexpr (kMask) {
 #pragma unroll
@@ -492,10 +510,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 #pragma unroll
     for (int r = 1; r < 32; ++r) tile_max = fmaxf(tile_max, z[r]);
     const float m_new = fmaxf(m_run, tile_max);
-    const float factor = (m_run == m_new) ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
+    const float factor = (m_run == m_new)
+                             ? 1.0f
+                             : __builtin_amdgcn_exp2f((m_run - m_new) * log2e_per_input<P2>(scale));
     S *= factor;
     A *= factor;
-    const float nml = (m_new == -INFINITY) ? 0.0f : -m_new * kLog2e;
+    const float nml = (m_new == -INFINITY) ? 0.0f : -m_new * log2e_per_input<P2>(scale);
     const float* pv_row = pv_lds[buf] + g * 64;
     // The stage's 32 terms go into partial sums that join the running sums once per stage:
     // a lane's running sums then take one addition per stage instead of one per key, which
@@ -507,7 +527,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
       const f32x4 w = *reinterpret_cast<const f32x4*>(pv_row + 8 * c + 4 * half);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z[4 * c + j], kLog2e, nml));
+        const float e =
+            __builtin_amdgcn_exp2f(__builtin_fmaf(z[4 * c + j], log2e_per_input<P2>(scale), nml));
         s_part += e;
         a_part = __builtin_fmaf(e, w[j], a_part);
       }
@@ -546,11 +567,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
   if (m == -INFINITY) {
     out = make_float4(NAN, NAN, NAN, NAN);
   } else {
-    const float f1 = (m_run == m) ? 1.0f : __builtin_amdgcn_exp2f((m_run - m) * kLog2e);
-    const float f2 = (m_other == m) ? 1.0f : __builtin_amdgcn_exp2f((m_other - m) * kLog2e);
+    const float lg = log2e_per_input<P2>(scale);
+    const float f1 = (m_run == m) ? 1.0f : __builtin_amdgcn_exp2f((m_run - m) * lg);
+    const float f2 = (m_other == m) ? 1.0f : __builtin_amdgcn_exp2f((m_other - m) * lg);
     const float total = S * f1 + S_other * f2;
     const float weighted = A * f1 + A_other * f2;
-    out = make_float4(-m * kLog2e, total, epsilon * total, weighted / total);
+    out = make_float4(-m * lg, total, epsilon * total, weighted / total);
   }
   stats[seg.stats_offset + static_cast<int64_t>(g) * window + query] = out;
 }
@@ -594,7 +616,7 @@ constexpr int column_waves_per_simd() { return column_key_tiles<D>() == 2 ? 2 : 
 template <int D>
 constexpr int column_units_per_stage() { return D == 128 ? 2 : 1; }
 
-template <int D>
+template <int D, bool P2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_waves_per_simd<D>()))) void column_scores_kernel(
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, const float* __restrict__ margin, float scale,
@@ -602,6 +624,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
     float* __restrict__ scores, int* __restrict__ nonfinite) {
   constexpr int KS = D / 16;
   constexpr int KT = column_key_tiles<D>();
+  const float lg = log2e_per_input<P2>(scale);  // logit input -> exp2 argument
   constexpr int kKeys = 4 * 32 * KT;  // candidate keys per workgroup
   constexpr int UP = column_units_per_stage<D>();
   __shared__ __bf16 q_lds[2][UP][32 * D];  // swizzled rows, double-buffered stages of UP units
@@ -793,9 +816,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r = 4 * c + j;
-            float z = logit_fast(acc[t][r], scale);
+            float z = logit_input<P2>(acc[t][r], scale);
             z = kp[j] <= query_position ? z : -INFINITY;
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, kLog2e, st.x));
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, lg, st.x));
             ratio[t][r] = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
           }
         }
@@ -804,7 +827,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(logit_fast(acc[t][r], scale), -kLog2e, -st.x));
+          const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(logit_input<P2>(acc[t][r], scale), -lg, -st.x));
           ratio[t][r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
         }
     }
@@ -951,7 +974,10 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
                  int64_t max_length, int64_t max_candidates, int64_t query_stride,
                  const int64_t* query_positions, const float* margin, float scale, float eps,
                  float4* stats, float* pv, float* scores, int* nonfinite, int stages,
-                 hipStream_t stream) {
+                 bool general_scale, hipStream_t stream) {
+  int scale_exponent = 0;
+  const bool p2 = !general_scale && scale > 0.0f && std::isfinite(scale) &&
+                  std::frexp(scale, &scale_exponent) == 0.5f && scale_exponent > -60;
   if (stages & 1) {
     // about six block steps per block: each block overlaps its next step's loads with the
     // current step's arithmetic (cfg1 shape: 3 blocks per segment, one wave of resident blocks)
@@ -964,16 +990,26 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
   if (stages & 2) {
     const int64_t qtiles = ceil_div(window, 32);
     const int64_t wg_per_segment = ceil_div(groups * qtiles, 4);
-    row_stats_kernel<D><<<static_cast<unsigned>(segments * wg_per_segment), 256, 0, stream>>>(
-        table, groups, window, query_stride, query_positions, scale, eps, wg_per_segment, pv,
-        stats);
+    if (p2)
+      row_stats_kernel<D, true><<<static_cast<unsigned>(segments * wg_per_segment), 256, 0, stream>>>(
+          table, groups, window, query_stride, query_positions, scale, eps, wg_per_segment, pv,
+          stats);
+    else
+      row_stats_kernel<D, false><<<static_cast<unsigned>(segments * wg_per_segment), 256, 0, stream>>>(
+          table, groups, window, query_stride, query_positions, scale, eps, wg_per_segment, pv,
+          stats);
     if (int rc = check_launch("row_stats")) return rc;
   }
   if (stages & 4) {
     const int64_t tiles = ceil_div(max_candidates, 4 * 32 * column_key_tiles<D>());
-    column_scores_kernel<D><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
-        table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
-        scores, nonfinite);
+    if (p2)
+      column_scores_kernel<D, true><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
+          table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
+          scores, nonfinite);
+    else
+      column_scores_kernel<D, false><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
+          table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
+          scores, nonfinite);
     if (int rc = check_launch("column_scores")) return rc;
   }
   return LR_OK;
@@ -1007,7 +1043,7 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
              "Invalid candidate interval");
   LR_REQUIRE(query_group_stride >= window, "Invalid query layout");
   LR_REQUIRE(epsilon > 0.0, "Chunk size and denominator epsilon must be positive");
-  LR_REQUIRE(stages >= 0 && stages <= 7, "stages is a bitmask of 1 | 2 | 4");
+  LR_REQUIRE(stages >= 0 && stages <= 15, "stages is a bitmask of 1 | 2 | 4 (| 8)");
   LR_REQUIRE(segment_table && query_positions && margin && workspace && scores,
              "Expected contiguous CUDA tensor");
   LR_REQUIRE(segments * ceil_div(max_candidates, kTileKeys) < (int64_t{1} << 31),
@@ -1021,19 +1057,21 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
   float* pv = reinterpret_cast<float*>(static_cast<char*>(workspace) + stats_bytes);
   const hipStream_t s = as_stream(stream);
   const float eps = static_cast<float>(epsilon);
+  const bool general_scale = (stages & 8) != 0;
+  const int run = (stages & 7) == 0 ? 7 : (stages & 7);
   switch (dim) {
     case 64:
       return launch_score<64>(segment_table, segments, groups, window, max_length, max_candidates,
                               query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                              scores, nonfinite, stages == 0 ? 7 : stages, s);
+                              scores, nonfinite, run, general_scale, s);
     case 128:
       return launch_score<128>(segment_table, segments, groups, window, max_length, max_candidates,
                                query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                               scores, nonfinite, stages == 0 ? 7 : stages, s);
+                               scores, nonfinite, run, general_scale, s);
     default:
       return launch_score<256>(segment_table, segments, groups, window, max_length, max_candidates,
                                query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                               scores, nonfinite, stages == 0 ? 7 : stages, s);
+                               scores, nonfinite, run, general_scale, s);
   }
 }
 

@@ -209,7 +209,9 @@ size_t lr_score_workspace_bytes(int64_t segments, int64_t groups, int64_t window
  * refuse a table (src/lazy_recall/scoring.py:292-293) without a separate reduction.
  * stages: 0 (or 7) runs the whole scorer; otherwise a bitmask of 1 = projected values,
  * 2 = row statistics, 4 = column scores, run in that order (for per-kernel timing; each stage
- * needs the earlier ones to have run on the same workspace). */
+ * needs the earlier ones to have run on the same workspace). With a power-of-two scale
+ * (1/sqrt(dim) for dim 64 and 256) the passes skip the second bf16 rounding, which is exact
+ * there; bit 8 of stages (a test hook) keeps the general form, whose scores are the same. */
 int lr_score_segments(const int64_t* segment_table, int64_t segments, int64_t groups,
                       int64_t window, int64_t dim, int64_t max_length, int64_t max_candidates,
                       int64_t query_group_stride, const int64_t* query_positions,

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from code_for_iclr27_amd import _C, _legacy_C, scoring, workloads
+from code_for_iclr27_amd import _C, _legacy_C, _lib, scoring, workloads
 from oracle import bf16 as obf16
 from oracle import scoring as oscoring
 
@@ -143,6 +143,42 @@ def test_fused_scorer_matches_oracle(device, dim, groups, window):
                                    err_msg=f"segment {segment} layer {seg.layer} head {seg.head}")
         offset += seg.count
     assert offset == scores.size
+
+
+def _scores_with_stages(plan, qpos, margin, stages, device):
+    segments = plan.segment_count
+    nbytes = _lib.load().lr_score_workspace_bytes(segments, plan.groups, plan.window,
+                                                  segments * plan.groups * plan.max_length)
+    table = plan.part("table").to(device)
+    workspace = torch.empty((nbytes,), dtype=torch.uint8, device=device)
+    scores = torch.full((plan.total,), -1.0, dtype=torch.float32, device=device)
+    _lib.call("lr_score_segments", table.data_ptr(), segments, plan.groups, plan.window,
+              plan.dim, plan.max_length, plan.max_candidates, plan.query_stride,
+              qpos.data_ptr(), margin.data_ptr(), float(1.0 / math.sqrt(plan.dim)), 1e-6,
+              workspace.data_ptr(), nbytes, scores.data_ptr(), None, stages,
+              torch.cuda.current_stream(device).cuda_stream)
+    torch.cuda.synchronize(device)
+    return to_np(scores)
+
+
+@pytest.mark.parametrize("dim,groups,window", [(64, 4, 250), (256, 6, 77), (256, 6, 512), (128, 4, 90)])
+def test_power_of_two_scale_path_equals_general_form(device, dim, groups, window):
+    """For d = 64 and 256 the scale 1/sqrt(d) is a power of two: the passes then skip the second
+    bf16 rounding of each logit and fold the scale into the exp2 constant. That is exact, so
+    the scores must equal, bit for bit, those of the general form (stages bit 8 forces it),
+    including masked keys (some keys after every query) and NaN rows. d = 128 takes the
+    general form either way."""
+    head_lengths = [[700, 41, 680, 300], [170, 900, 33, 299]]
+    layers, qpos = workloads.make_layers(head_lengths, groups, dim, window, device, seed=dim + window,
+                                         gradient="lognormal")
+    layers[0].positions[50:70] += 1.0e5   # head 0 of layer 0: keys after every query
+    layers[1].queries.mul_(3.0)            # larger logits: more of them far from the row max
+    plan = scoring.plan_segments(layers, protect_prompt=True, protect_recent=32)
+    margin = torch.tensor([2.0], device=device)
+    fast = _scores_with_stages(plan, qpos, margin, 0, device)
+    general = _scores_with_stages(plan, qpos, margin, 8, device)
+    assert np.isfinite(fast).mean() > 0.5
+    np.testing.assert_array_equal(fast, general)
 
 
 def test_fused_scorer_matches_reference_host_path(device):
