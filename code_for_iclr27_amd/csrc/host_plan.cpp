@@ -757,13 +757,22 @@ py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
   const int64_t slots = static_cast<int64_t>(layers) * heads;
   std::vector<int64_t> counts(static_cast<size_t>(slots), 0);
   const int64_t* meta = metadata.data_ptr<int64_t>();
+  // One pass checks and counts the identities and notes whether they already come grouped by
+  // slot in slot order (a transport batch does), which turns the grouping below into a copy.
+  bool grouped = true;
+  int64_t previous_slot = 0;
+  bool valid = true;
   for (int64_t i = 0; i < count; ++i) {
     const int64_t layer = meta[3 * i], head = meta[3 * i + 1], position = meta[3 * i + 2];
-    require(layer >= 0 && layer < static_cast<int64_t>(layers) && head >= 0 && head < heads &&
-                position >= 0 && position < (int64_t{1} << 31),
-            "Invalid recall identity");
-    ++counts[layer * heads + head];
+    valid &= layer >= 0 && layer < static_cast<int64_t>(layers) && head >= 0 && head < heads &&
+             position >= 0 && position < (int64_t{1} << 31);
+    if (!valid) break;
+    const int64_t slot = layer * heads + head;
+    grouped &= slot >= previous_slot;
+    previous_slot = slot;
+    ++counts[slot];
   }
+  require(valid, "Invalid recall identity");
   const torch::Tensor& k0 = keys[0];
   require(k0.dim() == 2 && k0.size(1) > 0, "Invalid KV layout");
   const int64_t dim = k0.size(1);
@@ -825,12 +834,19 @@ py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
   // group by slot: entry i goes to the next place of its slot's run
   int64_t* grouped_position = table + slots * LR_REINSERT_WORDS;
   int64_t* grouped_source = grouped_position + count;
-  std::vector<int64_t> cursor(static_cast<size_t>(slots));
-  for (int64_t slot = 0; slot < slots; ++slot) cursor[slot] = table[slot * LR_REINSERT_WORDS + 4];
-  for (int64_t i = 0; i < count; ++i) {
-    const int64_t at = cursor[meta[3 * i] * heads + meta[3 * i + 1]]++;
-    grouped_position[at] = meta[3 * i + 2];
-    grouped_source[at] = i;
+  if (grouped) {  // already in slot order: entry i stays at i
+    for (int64_t i = 0; i < count; ++i) {
+      grouped_position[i] = meta[3 * i + 2];
+      grouped_source[i] = i;
+    }
+  } else {
+    std::vector<int64_t> cursor(static_cast<size_t>(slots));
+    for (int64_t slot = 0; slot < slots; ++slot) cursor[slot] = table[slot * LR_REINSERT_WORDS + 4];
+    for (int64_t i = 0; i < count; ++i) {
+      const int64_t at = cursor[meta[3 * i] * heads + meta[3 * i + 1]]++;
+      grouped_position[at] = meta[3 * i + 2];
+      grouped_source[at] = i;
+    }
   }
   return py::make_tuple(block, new_lens, offsets, out_row, max_length);
 }

@@ -69,11 +69,17 @@ def check(outcome, layers, payload, meta):
             assert recalled_rows[rows[local]] == out_row - bounds[head]
 
 
-@pytest.mark.parametrize("on_device", [False, True])
-def test_reinsert_matches_merge_plan(device, on_device):
+@pytest.mark.parametrize("on_device,grouped", [(False, False), (True, False), (False, True)])
+def test_reinsert_matches_merge_plan(device, on_device, grouped):
+    """Identities in any order, or already grouped by (layer, head) in slot order (the host
+    planner then copies instead of scattering them), with empty slots and a layer without
+    recalls."""
     head_lengths = [[300, 41, 280, 1], [170, 300, 33, 299], [64, 200, 310, 90]]
     layers, payload, meta = make_case(device, head_lengths, [17, 0, 5, 129, 1], 128, seed=3,
                                       skip_layer=1)
+    if grouped:
+        order = np.argsort(meta[:, 0] * 4 + meta[:, 1], kind="stable")
+        meta, payload = meta[order], payload[torch.from_numpy(order)]
     source = payload.to(device) if on_device else payload.pin_memory()
     outcome = reinsert.Reinserter().run(layers, source, meta)
     torch.cuda.synchronize()
