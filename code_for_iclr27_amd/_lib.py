@@ -62,6 +62,8 @@ SIGNATURES = {
                          _P],
     "lr_select_refine_sets": [_P, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P,
                               _P],
+    "lr_pool_select_refine_sets": [_P, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _SZ, _P,
+                                   _P, _P, _P, _P, _P, _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
     "lr_reinsert_plan": [_P, _I64, _P, _I64, _P, _P, _P, _P],

@@ -50,7 +50,8 @@ def _native_planner():
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_library(address("lr_score_workspace_bytes"), address("lr_score_segments"),
                              address("lr_pool"), address("lr_select_workspace_bytes"),
-                             address("lr_select_refine_sets"), address("lr_select_refine_queue"),
+                             address("lr_pool_select_refine_sets"),
+                             address("lr_select_refine_queue"),
                              address("lr_queue_index"), address("lr_queue_evict_plan"),
                              address("lr_compact_heads"), address("lr_last_error"),
                              address("lr_staging_alloc"), address("lr_staging_free"),

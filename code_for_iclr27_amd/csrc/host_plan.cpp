@@ -225,7 +225,7 @@ struct Library {
   decltype(&lr_score_segments) score_segments = nullptr;
   decltype(&lr_pool) pool = nullptr;
   decltype(&lr_select_workspace_bytes) select_workspace_bytes = nullptr;
-  decltype(&lr_select_refine_sets) select_refine_sets = nullptr;
+  decltype(&lr_pool_select_refine_sets) pool_select_refine_sets = nullptr;
   decltype(&lr_select_refine_queue) select_refine_queue = nullptr;
   decltype(&lr_queue_index) queue_index = nullptr;
   decltype(&lr_queue_evict_plan) queue_evict_plan = nullptr;
@@ -249,7 +249,7 @@ void bind_one(F& slot, int64_t address) {
 }
 
 void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t pool,
-                  int64_t select_workspace_bytes, int64_t select_refine_sets,
+                  int64_t select_workspace_bytes, int64_t pool_select_refine_sets,
                   int64_t select_refine_queue, int64_t queue_index, int64_t queue_evict_plan,
                   int64_t compact_heads, int64_t last_error, int64_t staging_alloc,
                   int64_t staging_free, int64_t copy_words) {
@@ -257,7 +257,7 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
   bind_one(library.score_segments, score_segments);
   bind_one(library.pool, pool);
   bind_one(library.select_workspace_bytes, select_workspace_bytes);
-  bind_one(library.select_refine_sets, select_refine_sets);
+  bind_one(library.pool_select_refine_sets, pool_select_refine_sets);
   bind_one(library.select_refine_queue, select_refine_queue);
   bind_one(library.queue_index, queue_index);
   bind_one(library.queue_evict_plan, queue_evict_plan);
@@ -494,9 +494,13 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
         dptr(score_ws), score_bytes, raw, nonfinite, timed ? 1 << i : 7, stream));
     stage(timed ? kScoreStages[i] : "score");
   }
-  check_call(library.pool(raw, plan.total, words + plan.bounds_at(), S, plan.max_candidates,
-                          pool_kernel, pooled, stream));
-  stage("pool");
+  // With a selection to make, the pool runs inside lr_pool_select_refine_sets (its launch also
+  // resets the selection's counters); the "select" stage then covers both.
+  if (count <= 0) {
+    check_call(library.pool(raw, plan.total, words + plan.bounds_at(), S, plan.max_candidates,
+                            pool_kernel, pooled, stream));
+    stage("pool");
+  }
 
   // The lazy form: only the queue's first `immediate` slots leave now, the rest stay queued
   // (controller.py:148-158). It needs the queue order before the compaction.
@@ -524,10 +528,11 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
     queue_rank = torch::empty({count}, on_device.dtype(torch::kInt32));
     batch = torch::empty({count + S}, on_device.dtype(torch::kInt64));
     int64_t* host = sync != nullptr ? sync->info_buffer(S + 1) : nullptr;
-    check_call(library.select_refine_sets(
-        raw, pooled, plan.total, words + plan.ends_at(), words + plan.starts_at(), S, count,
-        dptr(select_ws), select_bytes, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
-        removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(), host, nonfinite, stream));
+    check_call(library.pool_select_refine_sets(
+        raw, plan.total, words + plan.bounds_at(), plan.max_candidates, pool_kernel, pooled,
+        words + plan.ends_at(), words + plan.starts_at(), S, count, dptr(select_ws), select_bytes,
+        quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(), removed.data_ptr<int64_t>(),
+        changed.data_ptr<int64_t>(), host, nonfinite, stream));
     int64_t* queue_segments = queue_order.data_ptr<int64_t>();
     int64_t* queue_positions = queue_segments + count;
     check_call(library.select_refine_queue(
@@ -563,11 +568,12 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
     removed = sets.narrow(0, 0, count);
     offsets = sets.narrow(0, count, S + 1);
     changed = sets.narrow(0, count + S + 1, S);
-    check_call(library.select_refine_sets(
-        raw, pooled, plan.total, words + plan.ends_at(), words + plan.starts_at(), S, count,
-        dptr(select_ws), select_bytes, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
-        removed.data_ptr<int64_t>(), changed.data_ptr<int64_t>(),
-        sync != nullptr ? sync->info_buffer(S + 1) : nullptr, nonfinite, stream));
+    check_call(library.pool_select_refine_sets(
+        raw, plan.total, words + plan.bounds_at(), plan.max_candidates, pool_kernel, pooled,
+        words + plan.ends_at(), words + plan.starts_at(), S, count, dptr(select_ws), select_bytes,
+        quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(), removed.data_ptr<int64_t>(),
+        changed.data_ptr<int64_t>(), sync != nullptr ? sync->info_buffer(S + 1) : nullptr,
+        nonfinite, stream));
     stage("select");
     if (sync != nullptr) sync->post(plan, device);
     check_call(library.compact_heads(

@@ -25,6 +25,13 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Launches never exceed this many blocks in x; kernels grid-stride beyond it.
 constexpr int64_t kMaxGridX = 1 << 30;
 
+// Sliding-max pool of every segment (temporal.hip), arguments checked by the caller. With
+// `clear` given, the launch also zeroes clear[0, clear_words) before any later launch on the
+// stream starts.
+int launch_pool(const float* scores, int64_t total, const int64_t* bounds, int64_t segments,
+                int64_t max_count, int64_t width, float* out, uint32_t* clear, int clear_words,
+                hipStream_t stream);
+
 }  // namespace lr
 
 #define LR_REQUIRE(cond, message)      \

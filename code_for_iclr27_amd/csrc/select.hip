@@ -279,8 +279,13 @@ __device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t remain
 // one global histogram with atomics. The next kernel finds pass p's digit itself, in every
 // workgroup (a scan of 2048 bins), so no launch is spent on reductions. states[p] is the
 // selection state before pass p; only workgroup 0 of the kernel that derives it writes it.
+// Passes 0 and 1 are kernels of their own; the last pass runs inside the per-segment counting
+// (segment_count_kernel). The three histograms and the ticket counter are one block of
+// kClearWords words that must be zero before pass 0: select_clear_kernel zeroes it, or the
+// pool launch of lr_pool_select_refine_sets does.
 constexpr int kHistBlocks = 256;
 constexpr int kHistStride = 2048;  // words per pass histogram
+constexpr int kClearWords = 3 * kHistStride + 1;  // histograms, then the ticket
 
 struct PassShape {
   int bits, shift;
@@ -289,17 +294,8 @@ __host__ __device__ constexpr PassShape pass_shape(int pass) {
   return pass == 0 ? PassShape{11, 21} : pass == 1 ? PassShape{11, 10} : PassShape{10, 0};
 }
 
-__global__ __launch_bounds__(256) void select_init_kernel(SelectState* __restrict__ states,
-                                                          uint32_t* __restrict__ hist,
-                                                          uint32_t* __restrict__ ticket,
-                                                          uint32_t count) {
-  for (int i = threadIdx.x; i < 3 * kHistStride; i += 256) hist[i] = 0;
-  if (threadIdx.x == 0) {
-    SelectState st{};
-    st.remaining = count;
-    states[0] = st;
-    *ticket = 0;
-  }
+__global__ __launch_bounds__(256) void select_clear_kernel(uint32_t* __restrict__ words) {
+  for (int i = threadIdx.x; i < kClearWords; i += 256) words[i] = 0;
 }
 
 // Extends `st` (the state before pass `pass`) by that pass's digit, read from its histogram.
@@ -321,18 +317,22 @@ __device__ __forceinline__ SelectState extend_state(SelectState st, const uint32
 template <int PASS>
 __global__ __launch_bounds__(256) void select_pass_kernel(const float* __restrict__ scores,
                                                           int64_t n, int64_t chunk,
+                                                          uint32_t count,
                                                           SelectState* __restrict__ states,
                                                           uint32_t* __restrict__ hist) {
+  static_assert(PASS == 0 || PASS == 1, "the last pass runs in segment_count_kernel");
   constexpr PassShape shape = pass_shape(PASS);
   constexpr int BINS = 1 << shape.bits;
   __shared__ uint32_t local[BINS];
   __shared__ uint32_t wave_sums[4][2];
   __shared__ uint32_t found[2];
-  SelectState st = states[PASS == 0 ? 0 : PASS - 1];
-  if constexpr (PASS > 0) {
-    st = extend_state<PASS - 1, 256>(st, hist, wave_sums, found);
-    if (blockIdx.x == 0 && threadIdx.x == 0) states[PASS] = st;
+  SelectState st{};
+  if constexpr (PASS == 0) {
+    st.remaining = count;  // nothing fixed yet: the count-th smallest of all keys
+  } else {
+    st = extend_state<PASS - 1, 256>(states[PASS - 1], hist, wave_sums, found);
   }
+  if (blockIdx.x == 0 && threadIdx.x == 0) states[PASS] = st;
   for (int i = threadIdx.x; i < BINS; i += 256) local[i] = 0;
   __syncthreads();
   const uint32_t prefix = st.prefix, mask = st.mask;
@@ -374,28 +374,42 @@ __global__ __launch_bounds__(256) void select_pass_kernel(const float* __restric
   }
 }
 
-// Per segment: how many raw keys are below / equal to the global threshold. Every workgroup
-// first finishes the threshold from the last pass histogram; workgroup 0 publishes it as
-// states[3] = {threshold, all-ones mask, threshold-equal keys to take, keys below}. The last
-// workgroup to finish (a ticket counter, no waiting) then plans the per-segment quotas: the
-// threshold-equal keys are granted in index order, i.e. segment order, and the quotas' exclusive
-// prefix gives each segment's offset.
+// Per segment: how many raw keys lie below / at the global threshold, with the threshold's
+// last digit found on the way. Every workgroup derives the threshold's 22-bit prefix from the
+// second pass histogram (workgroup 0 publishes it as states[2]), counts its segment's keys
+// below that prefix and histograms, in LDS, the last 10 bits of the keys that share it. A
+// workgroup whose segment holds such keys adds them to the last pass histogram and keeps that
+// LDS histogram's exclusive prefix in its row of `low_prefix` (kLowRow words). The last
+// workgroup to finish (a ticket counter, no waiting) finds the last digit from the complete
+// histogram, publishes states[3] = {threshold, all-ones mask, threshold-equal keys to take, keys
+// below}, turns every segment's counts into keys below / equal to the threshold, and plans the
+// per-segment quotas: the threshold-equal keys are granted in index order, i.e. segment order,
+// and the quotas' exclusive prefix gives each segment's offset.
+constexpr int kLowBins = 1 << pass_shape(2).bits;
+constexpr int kLowRow = kLowBins + 1;  // exclusive prefix of the LDS histogram, then its total
+
 __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
     const float* __restrict__ scores, const int64_t* __restrict__ ends,
-    SelectState* __restrict__ states, const uint32_t* __restrict__ hist,
+    SelectState* __restrict__ states, uint32_t* __restrict__ hist,
     uint32_t* __restrict__ seg_less, uint32_t* __restrict__ seg_equal,
-    uint32_t* __restrict__ ticket, int64_t segments, uint32_t* __restrict__ take_equal,
-    int64_t* __restrict__ quotas, int64_t* __restrict__ offsets, int64_t* __restrict__ host_info,
-    const int32_t* __restrict__ nonfinite) {
+    uint32_t* __restrict__ low_prefix, uint32_t* __restrict__ ticket, int64_t segments,
+    uint32_t* __restrict__ take_equal, int64_t* __restrict__ quotas, int64_t* __restrict__ offsets,
+    int64_t* __restrict__ host_info, const int32_t* __restrict__ nonfinite) {
+  constexpr int PER = kLowBins / kSegThreads;
+  static_assert(kLowBins % kSegThreads == 0, "low bins per thread");
   __shared__ uint32_t wave_sums[kSegThreads / 64][2];
   __shared__ uint32_t found[2];
+  __shared__ uint32_t low[kLowBins];
   __shared__ bool last;
-  const SelectState st = extend_state<2, kSegThreads>(states[2], hist, wave_sums, found);
-  if (blockIdx.x == 0 && threadIdx.x == 0) states[3] = st;
+  for (int i = threadIdx.x; i < kLowBins; i += kSegThreads) low[i] = 0;
+  // (extend_state ends with a barrier, which also publishes the zeroed histogram)
+  const SelectState st = extend_state<1, kSegThreads>(states[1], hist, wave_sums, found);
+  if (blockIdx.x == 0 && threadIdx.x == 0) states[2] = st;
   const int64_t s = blockIdx.x;
   const int64_t begin = s == 0 ? 0 : ends[s - 1], end = ends[s];
-  const uint32_t threshold = st.prefix;
-  uint32_t less = 0, equal = 0;
+  // st.prefix has its last 10 bits clear: key < st.prefix exactly when the key's first 22 bits
+  // lie below the threshold's
+  uint32_t less = 0, matched = 0;
   // kLoadBatch loads per thread in flight at once (a loop of single loads pays the memory
   // latency once per element)
   for (int64_t base = begin + threadIdx.x; base < end; base += kSegThreads * kLoadBatch) {
@@ -409,33 +423,71 @@ __global__ __launch_bounds__(kSegThreads) void segment_count_kernel(
     for (int u = 0; u < kLoadBatch; ++u) {
       if (base + u * kSegThreads < end) {
         const uint32_t key = float_key(v[u]);
-        less += key < threshold;
-        equal += key == threshold;
+        less += key < st.prefix;
+        if ((key & st.mask) == st.prefix) {
+          ++matched;
+          atomicAdd(&low[key & (kLowBins - 1)], 1u);
+        }
       }
     }
   }
-  uint32_t bl, be, total_less, total_equal;
-  block_scan_pair<kSegThreads>(less, equal, wave_sums, bl, be, total_less, total_equal);
+  uint32_t bl, bm, total_less, total_matched;
+  block_scan_pair<kSegThreads>(less, matched, wave_sums, bl, bm, total_less, total_matched);
+  if (total_matched != 0) {  // uniform; the scan's barriers published the LDS histogram
+    uint32_t c[PER], sum = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      c[j] = low[threadIdx.x * PER + j];
+      sum += c[j];
+      if (c[j] != 0) atomicAdd(&hist[2 * kHistStride + threadIdx.x * PER + j], c[j]);
+    }
+    uint32_t before, unused_b, unused_total, unused_t;
+    block_scan_pair<kSegThreads>(sum, 0u, wave_sums, before, unused_b, unused_total, unused_t);
+    uint32_t* row = low_prefix + s * kLowRow;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      row[threadIdx.x * PER + j] = before;
+      before += c[j];
+    }
+    if (threadIdx.x == kSegThreads - 1) row[kLowBins] = before;
+  }
+  // The workgroup barrier orders every wave's histogram additions and row stores before wave
+  // 0's device-scope release fence, which makes them visible device-wide before the ticket is
+  // taken. One release per workgroup (it writes back the XCD's L2); only the last workgroup
+  // acquires (which invalidates its XCD's L2), so the others' cached inputs survive.
+  __syncthreads();
   if (threadIdx.x == 0) {
     seg_less[s] = total_less;
-    seg_equal[s] = total_equal;
-    __threadfence();  // the counts are visible device-wide before the ticket is taken
+    seg_equal[s] = total_matched;  // non-zero exactly when the segment's row was written
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     last = atomicAdd(ticket, 1u) == gridDim.x - 1;
   }
   __syncthreads();
   if (!last) return;  // uniform across the workgroup
-  __threadfence();
-  const uint32_t need = st.remaining;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const SelectState fin = extend_state<2, kSegThreads>(st, hist, wave_sums, found);
+  if (threadIdx.x == 0) states[3] = fin;
+  const uint32_t digit = fin.prefix & (kLowBins - 1);
+  const uint32_t need = fin.remaining;
   uint32_t carry_equal = 0, carry_quota = 0;
   for (int64_t base = 0; base < segments; base += kSegThreads) {
     const int64_t t = base + threadIdx.x;
-    const uint32_t eq = t < segments ? seg_equal[t] : 0;
+    uint32_t lt = 0, eq = 0;
+    if (t < segments) {
+      lt = seg_less[t];
+      if (seg_equal[t] != 0) {
+        const uint32_t* row = low_prefix + t * kLowRow;
+        const uint32_t below = row[digit], through = row[digit + 1];
+        lt += below;
+        eq = through - below;
+      }
+    }
     uint32_t eq_before, unused, eq_total, unused_total;
     block_scan_pair<kSegThreads>(eq, 0u, wave_sums, eq_before, unused, eq_total, unused_total);
     eq_before += carry_equal;
     uint32_t take = 0;
     if (need > eq_before) take = need - eq_before < eq ? need - eq_before : eq;
-    const uint32_t quota = t < segments ? seg_less[t] + take : 0;
+    const uint32_t quota = t < segments ? lt + take : 0;
     uint32_t quota_before, quota_total;
     block_scan_pair<kSegThreads>(quota, 0u, wave_sums, quota_before, unused, quota_total, unused_total);
     quota_before += carry_quota;
@@ -768,10 +820,11 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
 
 struct SelectWorkspace {
   SelectState* states;  // [4]: before each threshold pass, then final
-  uint32_t* hist;       // [3][kHistStride]
+  uint32_t* hist;       // [3][kHistStride], then the ticket: kClearWords words zeroed per call
   uint32_t* ticket;     // workgroups of segment_count that have finished
   uint32_t* seg_less;
   uint32_t* seg_equal;
+  uint32_t* low_prefix;  // [segments][kLowRow]
   uint32_t* take_equal;
   uint32_t *run_keys, *run_slots, *refined_keys, *refined_local, *tmp_keys, *tmp_values;
   void* sort_storage;  // rocPRIM's temporary storage for the global order
@@ -789,10 +842,11 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
     return r;
   };
   w.states = reinterpret_cast<SelectState*>(take(4 * sizeof(SelectState)));
-  w.hist = reinterpret_cast<uint32_t*>(take(size_t{3} * kHistStride * 4));
-  w.ticket = reinterpret_cast<uint32_t*>(take(4));
+  w.hist = reinterpret_cast<uint32_t*>(take(size_t{kClearWords} * 4));
+  w.ticket = w.hist == nullptr ? nullptr : w.hist + 3 * kHistStride;
   w.seg_less = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.seg_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
+  w.low_prefix = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(segments) * kLowRow * 4));
   w.take_equal = reinterpret_cast<uint32_t*>(take(segments * 4));
   w.run_keys = reinterpret_cast<uint32_t*>(take(count * 4));
   w.run_slots = reinterpret_cast<uint32_t*>(take(count * 4));
@@ -806,23 +860,26 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
   return w;
 }
 
+// `cleared`: the caller's launch on the same stream has already zeroed w.hist[0, kClearWords).
 int launch_sets(const float* raw, const float* pooled, int64_t total, const int64_t* segment_ends,
                 const int64_t* position_starts, int64_t segments, int64_t count,
                 const SelectWorkspace& w, int64_t* quotas, int64_t* offsets,
                 int64_t* removed_positions, int64_t* changed, int64_t* host_info,
-                const int32_t* nonfinite, hipStream_t s) {
-  select_init_kernel<<<1, 256, 0, s>>>(w.states, w.hist, w.ticket, static_cast<uint32_t>(count));
-  if (int rc = check_launch("select_init")) return rc;
+                const int32_t* nonfinite, bool cleared, hipStream_t s) {
+  if (!cleared) {
+    select_clear_kernel<<<1, 256, 0, s>>>(w.hist);
+    if (int rc = check_launch("select_clear")) return rc;
+  }
   const int64_t chunk = ceil_div(ceil_div(total, kHistBlocks), 1024) * 1024;
   const int blocks = static_cast<int>(ceil_div(total, chunk));
-  select_pass_kernel<0><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
-  select_pass_kernel<1><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
-  select_pass_kernel<2><<<blocks, 256, 0, s>>>(raw, total, chunk, w.states, w.hist);
+  const uint32_t k = static_cast<uint32_t>(count);
+  select_pass_kernel<0><<<blocks, 256, 0, s>>>(raw, total, chunk, k, w.states, w.hist);
+  select_pass_kernel<1><<<blocks, 256, 0, s>>>(raw, total, chunk, k, w.states, w.hist);
   if (int rc = check_launch("select_pass")) return rc;
   segment_count_kernel<<<segments, kSegThreads, 0, s>>>(raw, segment_ends, w.states, w.hist,
-                                                        w.seg_less, w.seg_equal, w.ticket,
-                                                        segments, w.take_equal, quotas, offsets,
-                                                        host_info, nonfinite);
+                                                        w.seg_less, w.seg_equal, w.low_prefix,
+                                                        w.ticket, segments, w.take_equal, quotas,
+                                                        offsets, host_info, nonfinite);
   if (int rc = check_launch("segment_count")) return rc;
   segment_pick_kernel<<<segments, kPickThreads, 0, s>>>(
       raw, pooled, segment_ends, position_starts, w.states, w.take_equal, quotas, offsets,
@@ -884,7 +941,35 @@ extern "C" int lr_select_refine_sets(const float* raw, const float* pooled, int6
   const SelectWorkspace w = carve(workspace, total, segments, count);
   LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
   return launch_sets(raw, pooled, total, segment_ends, position_starts, segments, count, w, quotas,
-                     offsets, removed_positions, changed, host_info, nonfinite, as_stream(stream));
+                     offsets, removed_positions, changed, host_info, nonfinite, false,
+                     as_stream(stream));
+}
+
+extern "C" int lr_pool_select_refine_sets(const float* raw, int64_t total, const int64_t* bounds,
+                                          int64_t max_count, int64_t width, float* pooled,
+                                          const int64_t* segment_ends,
+                                          const int64_t* position_starts, int64_t segments,
+                                          int64_t count, void* workspace, size_t workspace_bytes,
+                                          int64_t* quotas, int64_t* offsets,
+                                          int64_t* removed_positions, int64_t* changed,
+                                          int64_t* host_info, const int32_t* nonfinite,
+                                          void* stream) {
+  clear_error();
+  LR_SELECT_CHECK_SHAPE();
+  LR_REQUIRE(width > 0 && width % 2 == 1 && max_count > 0, "Invalid pool configuration");
+  LR_REQUIRE(segments <= 65535, "Invalid pool layout");
+  LR_REQUIRE(raw && bounds && pooled && segment_ends && position_starts && workspace && quotas &&
+                 offsets && removed_positions && changed,
+             "Expected contiguous CUDA tensor");
+  LR_REQUIRE((reinterpret_cast<uintptr_t>(raw) & 15) == 0, "Score table must be 16-byte aligned");
+  const SelectWorkspace w = carve(workspace, total, segments, count);
+  LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
+  const hipStream_t s = as_stream(stream);
+  if (int rc = launch_pool(raw, total, bounds, segments, max_count, width, pooled, w.hist,
+                           kClearWords, s))
+    return rc;
+  return launch_sets(raw, pooled, total, segment_ends, position_starts, segments, count, w,
+                     quotas, offsets, removed_positions, changed, host_info, nonfinite, true, s);
 }
 
 extern "C" int lr_select_refine_queue(const int64_t* position_starts, int64_t total,

@@ -192,14 +192,20 @@ __global__ __launch_bounds__(kRiskCandidates* kRiskQueryLanes) void risk_kernel(
 
 // Sliding max of odd width inside each segment; NaN neighbours are ignored as by fmaxf and
 // out-of-segment neighbours do not exist (csrc/scoring.cu:190-203). Block tile + halo in LDS.
+// Workgroup (0, 0) also zeroes `clear[0, clear_words)` when given (the selection's counters, so
+// that a following selection needs no launch of its own to reset them).
 constexpr int kPoolThreads = 256;
 
 __global__ __launch_bounds__(kPoolThreads) void pool_kernel(const float* __restrict__ scores,
                                                              int64_t total,
                                                              const int64_t* __restrict__ bounds,
                                                              float* __restrict__ output,
-                                                             int half, int use_lds) {
+                                                             int half, int use_lds,
+                                                             uint32_t* __restrict__ clear,
+                                                             int clear_words) {
   extern __shared__ float tile[];
+  if (clear != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = threadIdx.x; i < clear_words; i += kPoolThreads) clear[i] = 0;
   const int64_t segment = blockIdx.y;
   int64_t begin = bounds[segment], end = bounds[segment + 1];
   if (begin < 0) begin = 0;
@@ -349,6 +355,23 @@ extern "C" int lr_temporal_risk(const float* probabilities, const float* output_
   return check_launch("temporal_risk");
 }
 
+namespace lr {
+
+int launch_pool(const float* scores, int64_t total, const int64_t* bounds, int64_t segments,
+                int64_t max_count, int64_t width, float* out, uint32_t* clear, int clear_words,
+                hipStream_t stream) {
+  const int half = static_cast<int>(width / 2);
+  const int use_lds = width <= 4097 ? 1 : 0;
+  const size_t lds = use_lds ? (kPoolThreads + 2 * half) * sizeof(float) : 0;
+  dim3 grid(static_cast<unsigned>(ceil_div(max_count, kPoolThreads)),
+            static_cast<unsigned>(segments));
+  pool_kernel<<<grid, kPoolThreads, lds, stream>>>(scores, total, bounds, out, half, use_lds,
+                                                   clear, clear_words);
+  return check_launch("pool");
+}
+
+}  // namespace lr
+
 extern "C" int lr_pool(const float* scores, int64_t total, const int64_t* bounds,
                        int64_t segments, int64_t max_count, int64_t width, float* out,
                        void* stream) {
@@ -358,14 +381,8 @@ extern "C" int lr_pool(const float* scores, int64_t total, const int64_t* bounds
   LR_REQUIRE(segments <= 65535, "Invalid pool layout");
   if (total == 0) return LR_OK;
   LR_REQUIRE(scores && bounds && out, "Expected contiguous CUDA tensor");
-  const int half = static_cast<int>(width / 2);
-  const int use_lds = width <= 4097 ? 1 : 0;
-  const size_t lds = use_lds ? (kPoolThreads + 2 * half) * sizeof(float) : 0;
-  dim3 grid(static_cast<unsigned>(ceil_div(max_count, kPoolThreads)),
-            static_cast<unsigned>(segments));
-  pool_kernel<<<grid, kPoolThreads, lds, as_stream(stream)>>>(scores, total, bounds, out, half,
-                                                             use_lds);
-  return check_launch("pool");
+  return launch_pool(scores, total, bounds, segments, max_count, width, out, nullptr, 0,
+                     as_stream(stream));
 }
 
 extern "C" int lr_decision_risk_scores(const float* probabilities, const void* values,

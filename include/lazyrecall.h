@@ -265,6 +265,20 @@ int lr_select_refine_queue(const int64_t* position_starts, int64_t total, int64_
                            const int64_t* quotas, const int64_t* offsets, float* out_values,
                            int64_t* out_segments, int64_t* out_positions, void* stream);
 
+/* lr_pool followed by lr_select_refine_sets on the pooled table, in one call: controller.py:147-150
+ * (pool_score_table, scoring.py:322-353, then allocation_preserving_references,
+ * selection.py:52-88). The pool launch also resets the selection's counters in `workspace`,
+ * which saves lr_select_refine_sets' own reset launch. raw, total, bounds [segments + 1],
+ * max_count, width and pooled (output) as lr_pool; the rest as lr_select_refine_sets, whose
+ * _queue half may follow with the same workspace. */
+int lr_pool_select_refine_sets(const float* raw, int64_t total, const int64_t* bounds,
+                               int64_t max_count, int64_t width, float* pooled,
+                               const int64_t* segment_ends, const int64_t* position_starts,
+                               int64_t segments, int64_t count, void* workspace,
+                               size_t workspace_bytes, int64_t* quotas, int64_t* offsets,
+                               int64_t* removed_positions, int64_t* changed, int64_t* host_info,
+                               const int32_t* nonfinite, void* stream);
+
 /* One head slot per (layer, KV head), LR_HEAD_WORDS i64 each (device):
  *   [0] keys ptr, [1] values ptr, [2] positions ptr (this head's first row),
  *   [3] length, [4] score-segment index or -1, [5] unused (0). */

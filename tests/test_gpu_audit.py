@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from code_for_iclr27_amd import audit, scoring, selection, workloads
+from code_for_iclr27_amd import _lib, audit, scoring, selection, workloads
 from oracle import kv_ops
 from oracle import selection as oselection
 
@@ -105,6 +105,58 @@ def test_select_many_segments_and_side_stream(device):
     two.wait_queue()
     torch.cuda.synchronize()
     compare(two, expect, ends)
+
+
+def _fused_sets(device, raw_d, bounds_d, starts_d, lengths, count, workspace):
+    """lr_pool_select_refine_sets: pooled table and removal sets."""
+    segments, total = len(lengths), raw_d.numel()
+    pooled = torch.empty_like(raw_d)
+    out = torch.empty((count + 3 * segments + 1,), dtype=torch.int64, device=device)
+    removed, quotas = out[:count], out[count:count + segments]
+    offsets, changed = out[count + segments:count + 2 * segments + 1], out[count + 2 * segments + 1:]
+    _lib.call("lr_pool_select_refine_sets", raw_d.data_ptr(), total, bounds_d.data_ptr(),
+              int(max(lengths)), 7, pooled.data_ptr(), bounds_d[1:].data_ptr(),
+              starts_d.data_ptr(), segments, count, workspace.data_ptr(), workspace.numel(),
+              quotas.data_ptr(), offsets.data_ptr(), removed.data_ptr(), changed.data_ptr(), None,
+              None, _lib.stream_of(raw_d))
+    torch.cuda.synchronize()
+    return pooled.cpu().numpy(), quotas.cpu().numpy(), offsets.cpu().numpy(), \
+        removed.cpu().numpy(), changed.cpu().numpy()
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_pool_select_fused_matches_oracle(device, ties):
+    """The fused pool + removal-set entry (its pool launch resets the selection's counters):
+    the pooled table equals the oracle's Pool7 bit for bit and the sets equal the oracle's, on
+    two calls in a row over one workspace (the second smaller, so stale counts of the first
+    would show), against the standalone lr_pool + lr_select_refine_sets as well."""
+    rng = np.random.default_rng(5 + ties)
+    lengths = [2218] * 9 + [1, 7, 300, 5000, 4097]
+    raw, pooled, ends = tables(rng, lengths, ties)
+    starts = rng.integers(0, 40, len(lengths))
+    raw_d = torch.from_numpy(raw).to(device)
+    bounds_d = torch.from_numpy(np.concatenate(([0], ends)).astype(np.int64)).to(device)
+    starts_d = torch.from_numpy(starts.astype(np.int64)).to(device)
+    first, second = raw.size // 3, max(1, raw.size // 50)
+    nbytes = _lib.load().lr_select_workspace_bytes(raw.size, len(lengths), first)
+    workspace = torch.full((nbytes,), 0xA5, dtype=torch.uint8, device=device)
+    for count in (first, second):
+        got_pooled, quotas, offsets, removed, changed = _fused_sets(
+            device, raw_d, bounds_d, starts_d, lengths, count, workspace)
+        np.testing.assert_array_equal(got_pooled, pooled)
+        expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+        np.testing.assert_array_equal(quotas, expect.quotas)
+        for s in range(len(lengths)):
+            np.testing.assert_array_equal(removed[offsets[s]:offsets[s + 1]],
+                                          np.sort(expect.positions[expect.segments == s]))
+        separate = selection.select_refine(raw_d, torch.from_numpy(pooled).to(device), list(ends),
+                                           list(starts), [(i, 0) for i in range(len(lengths))],
+                                           count, queue=False)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(separate.quotas.cpu().numpy(), quotas)
+        np.testing.assert_array_equal(separate.offsets.cpu().numpy(), offsets)
+        np.testing.assert_array_equal(separate.removed_positions.cpu().numpy(), removed)
+        np.testing.assert_array_equal(separate.changed.cpu().numpy(), changed)
 
 
 def test_select_all_equal_scores(device):
