@@ -586,9 +586,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 
 // all KT key tiles. After a query tile's last group every lane holds 16 drops per key tile
 // (its query x 16 keys); a transpose through LDS reduces them over the tile's queries, so a
 // lane keeps one running (min, max) pair per key tile.
-// On gfx950 MFMA and VALU work of a SIMD's waves do not overlap; the kernel is bound by their
-// sum; KT = 2 halves the per-unit overhead (copies, statistics, branches, barrier, B reads)
-// per key, at two waves per SIMD.
+// On gfx950 the MFMAs of one wave hide only part of their time behind another wave's VALU
+// work (about 60% in a probe of two waves per SIMD), so the kernel is bound by VALU issue plus
+// the exposed MFMA time; KT = 2 halves the per-unit overhead (copies, statistics, branches,
+// barrier, B reads) per key, at two waves per SIMD.
 // Key tiles per wave: two for d = 128 (measured faster there), one for d = 64 (three waves per
 // SIMD fit) and d = 256 (the K operand alone takes 64 registers per tile).
 template <int D>
@@ -784,21 +785,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
       }
       continue;
     }
-    f32x16 acc[KT];
-    {
-      bf16x8 b[KS];
-      const __bf16* brow = q_lds[buf][k] + col * D;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        b[ks] = *reinterpret_cast<const bf16x8*>(brow + 8 * swizzled_chunk<D>(col, half * KS + ks));
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        acc[t] = mfma_tile_zero();
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[t][ks], b[ks], acc[t], 0, 0, 0);
-      }
-    }
     const float4 st = st_lds[buf][k][col];
     const float query_position = qp_lds[buf][k][col];
     // ratio = p / max(1 - p, eps) = e / max(S - e, eps*S) for the lane's (key, query) pairs.
@@ -806,30 +792,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
     // is exact when no key of this wave lies after any query of the unit and every row has
     // S >= 2 and eps*S <= 1/2: then e <= 1 gives S - e >= 1 > eps*S. It also takes the ratio
     // as 1 / (S*u - 1) with u = 1/e = exp(m - z), one operation fewer than e / (S - e).
+    const bool general = __any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f));
     float ratio[KT][16];
-    if (__any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f))) {
+    // ratio of key tile t from its logit inputs z (logit_input of the accumulators)
+    auto ratio_general = [&](int t, const float (&z_in)[16]) {
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 kp = *reinterpret_cast<const f32x4*>(kpos_wave + 32 * t + 8 * c + 4 * half);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const f32x4 kp = *reinterpret_cast<const f32x4*>(kpos_wave + 32 * t + 8 * c + 4 * half);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * c + j;
-            float z = logit_input<P2>(acc[t][r], scale);
-            z = kp[j] <= query_position ? z : -INFINITY;
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, lg, st.x));
-            ratio[t][r] = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
-          }
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * c + j;
+          const float z = kp[j] <= query_position ? z_in[r] : -INFINITY;
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(z, lg, st.x));
+          ratio[t][r] = e * __builtin_amdgcn_rcpf(fmaxf(st.y - e, st.z));
         }
-    } else {
+      }
+    };
+    auto ratio_fast = [&](int t, const float (&z_in)[16]) {
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
+      for (int r = 0; r < 16; ++r) {
+        const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(z_in[r], -lg, -st.x));
+        ratio[t][r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
+      }
+    };
+    {
+      bf16x8 b[KS];
+      const __bf16* brow = q_lds[buf][k] + col * D;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(logit_input<P2>(acc[t][r], scale), -lg, -st.x));
-          ratio[t][r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
+      for (int ks = 0; ks < KS; ++ks)
+        b[ks] = *reinterpret_cast<const bf16x8*>(brow + 8 * swizzled_chunk<D>(col, half * KS + ks));
+      f32x16 acc0 = mfma_tile_zero();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[0][ks], b[ks], acc0, 0, 0, 0);
+      float z0[16];
+      if constexpr (KT == 2) {
+        // Key tile 1's MFMAs run while the wave rounds key tile 0's logits: one MFMA, then its
+        // share of that VALU work (a wave issues in order, so the placement is what lets the
+        // two overlap). The rounding is common to both forms of the ratio, so it comes before
+        // the branch between them.
+        constexpr int kPer = 16 / KS;  // tile-0 elements per tile-1 MFMA
+        __builtin_amdgcn_sched_barrier(0);  // tile 0's MFMAs stay ahead of this region
+        f32x16 acc1 = mfma_tile_zero();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[1][ks], b[ks], acc1, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) z0[ks * kPer + e] = logit_input<P2>(acc0[ks * kPer + e], scale);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, (P2 ? 1 : 3) * kPer, 0);
         }
+        float z1[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) z1[r] = logit_input<P2>(acc1[r], scale);
+        if (general) {
+          ratio_general(0, z0);
+          ratio_general(1, z1);
+        } else {
+          ratio_fast(0, z0);
+          ratio_fast(1, z1);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) z0[r] = logit_input<P2>(acc0[r], scale);
+        if (general) ratio_general(0, z0);
+        else ratio_fast(0, z0);
+      }
     }
     // The drops restart with each query tile: its first group writes them, the others add.
     const float* pv_row = pv_lds + g * kKeys + wave * 32 * KT;
