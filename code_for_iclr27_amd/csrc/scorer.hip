@@ -788,11 +788,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
     const float4 st = st_lds[buf][k][col];
     const float query_position = qp_lds[buf][k][col];
     // ratio = p / max(1 - p, eps) = e / max(S - e, eps*S) for the lane's (key, query) pairs.
-    // The general form applies the causal mask and the clamp. The fast form drops both, which
-    // is exact when no key of this wave lies after any query of the unit and every row has
-    // S >= 2 and eps*S <= 1/2: then e <= 1 gives S - e >= 1 > eps*S. It also takes the ratio
-    // as 1 / (S*u - 1) with u = 1/e = exp(m - z), one operation fewer than e / (S - e).
-    const bool general = __any(kmax > query_position || !(st.y >= 2.0f && st.z <= 0.5f));
+    // The general form applies the causal mask and the clamp. The fast form drops the clamp,
+    // which is exact for every visible key when every row has S >= 2 and eps*S <= 1/2: then
+    // e <= 1 gives S - e >= 1 > eps*S. It also takes the ratio as 1 / (S*u - 1) with
+    // u = 1/e = exp(m - z), one operation fewer than e / (S - e). Where some key of this wave
+    // lies after some query of the unit, the masked fast form sets those pairs' ratios to 0
+    // afterwards (whatever the fast form gave for them).
+    const bool general = __any(!(st.y >= 2.0f && st.z <= 0.5f));
+    const bool masked = __any(kmax > query_position);
     float ratio[KT][16];
     // ratio of key tile t from its logit inputs z (logit_input of the accumulators)
     auto ratio_general = [&](int t, const float (&z_in)[16]) {
@@ -813,6 +816,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
       for (int r = 0; r < 16; ++r) {
         const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(z_in[r], -lg, -st.x));
         ratio[t][r] = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
+      }
+    };
+    auto ratio_masked = [&](int t, const float (&z_in)[16]) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 kp = *reinterpret_cast<const f32x4*>(kpos_wave + 32 * t + 8 * c + 4 * half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * c + j;
+          const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(z_in[r], -lg, -st.x));
+          const float q = __builtin_amdgcn_rcpf(__builtin_fmaf(st.y, v, -1.0f));
+          ratio[t][r] = kp[j] <= query_position ? q : 0.0f;
+        }
       }
     };
     {
@@ -848,6 +864,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
         if (general) {
           ratio_general(0, z0);
           ratio_general(1, z1);
+        } else if (masked) {
+          ratio_masked(0, z0);
+          ratio_masked(1, z1);
         } else {
           ratio_fast(0, z0);
           ratio_fast(1, z1);
@@ -856,6 +875,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
 #pragma unroll
         for (int r = 0; r < 16; ++r) z0[r] = logit_input<P2>(acc0[r], scale);
         if (general) ratio_general(0, z0);
+        else if (masked) ratio_masked(0, z0);
         else ratio_fast(0, z0);
       }
     }
