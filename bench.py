@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the LazyRecall KV-management hot path on one MI355X.
 
-Headline (BASELINE.json metric): one full audit step on the Llama-3.1-8B cache (cfg1:
+Headline metric: one full audit step on the Llama-3.1-8B cache (cfg1:
 32 layers x 8 KV heads x d128, 2250 tokens per head, window 250, G=4): temporal scores of all
 567,808 candidates -> Pool7 -> allocation-preserving selection of 64,000 slots -> compaction
 of every layer. value = algorithmic bytes of the step / measured step time (GB/s).
@@ -696,7 +696,7 @@ def lazy_window_bench(torch, layers, qpos, margin, cfg, reps=5):
 
 
 def audit_config_bench(torch, name, seed, steps=10, warmup=3):
-    """A shorter audit-step measurement of another BASELINE configuration (cfg0, cfg4, cfg3)."""
+    """A shorter audit-step measurement of another benchmark configuration (cfg0, cfg4, cfg3)."""
     import numpy as np
 
     from code_for_iclr27_amd import audit, workloads

@@ -1,4 +1,4 @@
-"""Synthetic inputs of the BASELINE configurations (no weights, no datasets).
+"""Synthetic inputs of the benchmark configurations (no weights, no datasets).
 
 cfg0  Llama-3.2-1B cache: L16 H8 d64, G=4, T=2250, W=250, evict 250 per (layer, head)
 cfg1  Llama-3.1-8B cache: L32 H8 d128, G=4, T=2250, W=250, evict 250 per (layer, head)
