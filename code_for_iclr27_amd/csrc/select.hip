@@ -8,7 +8,8 @@
 // device: a multi-block radix select finds the global threshold, one workgroup per segment
 // does its counting, ordered compaction, radix select and stable radix sorts in LDS, and a
 // final stable sort orders the slots. Scores are compared through an order-preserving uint32
-// key (-0.0 and +0.0 are one key; NaN sorts last).
+// key (-0.0 and +0.0 are one key; every NaN, whatever its sign and payload, is one key above
+// +inf, so NaNs sort last and among themselves by index, as numpy and torch.topk order them).
 #include <utility>
 
 #include <rocprim/device/device_radix_sort.hpp>
@@ -26,6 +27,7 @@ constexpr int kPickThreads = 512;  // segment_pick workgroups (measured faster t
 __device__ __forceinline__ uint32_t float_key(float f) {
   uint32_t u = __float_as_uint(f);
   if (u == 0x80000000u) u = 0u;  // -0.0 == +0.0
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // any NaN
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 

@@ -170,6 +170,39 @@ def test_select_all_equal_scores(device):
         compare(result, expect, ends)
 
 
+def test_select_nan_and_infinities(device):
+    """NaNs of either sign and any payload sort after +inf and among themselves by index (as the
+    oracle's numpy sort, and torch.topk, place them); infinities and signed zeros in both tables,
+    at every count."""
+    rng = np.random.default_rng(23)
+    lengths = [40, 1, 57, 30]
+    ends = np.cumsum(lengths)
+    raw = rng.standard_normal(ends[-1]).astype(np.float32)
+    pooled = rng.standard_normal(ends[-1]).astype(np.float32)
+    bits = np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0xFFFFFFFF, 0x7FA00000], np.uint32)
+    specials = np.concatenate((bits.view(np.float32),
+                               np.array([np.inf, -np.inf, 0.0, -0.0], np.float32)))
+    for table in (raw, pooled):
+        at = rng.choice(table.size, 30, replace=False)
+        table[at] = specials[rng.integers(0, specials.size, at.size)]
+    starts = [0, 5, 9, 11]
+    for count in (1, 7, 40, 64, 100, 127, ends[-1]):
+        result = run_select(device, raw, pooled, ends, starts, int(count))
+        expect = oselection.refine_arrays(raw, pooled, ends, starts, int(count), tie="canonical")
+        np.testing.assert_array_equal(result.quotas.cpu().numpy(), expect.quotas)
+        np.testing.assert_array_equal(result.segments.cpu().numpy(), expect.segments)
+        np.testing.assert_array_equal(result.positions.cpu().numpy(), expect.positions)
+        got = result.values.cpu().numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(expect.values))
+        finite = ~np.isnan(got)
+        np.testing.assert_array_equal(got[finite], expect.values[finite])
+        offsets = result.offsets.cpu().numpy()
+        removed = result.removed_positions.cpu().numpy()
+        for s in range(len(ends)):
+            np.testing.assert_array_equal(removed[offsets[s]:offsets[s + 1]],
+                                          np.sort(expect.positions[expect.segments == s]))
+
+
 def test_select_negative_zero_and_signs(device):
     raw = np.asarray([0.0, -0.0, -1.0, 2.0, -0.0, 0.0, 1e-30, -1e-30], np.float32)
     pooled = raw[::-1].copy()
