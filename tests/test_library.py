@@ -40,6 +40,26 @@ def test_invalid_arguments_fail_on_host():
     assert library.lr_score_workspace_bytes(2, 4, 250, 1000) > 0
 
 
+def test_pool_select_checks_arguments_on_host():
+    """The fused pool + selection entry refuses bad shapes before touching the device, with the
+    messages of lr_pool and lr_select_refine_sets."""
+    library = _lib.load()
+    args = lambda total, max_count, width, segments, count: (
+        None, total, None, max_count, width, None, None, None, segments, count, None, 0, None,
+        None, None, None, None, None, None)
+    assert library.lr_pool_select_refine_sets(*args(100, 50, 7, 2, 101)) == 1
+    assert "Selection count must lie in [1, total]" in _lib.last_error()
+    assert library.lr_pool_select_refine_sets(*args(100, 50, 6, 2, 10)) == 1
+    assert "Invalid pool configuration" in _lib.last_error()
+    assert library.lr_pool_select_refine_sets(*args(100, 50, 7, 70000, 10)) == 1
+    assert "Invalid pool layout" in _lib.last_error()
+    assert library.lr_pool_select_refine_sets(*args(100, 50, 7, 2, 10)) == 1
+    assert "Expected contiguous CUDA tensor" in _lib.last_error()
+    # the workspace it needs grows with the segment count (one LDS-histogram row per segment)
+    assert (library.lr_select_workspace_bytes(1000, 64, 10)
+            > library.lr_select_workspace_bytes(1000, 2, 10))
+
+
 def test_noalloc_attention_size_check_needs_no_gpu():
     library = _lib.load()
     assert library.lr_packed_attention_scratch_bytes() == 16 << 20
