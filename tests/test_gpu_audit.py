@@ -107,7 +107,7 @@ def test_select_many_segments_and_side_stream(device):
     compare(two, expect, ends)
 
 
-def _fused_sets(device, raw_d, bounds_d, starts_d, lengths, count, workspace):
+def _fused_sets(device, raw_d, bounds_d, starts_d, lengths, count, workspace, width=7):
     """lr_pool_select_refine_sets: pooled table and removal sets."""
     segments, total = len(lengths), raw_d.numel()
     pooled = torch.empty_like(raw_d)
@@ -115,7 +115,7 @@ def _fused_sets(device, raw_d, bounds_d, starts_d, lengths, count, workspace):
     removed, quotas = out[:count], out[count:count + segments]
     offsets, changed = out[count + segments:count + 2 * segments + 1], out[count + 2 * segments + 1:]
     _lib.call("lr_pool_select_refine_sets", raw_d.data_ptr(), total, bounds_d.data_ptr(),
-              int(max(lengths)), 7, pooled.data_ptr(), bounds_d[1:].data_ptr(),
+              int(max(lengths)), width, pooled.data_ptr(), bounds_d[1:].data_ptr(),
               starts_d.data_ptr(), segments, count, workspace.data_ptr(), workspace.numel(),
               quotas.data_ptr(), offsets.data_ptr(), removed.data_ptr(), changed.data_ptr(), None,
               None, _lib.stream_of(raw_d))
@@ -157,6 +157,43 @@ def test_pool_select_fused_matches_oracle(device, ties):
         np.testing.assert_array_equal(separate.offsets.cpu().numpy(), offsets)
         np.testing.assert_array_equal(separate.removed_positions.cpu().numpy(), removed)
         np.testing.assert_array_equal(separate.changed.cpu().numpy(), changed)
+
+
+@pytest.mark.parametrize("width", [1, 3, 9])
+@pytest.mark.parametrize("case", ["one_segment", "count_all", "count_one", "ragged"])
+def test_pool_select_fused_edge_cases(device, width, case):
+    """The fused entry at pool widths other than 7 and at the edges of the selection: a single
+    segment, every candidate selected, a single one, and ragged segments of 1..3000 keys; pooled
+    table and sets against the oracle's Pool and refine_arrays."""
+    rng = np.random.default_rng(10 * width + ["one_segment", "count_all", "count_one",
+                                              "ragged"].index(case))
+    lengths = {"one_segment": [3001], "count_all": [17, 400, 5],
+               "count_one": [250, 250, 250], "ragged": [1, 2, 3000, 7, 64, 65, 1]}[case]
+    ends = np.cumsum(lengths)
+    raw = np.round(rng.random(ends[-1]) * 500).astype(np.float32) / 500  # with ties
+    pooled = np.empty_like(raw)
+    start = 0
+    for end in ends:
+        pooled[start:end] = kv_ops.pool(raw[start:end], [0, end - start], width)
+        start = end
+    count = {"one_segment": 777, "count_all": int(ends[-1]), "count_one": 1,
+             "ragged": int(ends[-1]) // 3}[case]
+    starts = rng.integers(0, 40, len(lengths))
+    raw_d = torch.from_numpy(raw).to(device)
+    bounds_d = torch.from_numpy(np.concatenate(([0], ends)).astype(np.int64)).to(device)
+    starts_d = torch.from_numpy(starts.astype(np.int64)).to(device)
+    nbytes = _lib.load().lr_select_workspace_bytes(raw.size, len(lengths), count)
+    workspace = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=device)
+    got_pooled, quotas, offsets, removed, changed = _fused_sets(
+        device, raw_d, bounds_d, starts_d, lengths, count, workspace, width)
+    np.testing.assert_array_equal(got_pooled, pooled)
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+    np.testing.assert_array_equal(quotas, expect.quotas)
+    assert offsets[-1] == count
+    for s in range(len(lengths)):
+        np.testing.assert_array_equal(removed[offsets[s]:offsets[s + 1]],
+                                      np.sort(expect.positions[expect.segments == s]))
+    assert int(changed.sum()) == expect.changed
 
 
 def test_select_all_equal_scores(device):
