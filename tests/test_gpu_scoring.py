@@ -145,6 +145,95 @@ def test_fused_scorer_matches_oracle(device, dim, groups, window):
     assert offset == scores.size
 
 
+def _peaked_layers(dim, groups, window, query_scale, device):
+    head_lengths = [[300, 190], [260, 75]]
+    layers, qpos = workloads.make_layers(head_lengths, groups, dim, window, device,
+                                         seed=dim + groups + 7)
+    for layer in layers:  # scale half of the query heads: some rows peaked, the rest ordinary
+        q = layer.queries.float()
+        q[: q.size(0) // 2] *= query_scale
+        layer.queries.copy_(q.to(layer.queries.dtype))
+    return layers, qpos
+
+
+@pytest.mark.parametrize("dim,groups,window,query_scale,epsilon", [
+    (128, 4, 90, 2.0, 1e-6),    # peaked rows (S < 2 in some): the clamped (general) form
+    (256, 6, 77, 2.0, 1e-6),
+    (64, 4, 70, 1.0, 0.4),      # eps * S > 1/2 in most rows: the general form almost everywhere
+    (128, 4, 90, 1.0, 0.4)])
+def test_fused_scorer_general_form_rows(device, dim, groups, window, query_scale, epsilon):
+    """Rows the fast forms may not take: peaked attention (queries scaled up, so S is below 2)
+    and a large denominator epsilon (eps * S > 1/2), mixed with ordinary rows; the scores against
+    the oracle at rtol 1e-5."""
+    layers, qpos = _peaked_layers(dim, groups, window, query_scale, device)
+    margin = torch.tensor([2.0], device=device)
+    plan = scoring.plan_segments(layers, protect_prompt=True, protect_recent=32)
+    scores = to_np(scoring.score_plan(plan, qpos, margin, denominator_epsilon=epsilon))
+    offset = 0
+    for segment, seg in enumerate(plan.segments):
+        layer = layers[seg.layer]
+        start = plan.head_starts[segment]
+        length = int(plan.table[segment, 5])
+        logits = _check_segment_logits(plan, layers, segment, device)
+        q = to_np(layer.queries[seg.head * groups:(seg.head + 1) * groups]).transpose(1, 0, 2)
+        expect = oscoring.head_scores(
+            q, qpos.cpu().numpy(), to_np(layer.keys[start:start + length]),
+            to_np(layer.positions[start:start + length]), to_np(layer.values[start:start + length]),
+            seg.position_start, seg.position_start + seg.count,
+            to_np(layer.gradient[seg.head * groups:(seg.head + 1) * groups]), np.float32(2.0),
+            epsilon, logits=logits)
+        got = scores[offset:offset + seg.count]
+        np.testing.assert_allclose(got, expect, rtol=1e-5, atol=1e-12,
+                                   err_msg=f"segment {segment} layer {seg.layer} head {seg.head}")
+        offset += seg.count
+    assert offset == scores.size
+
+
+@pytest.mark.parametrize("dim,groups", [(128, 4), (256, 6)])
+def test_fused_scorer_sharply_peaked_rows(device, dim, groups):
+    """Sharply peaked rows (queries scaled 6x: the top key's p within 1e-3 or less of 1). The
+    ratio p / (1 - p) of that key is then ill-conditioned in f32 for any implementation of the
+    formula (the reference's divides by 1 - p in f32, scoring.cu:101): an error of a few f32
+    ulps in the row sum S becomes a relative error of about ulps * S / (S - 1) in the ratio.
+    Scores must agree with the f64 oracle within that conditioning bound, and nine in ten of
+    them within rtol 1e-5."""
+    window = 90
+    layers, qpos = _peaked_layers(dim, groups, window, 6.0, device)
+    margin = torch.tensor([2.0], device=device)
+    plan = scoring.plan_segments(layers, protect_prompt=True, protect_recent=32)
+    scores = to_np(scoring.score_plan(plan, qpos, margin))
+    offset = 0
+    within = total = 0
+    for segment, seg in enumerate(plan.segments):
+        layer = layers[seg.layer]
+        start = plan.head_starts[segment]
+        length = int(plan.table[segment, 5])
+        logits = _check_segment_logits(plan, layers, segment, device)
+        positions = to_np(layer.positions[start:start + length])
+        q = to_np(layer.queries[seg.head * groups:(seg.head + 1) * groups]).transpose(1, 0, 2)
+        expect = oscoring.head_scores(
+            q, qpos.cpu().numpy(), to_np(layer.keys[start:start + length]), positions,
+            to_np(layer.values[start:start + length]), seg.position_start,
+            seg.position_start + seg.count,
+            to_np(layer.gradient[seg.head * groups:(seg.head + 1) * groups]), np.float32(2.0),
+            1e-6, logits=logits)
+        # conditioning of the segment's worst row: S / max(S - 1, eps * S) with S = sum
+        # exp(z - max z) (the clamp bounds it by 1 / eps)
+        z = logits.astype(np.float64)
+        visible = positions[None, None, :] <= qpos.cpu().numpy()[:, None, None]
+        z = np.where(visible, z, -np.inf)
+        row_sum = np.exp(z - z.max(axis=2, keepdims=True)).sum(axis=2)
+        condition = float(np.max(row_sum / np.maximum(row_sum - 1.0, 1e-6 * row_sum)))
+        bound = max(1e-5, 64 * 2.0 ** -24 * condition)
+        got = scores[offset:offset + seg.count]
+        np.testing.assert_allclose(got, expect, rtol=bound, atol=1e-12,
+                                   err_msg=f"segment {segment}: conditioning {condition:.3g}")
+        within += int(np.sum(np.abs(got - expect) <= 1e-5 * np.abs(expect) + 1e-12))
+        total += got.size
+        offset += seg.count
+    assert within >= 0.9 * total, (within, total)
+
+
 def _scores_with_stages(plan, qpos, margin, stages, device):
     segments = plan.segment_count
     nbytes = _lib.load().lr_score_workspace_bytes(segments, plan.groups, plan.window,
