@@ -115,7 +115,8 @@ def _check_segment_logits(plan, layers, segment, device):
 
 
 @pytest.mark.parametrize("dim,groups,window", [(128, 4, 250), (64, 4, 40), (256, 6, 77), (128, 3, 33),
-                                               (128, 8, 70), (128, 1, 100)])
+                                               (128, 8, 70), (128, 1, 100), (128, 16, 40),
+                                               (64, 16, 65), (256, 16, 33)])
 def test_fused_scorer_matches_oracle(device, dim, groups, window):
     head_lengths = [[300, 41, 280, 2], [170, 300, 33, 299]]
     prompts = [[0, 0, 5, 0], [12, 0, 0, 0]]
