@@ -196,6 +196,31 @@ def test_pool_select_fused_edge_cases(device, width, case):
     assert int(changed.sum()) == expect.changed
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_select_random_configurations(device, seed):
+    """Seeded random shapes: 1-300 segments of 1-5000 candidates, any count from 1 to all, and a
+    tie density from none to heavy, so the threshold's last digit and tie group fall in one,
+    several or many segments; removal sets and queue order identical to the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    segments = int(rng.integers(1, 301))
+    lengths = rng.integers(1, 5001 if segments < 20 else 400, segments)
+    ends = np.cumsum(lengths)
+    levels = int(rng.choice([0, 3, 50, 5000]))
+    raw = rng.random(ends[-1]).astype(np.float32)
+    if levels:
+        raw = np.floor(raw * levels).astype(np.float32) / levels
+    pooled = np.empty_like(raw)
+    start = 0
+    for end in ends:
+        pooled[start:end] = kv_ops.pool(raw[start:end], [0, end - start], 7)
+        start = end
+    starts = rng.integers(0, 40, segments)
+    count = int(rng.integers(1, raw.size + 1))
+    result = run_select(device, raw, pooled, ends, starts, count)
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+    compare(result, expect, ends)
+
+
 def test_select_all_equal_scores(device):
     lengths = [50, 60, 70]
     raw = np.full(180, 0.25, np.float32)
