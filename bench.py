@@ -95,6 +95,26 @@ def measured_traffic(kernel, config):
     return None
 
 
+SQ_PROFILE = os.path.join(ROOT, "profiles", "scorer_cfg1_sq_counters.md")
+SIMDS, ENGINE_CLOCK_GHZ = 1024, 2.4  # MI355X: 256 CUs x 4 SIMDs, peak engine clock
+
+
+def measured_valu_cycles(kernel, config):
+    """VALU-active cycles (all waves) per launch of `kernel`, from the committed rocprofv3
+    SQ_ACTIVE_INST_VALU summary (lines `valu_active_cycles_per_launch <config> <kernel> <n>`),
+    or None."""
+    try:
+        with open(SQ_PROFILE) as f:
+            for line in f:
+                parts = line.split()
+                if (len(parts) == 4 and parts[0] == "valu_active_cycles_per_launch"
+                        and parts[1] == config and parts[2] == kernel):
+                    return int(parts[3])
+    except OSError:
+        pass
+    return None
+
+
 class EventTimer:
     """Records a HIP event on the current stream at each mark (events are created up front,
     outside the timed loop). With `only`, marks with other names record nothing: every event
@@ -143,18 +163,24 @@ def cpu_baseline(torch, layers, qpos, margin, cfg, target_seconds):
                          positions=layer.positions.cpu(), head_lens=list(layer.head_lens),
                          queries=layer.queries.cpu(), gradient=layer.gradient.cpu()))
     qpos_c, margin_c = qpos.cpu(), margin.cpu().reshape(())
-    # calibrate on one layer, then run a whole audit step over as many layers as fit the budget
-    started = time.perf_counter()
-    cpu_path.audit_step_cpu(host[:1], qpos_c, margin_c, cfg.evict_per_head * cfg.heads,
-                            cfg.protect_recent, cfg.pool_kernel, cfg.epsilon)
-    per_layer = time.perf_counter() - started
-    n = max(1, min(len(host), int(target_seconds / max(per_layer, 1e-3))))
-    started = time.perf_counter()
-    cpu_path.audit_step_cpu(host[:n], qpos_c, margin_c, cfg.evict_per_head * cfg.heads * n,
-                            cfg.protect_recent, cfg.pool_kernel, cfg.epsilon)
-    seconds = time.perf_counter() - started
+
+    def step(n):
+        started = time.perf_counter()
+        cpu_path.audit_step_cpu(host[:n], qpos_c, margin_c, cfg.evict_per_head * cfg.heads * n,
+                                cfg.protect_recent, cfg.pool_kernel, cfg.epsilon)
+        return time.perf_counter() - started
+
+    # a one-layer step sizes the sample: the whole audit step over as many layers as make each
+    # of the `runs` timed runs about target_seconds / runs; then one warm-up run of that sample
+    # and the median of the timed runs
+    runs = 5
+    per_layer = step(1)
+    n = max(1, min(len(host), int(target_seconds / runs / max(per_layer, 1e-3))))
+    step(n)
+    times = sorted(step(n) for _ in range(runs))
+    seconds = times[runs // 2]
     scaled = seconds * len(host) / n
-    return n, seconds, scaled, threads
+    return n, seconds, scaled, threads, [round(t, 3) for t in times]
 
 
 def reinsert_bench(torch, seed, reps=5):
@@ -834,6 +860,15 @@ def main():
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                     "traffic": measured_traffic(dominant, cfg.name), "algorithmic_flops": flops}
+        # the kernel's real limit is VALU issue: its VALU-active time per SIMD (counted
+        # instructions, committed profile) against this run's measured kernel time
+        cycles = measured_valu_cycles(dominant, cfg.name)
+        if cycles is not None:
+            issue_us = cycles / SIMDS / (ENGINE_CLOCK_GHZ * 1e3)
+            roofline["valu"] = {"issue_us_per_simd": round(issue_us, 1),
+                                "kernel_us": round(dominant_us, 1),
+                                "frac": round(issue_us / dominant_us, 4),
+                                "source": "profiles/scorer_cfg1_sq_counters.md"}
     else:
         stage_bytes = {"compact": 2 * (rows_total - outcome.removed) * d * 2 * 2,
                        "projected_values": rows_total * d * 2}.get(dominant, nbytes)
@@ -888,27 +923,41 @@ def main():
                                  for name in others}
 
     if not args.no_cpu:
-        n, seconds, scaled, threads = cpu_baseline(torch, layers, qpos, margin, cfg, args.cpu_seconds)
+        n, seconds, scaled, threads, times = cpu_baseline(torch, layers, qpos, margin, cfg,
+                                                          args.cpu_seconds)
         line["cpu_baseline"] = {
             "value": round(nbytes / scaled / 1e9, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": (f"{cfg.name}: full audit step over the first {n} of {cfg.layers} layers "
-                       f"({n * cfg.heads} heads) took {seconds:.2f} s on the host, scaled by "
+                       f"({n * cfg.heads} heads), one warm-up run then the median of "
+                       f"{len(times)} runs, {seconds:.2f} s on the host, scaled by "
                        f"{cfg.layers}/{n} to {scaled:.2f} s per audit step"),
+            "run_seconds": times,
             "cpu_model": _cpu_model(),
         }
     print(json.dumps(line), flush=True)
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with its family / model / stepping and the
+    logical CPUs this process may use out of those listed."""
+    fields, listed = {}, 0
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, value = line.partition(":")
+                key = key.strip()
+                if key == "processor":
+                    listed += 1
+                elif key in ("model name", "cpu family", "model", "stepping", "cpu MHz"):
+                    fields.setdefault(key, value.strip())
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    detail = ", ".join(f"{key} {fields[key]}" for key in ("cpu family", "model", "stepping",
+                                                          "cpu MHz") if key in fields)
+    usable = len(os.sched_getaffinity(0))
+    return f"{name} ({detail}; {usable} of {listed} logical CPUs usable)"
 
 
 if __name__ == "__main__":

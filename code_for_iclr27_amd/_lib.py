@@ -47,6 +47,7 @@ SIGNATURES = {
     "lr_pack": [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _I64, _P, _P, _P],
     "lr_batch_append": [_P, _I64, _P, _P, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_pack_layers": [_P, _I64, _P, _I64, _I64, _P, _P, _P],
+    "lr_pack_heads": [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P],
     "lr_group_mean_queries": [_P, _I64, _I64, _I64, _I64, _I, _P, _P],
     "lr_append_flattened_cache": [_P, _I64, _P, _I64, _I64, _I64, _I, _P, _P, _P, _P],
     "lr_compact_flattened_kv": [_P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P],
@@ -66,7 +67,10 @@ SIGNATURES = {
                                    _P, _P, _P, _P, _P, _P],
     "lr_select_refine_queue": [_P, _I64, _I64, _I64, _P, _SZ, _P, _P, _P, _P, _P, _P],
     "lr_compact_heads": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _P],
+    "lr_compact_heads_layout": [_P, _I64, _P, _P, _P, _I64, _I, _I64, _I64, _P, _P, _P, _I64, _P,
+                                _P, _P],
     "lr_reinsert_plan": [_P, _I64, _P, _I64, _P, _P, _P, _P],
+    "lr_reinsert_plan_layout": [_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _P, _P],
     "lr_reinsert_resident": [_P, _I64, _P, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_reinsert_recalled": [_P, _I64, _P, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_queue_index": [_P, _P, _I64, _P, _P, _P, _I64, _P, _P],

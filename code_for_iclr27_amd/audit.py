@@ -53,7 +53,7 @@ def _native_planner():
                              address("lr_pool_select_refine_sets"),
                              address("lr_select_refine_queue"),
                              address("lr_queue_index"), address("lr_queue_evict_plan"),
-                             address("lr_compact_heads"), address("lr_last_error"),
+                             address("lr_compact_heads_layout"), address("lr_last_error"),
                              address("lr_staging_alloc"), address("lr_staging_free"),
                              address("lr_copy_words"))
         _bound = True
@@ -73,17 +73,42 @@ def pool_score_table(table: ScoreTable, kernel_size: int = 7) -> ScoreTable:
                       table.score_ms + (time.perf_counter() - started) * 1000.0)
 
 
+class DeviceLayout:
+    """The metadata the reference rebuilds with host-to-device copies after every layout change
+    (metadata.head_lens, metadata.cu_seqlens_k and metadata.max_seqlen_k; cache.py:171-178 after
+    a compaction, cache.py:246 after a reinsertion), here written on the device by the launch
+    that changed the layout. ``block`` is one i32 tensor: the new length of every (layer, head)
+    slot, then each layer's cumulative lengths (0, then the running sum).
+
+    ``head_lens[l]`` (i32 [H]) and ``cu_seqlens_k[l]`` (i32 [H + 1]) are device views, ready for
+    ``_C.append``'s ``cumulative`` argument; ``max_seqlen_k[l]`` is a host int, from the lengths
+    the host already knows. The views are valid in stream order after the launch."""
+
+    def __init__(self, block: torch.Tensor, kept: Sequence[Sequence[int]]):
+        layers, heads = len(kept), len(kept[0])
+        self.block = block
+        self.head_lens = block[:layers * heads].view(layers, heads)
+        self.cu_seqlens_k = block[layers * heads:].view(layers, heads + 1)
+        self.max_seqlen_k = [max(lengths, default=0) for lengths in kept]
+
+    def layer(self, index: int):
+        """(head_lens i32 [H], cu_seqlens_k i32 [H + 1], max_seqlen_k) of one layer."""
+        return self.head_lens[index], self.cu_seqlens_k[index], self.max_seqlen_k[index]
+
+
 class PackedLayers(abc.Sequence):
     """The compacted layers of an audit: every layer's rows live in one packed K, V and
     positions buffer (layer-major, heads in order). Layer i's LayerState, with views into those
-    buffers, is created when first indexed."""
+    buffers, is created when first indexed. ``layout`` (a DeviceLayout, or None) holds the
+    layers' metadata on the device when the launch that made them wrote it."""
 
     def __init__(self, keys, values, positions, kept: List[List[int]], offsets: List[int],
-                 sources: Sequence[LayerState]):
+                 sources: Sequence[LayerState], layout: Optional[DeviceLayout] = None):
         self.keys, self.values, self.positions = keys, values, positions
         self.kept = kept                                   # [L][H] rows kept per head
         self.offsets = offsets                             # [L + 1] first row of each layer
         self.sources = sources
+        self.layout = layout
         self._cache = {}
 
     def __len__(self) -> int:
@@ -105,6 +130,32 @@ class PackedLayers(abc.Sequence):
                                source.prompt_lens, source.queries, source.gradient)
             self._cache[index] = layer
         return layer
+
+
+def _archive_hook(transport, keys, count):
+    """The C++ launcher's archive hook for a RecallTransport (None without one): packs a fused
+    layout change's removed rows into a free archive slot, on the current stream, before the
+    compaction is enqueued. The batch of ``count`` rows is checked against the staging
+    capacity here, before any launch (record_evicted's check, transport.py:139-141)."""
+    if transport is None:
+        return None
+    if keys.dim() != 2 or keys.shape[1] != transport.dimension or keys.element_size() != 2:
+        raise RuntimeError("Recall configuration does not match the cache")
+    if count > transport.capacity:
+        transport.counters["archive_overflows"] += 1
+        raise RuntimeError("Eviction batch exceeds configured archive staging capacity")
+
+    def hook(head_table, slots, heads_per_layer, quotas, offsets, positions, count, max_rows):
+        transport.record_evicted_heads(head_table, slots, heads_per_layer, quotas, offsets,
+                                       positions, count, max_rows)
+    return hook
+
+
+def _removed_now(layers, count, immediate):
+    """Rows an audit step removes at once (an upper bound when fewer candidates exist)."""
+    if count <= 0:
+        return 0
+    return count if immediate < 0 or immediate >= count else immediate
 
 
 class EvictionQueue:
@@ -151,9 +202,12 @@ class EvictionQueue:
                                self.segments[start:].cpu().numpy(),
                                self.positions[start:].cpu().numpy(), self.coordinates)
 
-    def evict_prefix(self, layers: Sequence[LayerState], count: int):
+    def evict_prefix(self, layers: Sequence[LayerState], count: int, transport=None):
         """controller.py:57-70 for the device queue: removes the next ``count`` queued slots
-        and returns the new layers (a PackedLayers; ``.kept`` holds the head lengths)."""
+        and returns the new layers (a PackedLayers; ``.kept`` holds the head lengths, ``.layout``
+        the device metadata). With a ``transport`` (a RecallTransport) the removed rows are
+        packed for its archive before the compaction, as remove_positions archives them
+        (cache.py:110-112)."""
         count = int(count)
         if not count:
             return layers
@@ -171,12 +225,14 @@ class EvictionQueue:
             tensors = ([layer.keys for layer in layers], [layer.values for layer in layers],
                        [layer.positions for layer in layers])
             lengths, packed_offsets = [list(layer.head_lens) for layer in layers], []
-        out_keys, out_values, out_positions, kept, offsets = planner.queue_evict_launch(
+        out_keys, out_values, out_positions, kept, offsets, layout = planner.queue_evict_launch(
             *tensors, lengths, self.slot_segment, self.quotas, self.offsets, self.removed,
             self.rank, self._segments_host, self.consumed, self.consumed + count,
-            torch.cuda.current_stream(device).cuda_stream, self._sync, packed_offsets)
+            torch.cuda.current_stream(device).cuda_stream, self._sync, packed_offsets,
+            _archive_hook(transport, tensors[0][0], count))
         self.consumed += count
-        return PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers)
+        return PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers,
+                            DeviceLayout(layout, kept))
 
 
 @dataclass
@@ -190,6 +246,12 @@ class AuditOutcome:
     plan: SegmentPlan
     removed: int
     queue: Optional[EvictionQueue] = None  # the lazy queue (run(..., immediate=k), k < count)
+
+    @property
+    def layout(self) -> Optional[DeviceLayout]:
+        """The compacted layers' metadata on the device (None when no compaction ran: the
+        caller's metadata then still holds)."""
+        return getattr(self.layers, "layout", None)
 
     @property
     def segments(self) -> List[ScoreSegment]:
@@ -234,7 +296,7 @@ class AuditStep:
             margin: torch.Tensor, count: int, protect_recent: int = 32, pool_kernel: int = 7,
             denominator_epsilon: float = 1e-6, check_finite: bool = True,
             queue_order: bool = False, timer=None, native: bool = True,
-            immediate: Optional[int] = None) -> AuditOutcome:
+            immediate: Optional[int] = None, transport=None) -> AuditOutcome:
         """Scores and selects ``count`` slots (controller.run_audit, controller.py:140-159).
 
         ``immediate`` None (or >= count) removes every selected slot now; the lazy queue
@@ -247,6 +309,9 @@ class AuditStep:
         ``timer`` (optional) gets ``timer.mark(name)`` calls between the launches of each
         stage, on the current stream, for per-stage event timing. The launches are made by the
         C++ host module; ``native=False`` makes the same launches from Python (a cross-check).
+        ``transport`` (a RecallTransport, native launches only): the rows the step removes are
+        packed for its archive before the compaction, as remove_positions archives them
+        (cache.py:110-112); the queued slots follow with each evict_prefix batch given it.
         """
         if pool_kernel <= 0 or pool_kernel % 2 == 0:
             raise ValueError("pool kernel must be a positive odd integer")
@@ -254,12 +319,14 @@ class AuditStep:
         if immediate < -1:
             raise ValueError("immediate must be non-negative")
         if not native:
+            if transport is not None:
+                raise ValueError("archiving an audit's removals needs the native launcher")
             return self._run_python(layers, query_positions, margin, count, protect_recent,
                                     pool_kernel, denominator_epsilon, check_finite, queue_order,
                                     timer, immediate)
         return self._run_native(layers, query_positions, margin, count, protect_recent,
                                 pool_kernel, denominator_epsilon, check_finite, timer,
-                                queue_order, immediate)
+                                queue_order, immediate, transport)
 
     def _run_python(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
                     denominator_epsilon, check_finite, queue_order, timer, immediate=-1):
@@ -441,7 +508,7 @@ class AuditStep:
 
     def _run_native(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
                     denominator_epsilon, check_finite, timer=None, queue_order=False,
-                    immediate=-1):
+                    immediate=-1, transport=None):
         """The step with planning and every launch done by the C++ host module
         (csrc/host_plan.cpp audit_launch): no Python between the launches. With
         ``queue_order`` the queue half of the selection runs on a side stream after the
@@ -465,14 +532,15 @@ class AuditStep:
                     inner(name)
         (block, meta, segment_info, head_info, scores, info, quotas, offsets, removed, changed,
          out_keys, out_values, out_positions, device_block, select_ws,
-         queue_state) = planner.audit_launch(
+         queue_state, layout) = planner.audit_launch(
             [layer.keys for layer in layers], [layer.values for layer in layers],
             [layer.positions for layer in layers], [layer.queries for layer in layers],
             [layer.gradient for layer in layers], [list(layer.head_lens) for layer in layers],
             [None if layer.prompt_lens is None else list(layer.prompt_lens) for layer in layers],
             int(protect_recent), query_positions, margin, int(count), int(immediate),
             int(pool_kernel), float(denominator_epsilon),
-            torch.cuda.current_stream(device).cuda_stream, mark, sync)
+            torch.cuda.current_stream(device).cuda_stream, mark, sync,
+            _archive_hook(transport, layers[0].keys, _removed_now(layers, count, immediate)))
         plan = SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
         total = plan.total
         count = min(max(0, int(count)), total)
@@ -484,7 +552,7 @@ class AuditStep:
             kept, offsets_out = sync.wait(check_finite)
             if immediate:
                 new_layers = PackedLayers(out_keys, out_values, out_positions, kept, offsets_out,
-                                          layers)
+                                          layers, DeviceLayout(layout, kept))
             else:
                 new_layers = list(layers)
             queue = EvictionQueue(values, order, rank, quotas, offsets, removed,
@@ -503,6 +571,7 @@ class AuditStep:
                     timer.mark("queue_join")
         # waits for the selection only; the compaction may still run (outputs in stream order)
         kept, offsets = sync.wait(check_finite)
-        new_layers = PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers)
+        new_layers = PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers,
+                                  None if layout is None else DeviceLayout(layout, kept))
         return AuditOutcome(new_layers, [list(lengths) for lengths in kept], scores[:total],
                             scores[total:], selection, plan, count)

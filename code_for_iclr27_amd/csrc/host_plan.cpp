@@ -229,7 +229,7 @@ struct Library {
   decltype(&lr_select_refine_queue) select_refine_queue = nullptr;
   decltype(&lr_queue_index) queue_index = nullptr;
   decltype(&lr_queue_evict_plan) queue_evict_plan = nullptr;
-  decltype(&lr_compact_heads) compact_heads = nullptr;
+  decltype(&lr_compact_heads_layout) compact_heads = nullptr;
   decltype(&lr_append) append = nullptr;
   decltype(&lr_compact) compact = nullptr;
   decltype(&lr_append_layers) append_layers = nullptr;
@@ -284,6 +284,30 @@ void check_call(int status) {
 }
 
 inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
+
+// The recall archive's hook of a fused layout change (None: no transport): called with the
+// device addresses of the head table and of the removal sets the compaction is about to read,
+// so that the removed rows are packed for the archive before the compaction is enqueued, as
+// remove_positions calls record_evicted first (src/lazy_recall/cache.py:110-112). Arguments:
+// (head table, slots, heads per layer, quotas, offsets, positions, rows removed, most rows
+// removed from one slot).
+void archive_removals(const py::object& archive, const int64_t* head_table, int64_t slots,
+                      int64_t heads_per_layer, const int64_t* quotas, const int64_t* offsets,
+                      const int64_t* positions, int64_t count, int64_t max_rows) {
+  if (archive.is_none() || count <= 0) return;
+  auto address = [](const void* p) { return static_cast<int64_t>(reinterpret_cast<uintptr_t>(p)); };
+  archive(address(head_table), slots, heads_per_layer, address(quotas), address(offsets),
+          address(positions), count, max_rows);
+}
+
+// Device block for the per-layer metadata a compaction or reinsertion writes: the new length
+// of every (layer, head) slot (i32 [layers * heads]), then each layer's cumulative lengths
+// (i32 [layers, heads + 1]). Views of it are what the reference keeps as metadata.head_lens and
+// metadata.cu_seqlens_k (src/lazy_recall/cache.py:171-177).
+torch::Tensor new_layout(int64_t layers, int64_t heads, const torch::Device& device) {
+  return torch::empty({layers * heads + layers * (heads + 1)},
+                      torch::TensorOptions().device(device).dtype(torch::kInt32));
+}
 
 // The host side of an audit step's two copies and its one wait.
 //  - upload(): the metadata block goes through this object's pinned, host-coherent staging
@@ -376,6 +400,15 @@ struct StepSync {
     pending = true;
   }
 
+  // Drops a posted step whose launch sequence failed after post(): waits for its selection
+  // (which writes `info`) so that the buffers may be reused.
+  void abandon() {
+    if (!pending) return;
+    pending = false;
+    py::gil_scoped_release release;
+    ready.synchronize();
+  }
+
   void post(const Plan& plan, const torch::Device& device, bool removes = true) {
     const int64_t* slot = plan.head_info.data_ptr<int64_t>();
     post_slots(slot, slot + plan.slots, plan.slots, plan.layers, plan.segments, removes, device);
@@ -444,7 +477,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        int64_t protect_recent, const torch::Tensor& query_positions,
                        const torch::Tensor& margin, int64_t count, int64_t immediate,
                        int64_t pool_kernel, double epsilon, int64_t stream_handle,
-                       const py::object& mark, StepSync* sync) {
+                       const py::object& mark, StepSync* sync, const py::object& archive) {
   require(library.score_segments != nullptr, "library entry points are not bound");
   require(pool_kernel > 0 && pool_kernel % 2 == 1, "pool kernel must be a positive odd integer");
   // with a StepSync the block goes through its staging buffer, so it need not be pinned
@@ -515,6 +548,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   }
   torch::Tensor sets, quotas, offsets, removed, changed, select_ws;
   torch::Tensor queue_values, queue_order, queue_rank, batch;
+  torch::Tensor layout;  // device i32: head lengths [slots], then cumulative [layers, H + 1]
   if (lazy) {
     const size_t select_bytes = library.select_workspace_bytes(plan.total, S, count);
     select_ws = torch::empty({static_cast<int64_t>(select_bytes)}, on_device.dtype(torch::kUInt8));
@@ -553,11 +587,21 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
     stage("select");
     if (sync != nullptr) sync->post(plan, device, /*removes=*/immediate > 0);
     if (immediate > 0) {  // with nothing to remove now the layers stay as they are
+      try {
+        archive_removals(archive, words + plan.heads_at(), plan.slots, plan.slots / plan.layers,
+                         batch_quotas, offsets.data_ptr<int64_t>(), batch_positions, immediate,
+                         std::min(immediate, plan.max_candidates));
+      } catch (...) {
+        if (sync != nullptr) sync->abandon();
+        throw;
+      }
+      layout = new_layout(plan.layers, plan.slots / plan.layers, device);
       check_call(library.compact_heads(
           words + plan.heads_at(), plan.slots, batch_quotas, offsets.data_ptr<int64_t>(),
           batch_positions, plan.dim, static_cast<int>(keys[0].element_size()),
           plan.max_head_length, out_rows, dptr(out_keys), dptr(out_values),
-          out_positions.data_ptr<float>(), stream));
+          out_positions.data_ptr<float>(), plan.slots / plan.layers,
+          layout.data_ptr<int32_t>(), layout.data_ptr<int32_t>() + plan.slots, stream));
       stage("compact");
     }
   } else if (count > 0) {
@@ -576,11 +620,21 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
         nonfinite, stream));
     stage("select");
     if (sync != nullptr) sync->post(plan, device);
+    try {
+      archive_removals(archive, words + plan.heads_at(), plan.slots, plan.slots / plan.layers,
+                       quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
+                       removed.data_ptr<int64_t>(), count, std::min(count, plan.max_candidates));
+    } catch (...) {
+      if (sync != nullptr) sync->abandon();
+      throw;
+    }
+    layout = new_layout(plan.layers, plan.slots / plan.layers, device);
     check_call(library.compact_heads(
         words + plan.heads_at(), plan.slots, quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
         removed.data_ptr<int64_t>(), plan.dim, static_cast<int>(keys[0].element_size()),
         plan.max_head_length, out_rows, dptr(out_keys), dptr(out_values),
-        out_positions.data_ptr<float>(), stream));
+        out_positions.data_ptr<float>(), plan.slots / plan.layers, layout.data_ptr<int32_t>(),
+        layout.data_ptr<int32_t>() + plan.slots, stream));
     stage("compact");
   } else {
     if (sync != nullptr) {
@@ -597,9 +651,11 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   }
   py::object queue = py::none();
   if (lazy) queue = py::make_tuple(queue_values, queue_order, queue_rank);
+  py::object layout_out = py::none();
+  if (layout.defined()) layout_out = py::cast(layout);
   return py::make_tuple(plan.block, plan.meta(), plan.segment_info, plan.head_info, scores, info,
                         quotas, offsets, removed, changed, out_keys, out_values, out_positions,
-                        block, select_ws, queue);
+                        block, select_ws, queue, layout_out);
 }
 
 // One evict_prefix batch (controller.py:57-70) on the device: removes the queued slots
@@ -620,7 +676,8 @@ py::tuple queue_evict_launch(const std::vector<torch::Tensor>& keys,
                              const torch::Tensor& offsets, const torch::Tensor& removed,
                              const torch::Tensor& rank, const torch::Tensor& segments_host,
                              int64_t begin, int64_t end, int64_t stream_handle, StepSync* sync,
-                             const std::vector<int64_t>& packed_offsets) {
+                             const std::vector<int64_t>& packed_offsets,
+                             const py::object& archive) {
   require(library.queue_evict_plan != nullptr, "library entry points are not bound");
   require(sync != nullptr, "an evict_prefix batch needs a StepSync");
   // Packed form (an audit's or a batch's own output): one K, V and positions tensor holding
@@ -724,12 +781,17 @@ py::tuple queue_evict_launch(const std::vector<torch::Tensor>& keys,
   torch::Tensor out_keys = torch::empty({out_rows, dim}, kv);
   torch::Tensor out_values = torch::empty({out_rows, dim}, kv);
   torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
+  archive_removals(archive, head_table.data_ptr<int64_t>(), slots, heads, batch_quotas,
+                   offsets.data_ptr<int64_t>(), batch_positions, end - begin,
+                   *std::max_element(leaving.begin(), leaving.end()));
+  torch::Tensor layout = new_layout(static_cast<int64_t>(layers), heads, device);
   check_call(library.compact_heads(head_table.data_ptr<int64_t>(), slots, batch_quotas,
                                    offsets.data_ptr<int64_t>(), batch_positions, dim,
                                    static_cast<int>(keys[0].element_size()), max_length, out_rows,
                                    dptr(out_keys), dptr(out_values), out_positions.data_ptr<float>(),
-                                   stream));
-  return py::make_tuple(out_keys, out_values, out_positions, kept, layer_offsets);
+                                   heads, layout.data_ptr<int32_t>(),
+                                   layout.data_ptr<int32_t>() + slots, stream));
+  return py::make_tuple(out_keys, out_values, out_positions, kept, layer_offsets, layout);
 }
 
 // Host planning of a reinsertion (insert_payload, cache.py:201-253, for every layer): checks the

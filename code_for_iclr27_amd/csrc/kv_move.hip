@@ -486,7 +486,8 @@ __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
     const int64_t* __restrict__ head_table, const int64_t* __restrict__ quotas,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ removed_positions,
     RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
-    float* __restrict__ out_positions) {
+    float* __restrict__ out_positions, int64_t heads_per_layer, int32_t* __restrict__ head_lens,
+    int32_t* __restrict__ cumulative) {
   __shared__ int64_t partial[kThreads / 64];
   const int64_t head = blockIdx.y;
   const int64_t* row = head_table + head * LR_HEAD_WORDS;
@@ -494,6 +495,19 @@ __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
   const int64_t removed_count = segment >= 0 ? quotas[segment] : 0;
   const int64_t rows_out = length - removed_count;
   const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kCompactRows;
+  if (head_lens != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    // the layer's new metadata (cache.py:171-177): this head's length and its end in the
+    // layer's cumulative lengths; the layer's first head also writes the leading 0
+    const int64_t layer = head / heads_per_layer, h = head - layer * heads_per_layer;
+    int64_t end = 0;
+    for (int64_t k = layer * heads_per_layer; k <= head; ++k) {
+      const int64_t* other = head_table + k * LR_HEAD_WORDS;
+      end += other[3] - (other[4] >= 0 ? quotas[other[4]] : 0);
+    }
+    head_lens[head] = static_cast<int32_t>(rows_out);
+    cumulative[layer * (heads_per_layer + 1) + h + 1] = static_cast<int32_t>(end);
+    if (h == 0) cumulative[layer * (heads_per_layer + 1)] = 0;
+  }
   if (d0 >= rows_out) return;  // uniform across the block, before any barrier
   // output start of this head slot
   int64_t before = 0;
@@ -539,11 +553,24 @@ __global__ __launch_bounds__(kThreads) void reinsert_plan_kernel(
     const int64_t* __restrict__ table, const int64_t* __restrict__ grouped,
     int64_t* __restrict__ sorted_position, int64_t* __restrict__ sorted_source,
     int64_t* __restrict__ sorted_destination, int64_t* __restrict__ recalled_rows, int64_t count,
-    int32_t* __restrict__ flag) {
+    int32_t* __restrict__ flag, int64_t heads_per_layer, int32_t* __restrict__ head_lens,
+    int32_t* __restrict__ cumulative) {
   __shared__ int64_t key[kReinsertMax];
   __shared__ int64_t value[kReinsertMax];
-  const int64_t* entry = table + static_cast<int64_t>(blockIdx.x) * LR_REINSERT_WORDS;
+  const int64_t slot = blockIdx.x;
+  const int64_t* entry = table + slot * LR_REINSERT_WORDS;
   const int64_t first = entry[4], r = entry[5];
+  if (head_lens != nullptr && threadIdx.x == 0) {
+    // the layer's new metadata (replace_head_lens after insert_payload, cache.py:246): this
+    // head's merged length and its end in the layer's cumulative lengths
+    const int64_t layer = slot / heads_per_layer, h = slot - layer * heads_per_layer;
+    int64_t end = 0;
+    for (int64_t k = layer * heads_per_layer; k <= slot; ++k)
+      end += table[k * LR_REINSERT_WORDS + 3] + table[k * LR_REINSERT_WORDS + 5];
+    head_lens[slot] = static_cast<int32_t>(entry[3] + r);
+    cumulative[layer * (heads_per_layer + 1) + h + 1] = static_cast<int32_t>(end);
+    if (h == 0) cumulative[layer * (heads_per_layer + 1)] = 0;
+  }
   if (r == 0) return;
   if (r > kReinsertMax) {
     if (threadIdx.x == 0) atomicOr(flag, 8);
@@ -881,48 +908,82 @@ extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
   });
 }
 
-extern "C" int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* quotas,
-                                const int64_t* offsets, const int64_t* removed_positions,
-                                int64_t dim, int elem_bytes, int64_t max_length,
-                                int64_t total_out_rows, void* out_keys, void* out_values,
-                                float* out_positions, void* stream) {
+extern "C" int lr_compact_heads_layout(const int64_t* head_table, int64_t heads,
+                                       const int64_t* quotas, const int64_t* offsets,
+                                       const int64_t* removed_positions, int64_t dim,
+                                       int elem_bytes, int64_t max_length, int64_t total_out_rows,
+                                       void* out_keys, void* out_values, float* out_positions,
+                                       int64_t heads_per_layer, int32_t* head_lens,
+                                       int32_t* cumulative, void* stream) {
   clear_error();
   LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Invalid KV layout");
   LR_REQUIRE(heads > 0 && heads <= 65535 && max_length >= 0, "Invalid head table");
-  if (total_out_rows == 0 || max_length == 0) return LR_OK;
-  LR_REQUIRE(head_table && quotas && offsets && removed_positions && out_keys && out_values &&
-                 out_positions,
+  const bool layout_out = head_lens != nullptr;
+  LR_REQUIRE(!layout_out || (cumulative != nullptr && heads_per_layer > 0 &&
+                             heads % heads_per_layer == 0),
+             "Invalid head table");
+  if (!layout_out && (total_out_rows == 0 || max_length == 0)) return LR_OK;
+  LR_REQUIRE(head_table && quotas && offsets && removed_positions &&
+                 (total_out_rows == 0 || (out_keys && out_values && out_positions)),
              "Expected contiguous CUDA tensor");
+  LR_REQUIRE(total_out_rows < (int64_t{1} << 31) || !layout_out,
+             "Cumulative lengths exceed int32");
   const int64_t row_bytes = dim * elem_bytes;
   // Head rows are whole rows of 256-byte aligned allocations; the outputs bound the granule.
-  const int g = granule_for(row_bytes, {out_keys, out_values});
+  const int g = total_out_rows > 0 ? granule_for(row_bytes, {out_keys, out_values})
+                                   : granule_for(row_bytes, {});
   LR_REQUIRE(max_length < (int64_t{1} << 31), "Invalid head table");
-  const RowLayout layout = make_layout(row_bytes, g, total_out_rows, 8);
-  const int64_t bx = ceil_div(max_length, kCompactRows);
+  const RowLayout layout = make_layout(row_bytes, g, total_out_rows > 0 ? total_out_rows : 1, 8);
+  int64_t bx = ceil_div(max_length, kCompactRows);
+  if (bx < 1) bx = 1;  // block 0 of every head writes the layout
   LR_REQUIRE(bx <= 65535, "Invalid head table");
   dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(heads));
   return dispatch_granule(g, [&]<int G>() {
     compact_heads_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
         head_table, quotas, offsets, removed_positions, layout, bytes(out_keys),
-        bytes(out_values), out_positions);
+        bytes(out_values), out_positions, layout_out ? heads_per_layer : 1, head_lens,
+        cumulative);
     return check_launch("compact_heads");
   });
 }
 
-extern "C" int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64_t* grouped,
-                                int64_t count, int64_t* workspace, int64_t* recalled_rows,
-                                int32_t* flag, void* stream) {
+extern "C" int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* quotas,
+                                const int64_t* offsets, const int64_t* removed_positions,
+                                int64_t dim, int elem_bytes, int64_t max_length,
+                                int64_t total_out_rows, void* out_keys, void* out_values,
+                                float* out_positions, void* stream) {
+  return lr_compact_heads_layout(head_table, heads, quotas, offsets, removed_positions, dim,
+                                 elem_bytes, max_length, total_out_rows, out_keys, out_values,
+                                 out_positions, 0, nullptr, nullptr, stream);
+}
+
+extern "C" int lr_reinsert_plan_layout(const int64_t* table, int64_t slots,
+                                       const int64_t* grouped, int64_t count, int64_t* workspace,
+                                       int64_t* recalled_rows, int32_t* flag,
+                                       int64_t heads_per_layer, int32_t* head_lens,
+                                       int32_t* cumulative, void* stream) {
   clear_error();
   LR_REQUIRE(slots > 0 && slots <= (int64_t{1} << 31) - 1 && count >= 0 &&
                  count < (int64_t{1} << 40),
              "Invalid reinsert layout");
   LR_REQUIRE(table && flag && (count == 0 || (grouped && workspace && recalled_rows)),
              "Expected contiguous CUDA tensor");
-  if (count == 0) return LR_OK;
+  const bool layout_out = head_lens != nullptr;
+  LR_REQUIRE(!layout_out || (cumulative != nullptr && heads_per_layer > 0 &&
+                             slots % heads_per_layer == 0),
+             "Invalid reinsert layout");
+  if (count == 0 && !layout_out) return LR_OK;
   reinsert_plan_kernel<<<static_cast<unsigned>(slots), kThreads, 0, as_stream(stream)>>>(
       table, grouped, workspace, workspace + count, workspace + 2 * count, recalled_rows, count,
-      flag);
+      flag, layout_out ? heads_per_layer : 1, head_lens, cumulative);
   return check_launch("reinsert_plan");
+}
+
+extern "C" int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64_t* grouped,
+                                int64_t count, int64_t* workspace, int64_t* recalled_rows,
+                                int32_t* flag, void* stream) {
+  return lr_reinsert_plan_layout(table, slots, grouped, count, workspace, recalled_rows, flag, 0,
+                                 nullptr, nullptr, stream);
 }
 
 extern "C" int lr_reinsert_resident(const int64_t* table, int64_t slots, const int64_t* workspace,

@@ -25,13 +25,13 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import List, Sequence
+from typing import List, Optional, Sequence
 
 import numpy as np
 import torch
 
 from . import _lib
-from .audit import PackedLayers
+from .audit import DeviceLayout, PackedLayers
 from .scoring import LayerState, _planner
 
 _FLAG_DUPLICATE, _FLAG_HEAD_LIMIT = 1, 8
@@ -43,6 +43,17 @@ class ReinsertOutcome:
     head_lens: List[List[int]]
     recalled_rows: torch.Tensor   # i64 [M] (device): row of each recalled entry in its merged head
     inserted: int
+    # Recorded on the side stream after the copy of a caller-owned pinned host payload: the
+    # payload buffer is read until it completes, so the caller must not refill or free it
+    # before (payload_copied.synchronize(), or a stream wait on it). None when nothing of the
+    # caller's is read after run() returns (a device payload, or an unpinned one, which run()
+    # stages through pinned memory of its own).
+    payload_copied: Optional[torch.cuda.Event] = None
+
+    @property
+    def layout(self) -> DeviceLayout:
+        """The merged layers' metadata on the device (head_lens, cu_seqlens_k, max_seqlen_k)."""
+        return self.layers.layout
 
 
 class Reinserter:
@@ -81,7 +92,8 @@ class Reinserter:
         device memory) with identities metadata [M, 3] = (layer, head, position) into
         ``layers`` (a list of LayerState or a PackedLayers). Returns the merged layers; raises
         before returning, as the reference does, if an identity is already resident or
-        repeated. The merges are enqueued on the current stream."""
+        repeated. The merges are enqueued on the current stream. A pinned host payload is still
+        being read when run() returns: ``outcome.payload_copied`` marks the end of its copy."""
         metadata = np.ascontiguousarray(np.asarray(metadata, dtype=np.int64).reshape(-1, 3))
         count = len(metadata)
         if tuple(payload.shape[:2]) != (count, 2):
@@ -140,9 +152,13 @@ class Reinserter:
         current.wait_event(planned_in)
         host_flag = self._host_flag(device)
         table = block_device.data_ptr()
-        _lib.call("lr_reinsert_plan", table, slots,
+        heads = len(lengths[0])
+        layout = torch.empty((slots + len(lengths) * (heads + 1),), dtype=torch.int32,
+                             device=device)
+        _lib.call("lr_reinsert_plan_layout", table, slots,
                   table + 8 * slots * _lib.LR_REINSERT_WORDS if count else None, count,
-                  workspace.data_ptr(), _lib.ptr(recalled_rows), flag.data_ptr(), stream)
+                  workspace.data_ptr(), _lib.ptr(recalled_rows), flag.data_ptr(), heads,
+                  layout.data_ptr(), layout.data_ptr() + 4 * slots, stream)
         _lib.call("lr_copy_words", flag.data_ptr(), host_flag, 1, stream)
         planned = torch.cuda.Event()
         planned.record(current)
@@ -161,8 +177,11 @@ class Reinserter:
         if word & _FLAG_HEAD_LIMIT:
             raise ValueError("Too many recalled rows for one head")
         merged = PackedLayers(out_keys, out_values, out_positions, new_lens, offsets,
-                              layers.sources if packed else list(layers))
-        return ReinsertOutcome(merged, new_lens, recalled_rows, count)
+                              layers.sources if packed else list(layers),
+                              DeviceLayout(layout, new_lens))
+        caller_buffer = not on_device and source is payload
+        return ReinsertOutcome(merged, new_lens, recalled_rows, count,
+                               payload_ready if caller_buffer else None)
 
 
 _default = Reinserter()

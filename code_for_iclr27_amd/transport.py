@@ -236,6 +236,46 @@ class RecallTransport:
         self.counters["archive_batches"] += 1
         self.counters["d2h_bytes"] += count * (2 * self.dimension * 2 + 3 * 8)
 
+    @torch.no_grad()
+    def record_evicted_heads(self, head_table, slots, heads_per_layer, quotas, offsets,
+                             positions, count, max_rows):
+        """record_evicted for a fused layout change (an audit's removals or an evict_prefix
+        batch), whose removal sets are already on the device: the same capacity check, slot,
+        pack layout, commit and counters, with the rows packed by lr_pack_heads straight from
+        the sets the compaction reads (device addresses; ``count`` rows, at most ``max_rows``
+        from one (layer, head)), on the current stream. The reference packs the same rows from
+        host removals (transport.py:129-177)."""
+        self.pump()
+        count = int(count)
+        if count == 0:
+            return
+        if slots != self.layers * self.heads or heads_per_layer != self.heads:
+            raise RuntimeError("Recall configuration does not match the cache")
+        if count > self.capacity:
+            self.counters["archive_overflows"] += 1
+            raise RuntimeError("Eviction batch exceeds configured archive staging capacity")
+        library = load()
+        slot, waited = ctypes.c_int(-1), ctypes.c_int(0)
+        status = library.lrr_acquire_archive(self._ring, self.timeout, ctypes.byref(slot),
+                                             ctypes.byref(waited))
+        if waited.value:
+            self.counters["archive_backpressure"] += 1
+        _check(status)
+        slot = slot.value
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        try:
+            _lib.call("lr_pack_heads", head_table, slots, heads_per_layer, quotas, offsets,
+                      positions, int(max_rows), self.dimension, self.capacity,
+                      self.archive_gpu[slot].data_ptr(), self.archive_meta_gpu[slot].data_ptr(),
+                      stream)
+            _check(library.lrr_commit_archive(self._ring, slot, count, stream))
+        except BaseException:
+            library.lrr_abandon_archive(self._ring, slot)
+            raise
+        self.counters["archived_vectors"] += count
+        self.counters["archive_batches"] += 1
+        self.counters["d2h_bytes"] += count * (2 * self.dimension * 2 + 3 * 8)
+
     def _pack(self, cache, batch, slot):
         """One upload (layer pointer table + row descriptors) and one lr_pack_layers launch."""
         L, count = self.layers, len(batch)

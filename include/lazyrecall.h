@@ -132,6 +132,21 @@ int lr_batch_append(const int64_t* descriptors, int64_t segments, const void* ne
 int lr_pack_layers(const int64_t* layer_table, int64_t layers, const int64_t* rows,
                    int64_t count, int64_t dim, void* payload, int64_t* metadata, void* stream);
 
+/* The eviction batch of a fused layout change, packed on the device from the removal sets the
+ * following lr_compact_heads(_layout) call reads: LazyRecallCache.remove_positions archives
+ * its removals with transport.record_evicted before compacting (src/lazy_recall/cache.py:
+ * 110-112; transport.py:129-177), which needs the removals on the host. head_table as
+ * lr_compact_heads (LR_HEAD_WORDS per slot, layer-major, heads_per_layer per layer); slot s
+ * with segment g >= 0 removes quotas[g] positions at positions[offsets[g]...] (ascending).
+ * Writes payload [*, 2, dim] (2-byte key row, value row) and metadata [*, 3] i64 = (layer,
+ * head, int64(position)) in (layer, head, position) order, at most `capacity` rows; max_rows
+ * bounds any one slot's removals (it sizes the grid). payload 16-byte aligned, dim * 2 a
+ * multiple of 16. */
+int lr_pack_heads(const int64_t* head_table, int64_t slots, int64_t heads_per_layer,
+                  const int64_t* quotas, const int64_t* offsets, const int64_t* positions,
+                  int64_t max_rows, int64_t dim, int64_t capacity, void* payload,
+                  int64_t* metadata, void* stream);
+
 /* Group-mean decode queries of every layer (src/lazy_recall/recall/transport.py:293-296: the
  * last decode query [Hq, d] of each layer viewed as [H, G, d] and averaged over G in f32).
  * query_table: DEVICE [layers, 2] i64 = (queries ptr, query-head stride in elements);
@@ -292,6 +307,18 @@ int lr_compact_heads(const int64_t* head_table, int64_t heads, const int64_t* qu
                      const int64_t* offsets, const int64_t* removed_positions, int64_t dim,
                      int elem_bytes, int64_t max_length, int64_t total_out_rows,
                      void* out_keys, void* out_values, float* out_positions, void* stream);
+/* lr_compact_heads plus the compacted layers' metadata on the device, written by the same
+ * launch (the per-layer rebuild of metadata.head_lens / metadata.cu_seqlens_k after a
+ * compaction, src/lazy_recall/cache.py:171-177, without its host-to-device copies). The head
+ * slots are layer-major with heads_per_layer heads per layer. head_lens: device i32
+ * [heads] (the new length of every slot); cumulative: device i32 [layers, heads_per_layer + 1]
+ * (per layer 0 then the running sum). With head_lens NULL it is lr_compact_heads. */
+int lr_compact_heads_layout(const int64_t* head_table, int64_t heads, const int64_t* quotas,
+                            const int64_t* offsets, const int64_t* removed_positions,
+                            int64_t dim, int elem_bytes, int64_t max_length,
+                            int64_t total_out_rows, void* out_keys, void* out_values,
+                            float* out_positions, int64_t heads_per_layer, int32_t* head_lens,
+                            int32_t* cumulative, void* stream);
 
 /* The lazy eviction queue (src/lazy_recall/controller.py:140-159 keeps references[immediate:]
  * after removing the first `immediate`; controller.py:57-70 evict_prefix removes the next
@@ -341,6 +368,15 @@ int lr_queue_evict_plan(const int64_t* quotas, const int64_t* offsets,
 #define LR_REINSERT_MAX_PER_HEAD 4096
 int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64_t* grouped, int64_t count,
                      int64_t* workspace, int64_t* recalled_rows, int32_t* flag, void* stream);
+/* lr_reinsert_plan plus the merged layers' metadata on the device, written by the same
+ * launch (LazyRecallCache.insert_payload's replace_head_lens, src/lazy_recall/cache.py:246,
+ * without its host-to-device copies): head_lens i32 [slots] and cumulative i32
+ * [layers, heads_per_layer + 1], as lr_compact_heads_layout. With head_lens NULL it is
+ * lr_reinsert_plan; with it, the launch also runs when count is 0. */
+int lr_reinsert_plan_layout(const int64_t* table, int64_t slots, const int64_t* grouped,
+                            int64_t count, int64_t* workspace, int64_t* recalled_rows,
+                            int32_t* flag, int64_t heads_per_layer, int32_t* head_lens,
+                            int32_t* cumulative, void* stream);
 int lr_reinsert_resident(const int64_t* table, int64_t slots, const int64_t* workspace,
                          int64_t count, int64_t max_length, int64_t dim, int elem_bytes,
                          int64_t out_rows, void* out_keys, void* out_values, float* out_positions,

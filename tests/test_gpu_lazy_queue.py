@@ -189,3 +189,70 @@ def test_lazy_window_full_size(device):
         np.testing.assert_array_equal(bits(current[l].values), oracle.values[l])
         np.testing.assert_array_equal(current[l].positions.cpu().numpy().reshape(-1),
                                       oracle.positions[l])
+
+
+def staged_rows(oracle, removals):
+    """What record_evicted archives for `removals` of the oracle's current cache: (layer, head,
+    int64 position) and the K, V rows, in (layer, head, position) order (transport.py:141-167)."""
+    meta, payload = [], []
+    for l, h in sorted(removals):
+        starts = np.concatenate(([0], np.cumsum(oracle.lens[l])))
+        for position in sorted(int(p) for p in removals[(l, h)]):
+            row = starts[h] + position
+            meta.append((l, h, int(oracle.positions[l][row])))
+            payload.append(np.stack([oracle.keys[l][row], oracle.values[l][row]]))
+    return np.asarray(meta, np.int64).reshape(-1, 3), np.asarray(payload, np.int16)
+
+
+def check_staged(transport, meta, payload, archived_before):
+    """The batch the transport just committed (one archive slot: slot 0), bit-exact."""
+    transport.wait_pending()
+    n = len(meta)
+    assert transport.counters["archived_vectors"] == archived_before + n
+    assert transport.counters["indexed_vectors"] == archived_before + n
+    np.testing.assert_array_equal(transport.archive_meta_gpu[0][:n].cpu().numpy(), meta)
+    np.testing.assert_array_equal(transport.archive_gpu[0][:n].view(torch.int16).cpu().numpy(),
+                                  payload)
+    return archived_before + n
+
+
+@pytest.mark.parametrize("immediate", [None, 150])
+def test_fused_removals_feed_the_recall_archive(device, immediate):
+    """With a RecallTransport attached, the audit's removals (all of them, or the lazy form's
+    first `immediate`) and every evict_prefix batch are packed for the archive before their
+    compaction, as remove_positions archives its removals first (cache.py:110-112): each
+    batch's staged payload and metadata bit-exact against the rows the oracle removes, and the
+    worker indexes every one."""
+    from code_for_iclr27_amd.transport import RecallTransport
+
+    head_lengths = [[300, 41, 280, 120], [170, 300, 33, 299], [64, 200, 310, 90]]
+    layers, qpos = workloads.make_layers(head_lengths, 4, 128, 40, device, seed=21)
+    margin = torch.tensor([2.0], device=device)
+    transport = RecallTransport(3, 4, 16, 128, topk=2, archive_buffers=1, cpu_threads=2,
+                                evict_interval=16, timeout_seconds=30.0)  # 192 rows per batch
+    oracle = OracleCache(layers)
+    count = 180 if immediate is None else 900
+    outcome = audit.AuditStep().run(layers, qpos, margin, count, immediate=immediate,
+                                    transport=transport)
+    queue = oracle_queue(outcome, count)
+    now = count if immediate is None else immediate
+    removed_at_audit = {key: np.asarray(v, np.int64) for key, v in queue[:now].groups().items()}
+    archived = check_staged(transport, *staged_rows(oracle, removed_at_audit), 0)
+    oracle.remove(removed_at_audit)
+    oracle.check(outcome.layers, outcome.head_lens)
+    if immediate is not None:
+        queue = queue[immediate:]
+        current = outcome.layers
+        for size in (37, 1, 192):
+            removals, queue = evict_prefix(queue, removed_at_audit, size)
+            expected = staged_rows(oracle, removals)
+            current = outcome.queue.evict_prefix(current, size, transport=transport)
+            archived = check_staged(transport, *expected, archived)
+            oracle.remove(removals)
+            oracle.check(current, current.kept)
+        with pytest.raises(RuntimeError, match="exceeds configured archive staging capacity"):
+            outcome.queue.evict_prefix(current, 193, transport=transport)
+        assert transport.counters["archive_overflows"] == 1
+        current = outcome.queue.evict_prefix(current, 100)  # a batch without the archive
+        assert transport.counters["archived_vectors"] == archived
+    transport.close()
