@@ -227,14 +227,14 @@ def batch_append(keys: List[torch.Tensor], values: List[torch.Tensor],
            and len(positions) == requests and len(lengths) == requests
            and len(logical_positions) == requests, "Request metadata mismatch")
     elem = _elem_bytes(new_keys, "batch_append")
-    from .scoring import _planner
+    from .audit import _native_planner
     with torch.cuda.device(new_keys.device):
         # csrc/host_plan.cpp: the reference's descriptor loop (csrc/batch_append.cu:49-80) and
-        # its checks, then a non-blocking upload from pinned memory (the reference's copy,
-        # csrc/batch_append.cu:81, blocks the host)
-        device_descriptors, rows, maximum = _planner().plan_batch_append(
+        # its checks, then an upload through host-coherent staging and a copy kernel on the
+        # current stream (the reference's copy, csrc/batch_append.cu:81, blocks the host)
+        device_descriptors, rows, maximum = _native_planner().plan_batch_append(
             keys, values, positions, heads, dimension, new_keys.dtype, new_keys.device,
-            lengths, logical_positions)
+            lengths, logical_positions, _lib.stream_of(new_keys))
         output_keys = torch.empty((rows, dimension), dtype=new_keys.dtype, device=new_keys.device)
         output_values = torch.empty_like(output_keys)
         output_positions = torch.empty((rows, 1), dtype=torch.float32, device=new_keys.device)

@@ -1154,19 +1154,73 @@ py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
 // logical position]; same checks, order and messages as the reference's host loop. Returns
 // (descriptors int64 [R*H, 7] already copied to `device` on the current stream (from pinned
 // memory, without blocking the host), total output rows, rows of the longest head + 1).
+// Small per-call metadata blocks (batch_append's descriptors) go to the device the way the
+// audit's block does: written into a pinned, host-coherent staging buffer and copied by a copy
+// kernel (lr_copy_words) on the caller's stream, not by a copy-engine transfer. A ring of
+// buffers per device lets consecutive calls (one per layer in a decode step) proceed without
+// waiting: a buffer is rewritten only after the event recorded behind its copy kernel, which
+// for a ring this long has long completed. The rings live until the process ends (their
+// pinned memory is released with it), so no buffer is freed while the runtime shuts down.
+struct StagingRing {
+  static constexpr size_t kSlots = 64;
+  struct Slot {
+    void* host = nullptr;
+    size_t bytes = 0;
+    c10::Event done{c10::DeviceType::CUDA};
+    bool pending = false;
+  };
+  std::vector<Slot> slots{kSlots};
+  size_t next = 0;
+
+  torch::Tensor upload(const int64_t* words, int64_t count, const torch::Device& device,
+                       void* stream) {
+    Slot& slot = slots[next];
+    next = (next + 1) % kSlots;
+    if (slot.pending) {
+      slot.done.synchronize();
+      slot.pending = false;
+    }
+    const size_t bytes = static_cast<size_t>(count) * sizeof(int64_t);
+    if (slot.bytes < bytes) {
+      if (slot.host != nullptr) check_call(library.staging_free(slot.host));
+      slot.host = nullptr;
+      slot.bytes = 0;
+      check_call(library.staging_alloc(bytes, &slot.host));
+      slot.bytes = bytes;
+    }
+    std::memcpy(slot.host, words, bytes);
+    torch::Tensor block =
+        torch::empty({count}, torch::TensorOptions().device(device).dtype(torch::kInt64));
+    check_call(library.copy_words(static_cast<const int64_t*>(slot.host),
+                                  block.data_ptr<int64_t>(), count, stream));
+    slot.done.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+    slot.pending = true;
+    return block;
+  }
+};
+
+StagingRing& staging_ring(const torch::Device& device) {
+  static std::vector<StagingRing*> rings;
+  const size_t index = static_cast<size_t>(device.index() < 0 ? 0 : device.index());
+  if (rings.size() <= index) rings.resize(index + 1, nullptr);
+  if (rings[index] == nullptr) rings[index] = new StagingRing();  // kept until exit, see above
+  return *rings[index];
+}
+
 py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
                             const std::vector<torch::Tensor>& values,
                             const std::vector<torch::Tensor>& positions, int64_t heads,
                             int64_t dim, torch::ScalarType dtype, const torch::Device& device,
                             const std::vector<std::vector<int64_t>>& lengths,
-                            const std::vector<int64_t>& logical_positions) {
+                            const std::vector<int64_t>& logical_positions,
+                            int64_t stream_handle) {
+  require(library.copy_words != nullptr, "library entry points are not bound");
   const size_t requests = keys.size();
   const int64_t row_bytes = dim * c10::elementSize(dtype);
   int64_t granule = 16;
   while (granule > 1 && row_bytes % granule) granule /= 2;
-  torch::Tensor host = torch::empty({static_cast<int64_t>(requests) * heads, 7},
-                                    torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
-  int64_t* out = host.data_ptr<int64_t>();
+  std::vector<int64_t> host(requests * static_cast<size_t>(heads) * 7);
+  int64_t* out = host.data();
   int64_t destination = 0, maximum = 0;
   for (size_t r = 0; r < requests; ++r) {
     const torch::Tensor &k = keys[r], &v = values[r], &p = positions[r];
@@ -1204,7 +1258,11 @@ py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
     }
     require(source == k.size(0), "Head lengths do not cover cache rows");
   }
-  return py::make_tuple(host.to(device, /*non_blocking=*/true), destination, maximum);
+  void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
+  torch::Tensor block = host.empty()
+      ? torch::empty({0}, torch::TensorOptions().device(device).dtype(torch::kInt64))
+      : staging_ring(device).upload(host.data(), static_cast<int64_t>(host.size()), device, stream);
+  return py::make_tuple(block, destination, maximum);
 }
 
 }  // namespace

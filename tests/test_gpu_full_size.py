@@ -11,8 +11,8 @@ The eviction-queue order is checked exactly at cfg1, cfg3 and cfg4 (where some s
 more than the in-LDS sort's 1024 picks). The scorer's own parity at these sizes is checked on
 sampled heads (cfg0, cfg1, cfg4, and one head of cfg3) against the oracle fed the GPU's logits,
 rtol 1e-5 as in the scorer tests. Agreement with the reference's own tie and GEMM choices is
-measured at cfg1: pooled picks against torch.topk's choice inside tie groups, and the whole
-selection against the reference's GPU path (torch.matmul logits). cfg2's batch append and cfg3's
+measured at cfg1, cfg3 and cfg4: pooled picks against torch.topk's choice inside tie groups,
+and the whole selection against the reference's GPU path (torch.matmul logits). cfg2's batch append and cfg3's
 reinsertion merge run one full-size layer bit-exactly against the oracle.
 """
 
@@ -146,13 +146,26 @@ def _segment_picks(positions, segments, count_segments):
     return [set(positions[order[bounds[s]:bounds[s + 1]]].tolist()) for s in range(count_segments)]
 
 
-def test_pooled_picks_agree_with_torch_topk_up_to_ties(device):
-    """cfg1 at full size: the device selection (ties at a cut to the lower index) against the
-    same selection with CPU torch.topk's choices (the reference's routine), both on the GPU's
+# Agreement with the reference's own choices at full size, and the least fraction each config
+# must reach (the measured fractions are printed; a little below them)
+AGREEMENT = {
+    # name: (pooled picks identical, scores within rtol 1e-5, scores within 1e-2, evicted
+    #        slots identical); measured 0.9977 / 0.9975 / 0.999996 / 0.9976 (cfg1),
+    #        0.9996 / 0.9990 / 0.999991 / 0.9997 (cfg3), 0.9993 / 0.9961 / 0.999983 / 0.9996 (cfg4)
+    "cfg1": (0.995, 0.99, 0.9999, 0.99),
+    "cfg3": (0.995, 0.99, 0.9999, 0.99),
+    "cfg4": (0.995, 0.99, 0.9999, 0.99),
+}
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg3", "cfg4"])
+def test_pooled_picks_agree_with_torch_topk_up_to_ties(device, name):
+    """Full size: the device selection (ties at a cut to the lower index) against the same
+    selection with CPU torch.topk's choices (the reference's routine), both on the GPU's
     scores. The raw allocation agrees exactly; inside a segment every pick that differs has the
     pooled value of that segment's cut (Pool7 plateaus tie there), i.e. lies in the k-th-value
     tie group, where torch.topk's order is unspecified."""
-    cfg = workloads.CONFIGS["cfg1"]
+    cfg = workloads.CONFIGS[name]
     layers, qpos, margin = workloads.make_audit(cfg, device, seed=10, generator_device="cuda")
     outcome = audit.AuditStep().run(layers, qpos, margin, cfg.count, cfg.protect_recent,
                                     cfg.pool_kernel, cfg.epsilon)
@@ -179,19 +192,23 @@ def test_pooled_picks_agree_with_torch_topk_up_to_ties(device):
             segment = pooled[bounds[s]:bounds[s + 1]]
             cut = np.sort(segment)[quota - 1]
             assert np.all(segment[differ - starts[s]] == cut), s
-    print(f"cfg1 pooled picks identical to the torch.topk rule: {same}/{cfg.count} = "
+    print(f"{name} pooled picks identical to the torch.topk rule: {same}/{cfg.count} = "
           f"{same / cfg.count:.6f}; segments with a tie group at the cut where the rules "
           f"choose differently: {tie_segments}/{len(ends)}", flush=True)
+    assert same / cfg.count >= AGREEMENT[name][0]
 
 
-def test_chained_agreement_with_reference_gpu_path(device):
-    """cfg1 at full size: the fused scorer + device selection against the reference's GPU path
+@pytest.mark.parametrize("name", ["cfg1", "cfg3", "cfg4"])
+def test_chained_agreement_with_reference_gpu_path(device, name):
+    """Full size: the fused scorer + device selection against the reference's GPU path
     restated with this package's drop-ins (per head: torch.matmul bf16 logits,
     _C.temporal_probabilities, _C.temporal_risk; then Pool7 and refine_arrays with CPU
     torch.topk). torch's GEMM rounds some logits to the other bf16 neighbour than the MFMA
     sequence does, so scores differ slightly where that happens; the test reports the fraction
-    of scores within rtol 1e-5 and of evicted slots that are identical."""
-    cfg = workloads.CONFIGS["cfg1"]
+    of scores within rtol 1e-5 and of evicted slots that are identical. The reference path
+    chunks its queries by its 64 MiB rule (scoring.py:178-179), so at cfg3 and cfg4 the
+    chunks' scores are combined with torch.maximum as there."""
+    cfg = workloads.CONFIGS[name]
     layers, qpos, margin = workloads.make_audit(cfg, device, seed=11, generator_device="cuda")
     outcome = audit.AuditStep().run(layers, qpos, margin, cfg.count, cfg.protect_recent,
                                     cfg.pool_kernel, cfg.epsilon)
@@ -225,14 +242,15 @@ def test_chained_agreement_with_reference_gpu_path(device):
     removed = outcome.selection.removed_positions.cpu().numpy()
     same = sum(len(set(removed[offsets[s]:offsets[s] + q].tolist()) & expect[s])
                for s, q in enumerate(quotas))
-    print(f"cfg1 chained agreement with the reference GPU path: scores within rtol 1e-5 "
+    print(f"{name} chained agreement with the reference GPU path: scores within rtol 1e-5 "
           f"{close:.6f}, within 1e-2 {near:.6f}, largest relative difference "
           f"{relative.max():.3e}; evicted slots identical {same}/{cfg.count} = "
           f"{same / cfg.count:.6f}; per-head quotas equal in "
           f"{int((quotas == rule.quotas).sum())}/{len(ends)} heads", flush=True)
-    assert close > 0.97
-    assert near > 0.9999
-    assert same / cfg.count > 0.95
+    _, least_close, least_near, least_same = AGREEMENT[name]
+    assert close > least_close
+    assert near > least_near
+    assert same / cfg.count > least_same
 
 
 def test_batch_append_full_size(device):
