@@ -71,6 +71,7 @@ SIGNATURES = {
                                 _P, _P],
     "lr_reinsert_plan": [_P, _I64, _P, _I64, _P, _P, _P, _P],
     "lr_reinsert_plan_layout": [_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _P, _P],
+    "lr_reinsert_group": [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P],
     "lr_reinsert_resident": [_P, _I64, _P, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_reinsert_recalled": [_P, _I64, _P, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_queue_index": [_P, _P, _I64, _P, _P, _P, _I64, _P, _P],

@@ -285,6 +285,59 @@ void check_call(int status) {
 
 inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 
+// Small per-call metadata blocks (batch_append's descriptors) go to the device the way the
+// audit's block does: written into a pinned, host-coherent staging buffer and copied by a copy
+// kernel (lr_copy_words) on the caller's stream, not by a copy-engine transfer. A ring of
+// buffers per device lets consecutive calls (one per layer in a decode step) proceed without
+// waiting: a buffer is rewritten only after the event recorded behind its copy kernel, which
+// for a ring this long has long completed. The rings live until the process ends (their
+// pinned memory is released with it), so no buffer is freed while the runtime shuts down.
+struct StagingRing {
+  static constexpr size_t kSlots = 64;
+  struct Slot {
+    void* host = nullptr;
+    size_t bytes = 0;
+    c10::Event done{c10::DeviceType::CUDA};
+    bool pending = false;
+  };
+  std::vector<Slot> slots{kSlots};
+  size_t next = 0;
+
+  torch::Tensor upload(const int64_t* words, int64_t count, const torch::Device& device,
+                       void* stream) {
+    Slot& slot = slots[next];
+    next = (next + 1) % kSlots;
+    if (slot.pending) {
+      slot.done.synchronize();
+      slot.pending = false;
+    }
+    const size_t bytes = static_cast<size_t>(count) * sizeof(int64_t);
+    if (slot.bytes < bytes) {
+      if (slot.host != nullptr) check_call(library.staging_free(slot.host));
+      slot.host = nullptr;
+      slot.bytes = 0;
+      check_call(library.staging_alloc(bytes, &slot.host));
+      slot.bytes = bytes;
+    }
+    std::memcpy(slot.host, words, bytes);
+    torch::Tensor block =
+        torch::empty({count}, torch::TensorOptions().device(device).dtype(torch::kInt64));
+    check_call(library.copy_words(static_cast<const int64_t*>(slot.host),
+                                  block.data_ptr<int64_t>(), count, stream));
+    slot.done.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+    slot.pending = true;
+    return block;
+  }
+};
+
+StagingRing& staging_ring(const torch::Device& device) {
+  static std::vector<StagingRing*> rings;
+  const size_t index = static_cast<size_t>(device.index() < 0 ? 0 : device.index());
+  if (rings.size() <= index) rings.resize(index + 1, nullptr);
+  if (rings[index] == nullptr) rings[index] = new StagingRing();  // kept until exit, see above
+  return *rings[index];
+}
+
 // The recall archive's hook of a fused layout change (None: no transport): called with the
 // device addresses of the head table and of the removal sets the compaction is about to read,
 // so that the removed rows are packed for the archive before the compaction is enqueued, as
@@ -919,6 +972,77 @@ py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
   return py::make_tuple(block, new_lens, offsets, out_row, max_length);
 }
 
+// The reinsert table for identities already in device memory (lr_reinsert_group fills the
+// rest on the device): checks the layers, writes words [0..3] of every slot (the head's first
+// resident row and its length; [4..7] zero) and uploads the table through the staging ring on
+// `stream`. Nothing here depends on the identities. Returns (device table, resident rows of
+// each layer [L], longest resident head).
+py::tuple reinsert_table(const std::vector<torch::Tensor>& keys,
+                         const std::vector<torch::Tensor>& values,
+                         const std::vector<torch::Tensor>& positions,
+                         const std::vector<std::vector<int64_t>>& head_lens,
+                         const std::vector<int64_t>& packed_offsets, int64_t stream_handle) {
+  require(library.copy_words != nullptr, "library entry points are not bound");
+  const bool packed = !packed_offsets.empty();
+  const size_t layers = head_lens.size();
+  require(layers > 0 && (packed ? packed_offsets.size() == layers + 1 && keys.size() == 1 &&
+                                      values.size() == 1 && positions.size() == 1
+                                : keys.size() == layers && values.size() == layers &&
+                                      positions.size() == layers),
+          "Layer lists differ in length");
+  const int64_t heads = static_cast<int64_t>(head_lens[0].size());
+  require(heads > 0, "Invalid KV layout");
+  const torch::Tensor& k0 = keys[0];
+  require(k0.dim() == 2 && k0.size(1) > 0, "Invalid KV layout");
+  const int64_t dim = k0.size(1);
+  const auto dtype = k0.scalar_type();
+  const torch::Device device = k0.device();
+  const int64_t row_bytes = dim * static_cast<int64_t>(k0.element_size());
+  for (size_t t = 0; t < keys.size(); ++t) {
+    const torch::Tensor &k = keys[t], &v = values[t], &p = positions[t];
+    for (const torch::Tensor* x : {&k, &v, &p})
+      require(x->is_cuda() && x->is_contiguous() && x->device() == device,
+              "Expected contiguous CUDA tensor");
+    require(k.dim() == 2 && k.sizes() == v.sizes() && k.size(1) == dim &&
+                k.scalar_type() == dtype && v.scalar_type() == dtype,
+            "Expected contiguous CUDA tensor");
+    require(p.scalar_type() == torch::kFloat32 && p.numel() == k.size(0),
+            "Position lengths do not match metadata");
+  }
+  const int64_t slots = static_cast<int64_t>(layers) * heads;
+  std::vector<int64_t> table(static_cast<size_t>(slots * LR_REINSERT_WORDS), 0);
+  py::list resident(layers);
+  int64_t max_length = 0;
+  for (size_t l = 0; l < layers; ++l) {
+    require(static_cast<int64_t>(head_lens[l].size()) == heads,
+            "Every layer must have the same number of KV heads");
+    const size_t t = packed ? 0 : l;
+    const int64_t first = packed ? packed_offsets[l] : 0;
+    const int64_t layer_rows = packed ? packed_offsets[l + 1] - first : keys[t].size(0);
+    require(first >= 0 && layer_rows >= 0 && first + layer_rows <= keys[t].size(0),
+            "Position lengths do not match metadata");
+    const int64_t kp = ptr(keys[t]), vp = ptr(values[t]), pp = ptr(positions[t]);
+    int64_t base = first;
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t n = head_lens[l][h];
+      require(n >= 0, "Position lengths do not match metadata");
+      int64_t* row = table.data() + (static_cast<int64_t>(l) * heads + h) * LR_REINSERT_WORDS;
+      row[0] = kp + base * row_bytes;
+      row[1] = vp + base * row_bytes;
+      row[2] = pp + base * 4;
+      row[3] = n;
+      base += n;
+      max_length = std::max(max_length, n);
+    }
+    require(base == first + layer_rows, "Position lengths do not match metadata");
+    resident[l] = py::int_(layer_rows);
+  }
+  void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
+  torch::Tensor block = staging_ring(device).upload(table.data(), static_cast<int64_t>(table.size()),
+                                                    device, stream);
+  return py::make_tuple(block, resident, max_length);
+}
+
 void* current_stream(const torch::Device& device);
 
 // ---------------------------------------------------------------------------------------
@@ -1154,59 +1278,6 @@ py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
 // logical position]; same checks, order and messages as the reference's host loop. Returns
 // (descriptors int64 [R*H, 7] already copied to `device` on the current stream (from pinned
 // memory, without blocking the host), total output rows, rows of the longest head + 1).
-// Small per-call metadata blocks (batch_append's descriptors) go to the device the way the
-// audit's block does: written into a pinned, host-coherent staging buffer and copied by a copy
-// kernel (lr_copy_words) on the caller's stream, not by a copy-engine transfer. A ring of
-// buffers per device lets consecutive calls (one per layer in a decode step) proceed without
-// waiting: a buffer is rewritten only after the event recorded behind its copy kernel, which
-// for a ring this long has long completed. The rings live until the process ends (their
-// pinned memory is released with it), so no buffer is freed while the runtime shuts down.
-struct StagingRing {
-  static constexpr size_t kSlots = 64;
-  struct Slot {
-    void* host = nullptr;
-    size_t bytes = 0;
-    c10::Event done{c10::DeviceType::CUDA};
-    bool pending = false;
-  };
-  std::vector<Slot> slots{kSlots};
-  size_t next = 0;
-
-  torch::Tensor upload(const int64_t* words, int64_t count, const torch::Device& device,
-                       void* stream) {
-    Slot& slot = slots[next];
-    next = (next + 1) % kSlots;
-    if (slot.pending) {
-      slot.done.synchronize();
-      slot.pending = false;
-    }
-    const size_t bytes = static_cast<size_t>(count) * sizeof(int64_t);
-    if (slot.bytes < bytes) {
-      if (slot.host != nullptr) check_call(library.staging_free(slot.host));
-      slot.host = nullptr;
-      slot.bytes = 0;
-      check_call(library.staging_alloc(bytes, &slot.host));
-      slot.bytes = bytes;
-    }
-    std::memcpy(slot.host, words, bytes);
-    torch::Tensor block =
-        torch::empty({count}, torch::TensorOptions().device(device).dtype(torch::kInt64));
-    check_call(library.copy_words(static_cast<const int64_t*>(slot.host),
-                                  block.data_ptr<int64_t>(), count, stream));
-    slot.done.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
-    slot.pending = true;
-    return block;
-  }
-};
-
-StagingRing& staging_ring(const torch::Device& device) {
-  static std::vector<StagingRing*> rings;
-  const size_t index = static_cast<size_t>(device.index() < 0 ? 0 : device.index());
-  if (rings.size() <= index) rings.resize(index + 1, nullptr);
-  if (rings[index] == nullptr) rings[index] = new StagingRing();  // kept until exit, see above
-  return *rings[index];
-}
-
 py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
                             const std::vector<torch::Tensor>& values,
                             const std::vector<torch::Tensor>& positions, int64_t heads,
@@ -1288,6 +1359,8 @@ PYBIND11_MODULE(_plan, module) {
              "packed_attention: checks, output and workspace allocation and launch from C++");
   module.def("reinsert_prepare", &reinsert_prepare,
              "Check a reinsertion and build its pinned table + metadata block");
+  module.def("reinsert_table", &reinsert_table,
+             "Check a reinsertion's layers and upload its table for lr_reinsert_group");
   module.def("plan_batch_append", &plan_batch_append,
              "Validate a batch and upload its batch_append descriptors");
   module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;

@@ -681,6 +681,89 @@ __global__ __launch_bounds__(kThreads) void reinsert_resident_kernel(
   }
 }
 
+// Device grouping of a reinsertion whose identities (metadata [count, 3] i64: layer, head,
+// position) are already in device memory, so that the host never walks them (the reference's
+// merge_plan runs on the host per layer, src/lazy_recall/recall/planning.py:34-52). The host
+// uploads the reinsert table with words [4..7] zero; then:
+//   count: each valid identity adds one to its slot's word [5] (invalid ones set flag bit 2);
+//   table: one workgroup turns the counts into each slot's first recalled entry [4] and first
+//          output row [6] (exclusive prefixes, slot order), clears the cursor [7], copies the
+//          counts to host-coherent memory for the host's layout, and flags (bit 3) a slot past
+//          LR_REINSERT_MAX_PER_HEAD;
+//   group: each valid identity takes the next place of its slot's run (a cursor atomic; the
+//          order inside a run does not matter, the plan sorts each run by position).
+__device__ __forceinline__ bool recall_identity(const int64_t* metadata, int64_t i, int64_t layers,
+                                                int64_t heads, int64_t* slot, int64_t* position) {
+  const int64_t layer = metadata[3 * i], head = metadata[3 * i + 1], p = metadata[3 * i + 2];
+  const bool valid = layer >= 0 && layer < layers && head >= 0 && head < heads && p >= 0 &&
+                     p < (int64_t{1} << 31);
+  *slot = layer * heads + head;
+  *position = p;
+  return valid;
+}
+
+__global__ __launch_bounds__(kThreads) void reinsert_count_kernel(
+    const int64_t* __restrict__ metadata, int64_t count, int64_t layers, int64_t heads,
+    int64_t* __restrict__ table, int32_t* __restrict__ flag) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= count) return;
+  int64_t slot, position;
+  if (!recall_identity(metadata, i, layers, heads, &slot, &position)) {
+    atomicOr(flag, 4);
+    return;
+  }
+  atomicAdd(reinterpret_cast<unsigned long long*>(table + slot * LR_REINSERT_WORDS + 5), 1ull);
+}
+
+__global__ __launch_bounds__(1024) void reinsert_table_kernel(int64_t* __restrict__ table,
+                                                              int64_t slots,
+                                                              int64_t* __restrict__ host_counts,
+                                                              int32_t* __restrict__ flag) {
+  __shared__ int64_t wave_sums[16][2];
+  int64_t carry_run = 0, carry_rows = 0;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int64_t base = 0; base < slots; base += 1024) {
+    const int64_t slot = base + threadIdx.x;
+    int64_t* entry = table + slot * LR_REINSERT_WORDS;
+    const int64_t r = slot < slots ? entry[5] : 0, n = slot < slots ? entry[3] : 0;
+    // inclusive wave scans of (r, n + r), then the waves' totals
+    int64_t run = r, rows = n + r;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t a = __shfl_up(run, o, 64), b = __shfl_up(rows, o, 64);
+      if (lane >= o) run += a, rows += b;
+    }
+    if (lane == 63) wave_sums[wave][0] = run, wave_sums[wave][1] = rows;
+    __syncthreads();
+    int64_t before_run = carry_run, before_rows = carry_rows;
+    for (int w = 0; w < wave; ++w) before_run += wave_sums[w][0], before_rows += wave_sums[w][1];
+    for (int w = 0; w < 16; ++w) carry_run += wave_sums[w][0], carry_rows += wave_sums[w][1];
+    if (slot < slots) {
+      entry[4] = before_run + run - r;
+      entry[6] = before_rows + rows - (n + r);
+      entry[7] = 0;
+      if (host_counts != nullptr) host_counts[slot] = r;
+      if (r > LR_REINSERT_MAX_PER_HEAD) atomicOr(flag, 8);
+    }
+    __syncthreads();  // wave_sums is rewritten by the next round
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void reinsert_group_kernel(
+    const int64_t* __restrict__ metadata, int64_t count, int64_t layers, int64_t heads,
+    int64_t* __restrict__ table, int64_t* __restrict__ grouped) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= count) return;
+  int64_t slot, position;
+  if (!recall_identity(metadata, i, layers, heads, &slot, &position)) return;
+  int64_t* entry = table + slot * LR_REINSERT_WORDS;
+  const int64_t at = static_cast<int64_t>(
+      atomicAdd(reinterpret_cast<unsigned long long*>(entry + 7), 1ull));
+  if (at >= entry[5]) return;  // cannot happen: the count saw the same identities
+  grouped[entry[4] + at] = position;
+  grouped[count + entry[4] + at] = i;
+}
+
 // Recalled rows: sorted entry q copies payload row sorted_source[q] (key half, value half) to
 // output row sorted_destination[q], with its position.
 template <int G>
@@ -984,6 +1067,32 @@ extern "C" int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64
                                 int32_t* flag, void* stream) {
   return lr_reinsert_plan_layout(table, slots, grouped, count, workspace, recalled_rows, flag, 0,
                                  nullptr, nullptr, stream);
+}
+
+extern "C" int lr_reinsert_group(int64_t* table, int64_t slots, int64_t heads,
+                                 const int64_t* metadata, int64_t count, int64_t* grouped,
+                                 int64_t* host_counts, int32_t* flag, void* stream) {
+  clear_error();
+  LR_REQUIRE(slots > 0 && slots <= (int64_t{1} << 31) - 1 && heads > 0 && slots % heads == 0 &&
+                 count >= 0 && count < (int64_t{1} << 40),
+             "Invalid reinsert layout");
+  LR_REQUIRE(table && flag && (count == 0 || (metadata && grouped)),
+             "Expected contiguous CUDA tensor");
+  const hipStream_t s = as_stream(stream);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(count, int64_t{kThreads}));
+  if (count > 0) {
+    reinsert_count_kernel<<<blocks, kThreads, 0, s>>>(metadata, count, slots / heads, heads,
+                                                      table, flag);
+    if (int rc = check_launch("reinsert_count")) return rc;
+  }
+  reinsert_table_kernel<<<1, 1024, 0, s>>>(table, slots, host_counts, flag);
+  if (int rc = check_launch("reinsert_table")) return rc;
+  if (count > 0) {
+    reinsert_group_kernel<<<blocks, kThreads, 0, s>>>(metadata, count, slots / heads, heads, table,
+                                                      grouped);
+    return check_launch("reinsert_group");
+  }
+  return LR_OK;
 }
 
 extern "C" int lr_reinsert_resident(const int64_t* table, int64_t slots, const int64_t* workspace,

@@ -34,7 +34,7 @@ from . import _lib
 from .audit import DeviceLayout, PackedLayers
 from .scoring import LayerState, _planner
 
-_FLAG_DUPLICATE, _FLAG_HEAD_LIMIT = 1, 8
+_FLAG_DUPLICATE, _FLAG_IDENTITY, _FLAG_HEAD_LIMIT = 1, 4, 8
 
 
 @dataclass
@@ -63,6 +63,7 @@ class Reinserter:
     def __init__(self):
         self.streams = {}
         self.flags = {}
+        self.counts = {}
 
     def _side_stream(self, device) -> torch.cuda.Stream:
         stream = self.streams.get(device)
@@ -78,6 +79,18 @@ class Reinserter:
             address = self.flags[device] = pointer.value
         return address
 
+    def _host_counts(self, device, slots) -> int:
+        """Host-coherent words for the recalled rows of every slot (device-grouped path)."""
+        address, size = self.counts.get(device, (None, 0))
+        if size < slots:
+            if address is not None:
+                _lib.call("lr_staging_free", address)
+            pointer = ctypes.c_void_p()
+            _lib.call("lr_staging_alloc", 8 * slots, ctypes.byref(pointer))
+            address, size = pointer.value, slots
+            self.counts[device] = (address, size)
+        return address
+
     def __del__(self):
         # at interpreter exit the module globals may already be gone; the process releases
         # its pinned memory then anyway
@@ -86,6 +99,8 @@ class Reinserter:
             return
         for address in getattr(self, "flags", {}).values():
             library.lr_staging_free(address)
+        for address, _ in getattr(self, "counts", {}).values():
+            library.lr_staging_free(address)
 
     def run(self, layers: Sequence[LayerState], payload: torch.Tensor, metadata) -> ReinsertOutcome:
         """Inserts payload rows [M, 2, d] (K at [i, 0], V at [i, 1]; pinned host memory or
@@ -93,7 +108,15 @@ class Reinserter:
         ``layers`` (a list of LayerState or a PackedLayers). Returns the merged layers; raises
         before returning, as the reference does, if an identity is already resident or
         repeated. The merges are enqueued on the current stream. A pinned host payload is still
-        being read when run() returns: ``outcome.payload_copied`` marks the end of its copy."""
+        being read when run() returns: ``outcome.payload_copied`` marks the end of its copy.
+
+        ``metadata`` on the host (a numpy array or an unpinned tensor) is checked and grouped
+        by head in C++ before the launches. An int64 tensor in device memory, or in pinned host
+        memory (copied in on the side stream ahead of the payload), is grouped on the device
+        instead (lr_reinsert_group): the host never walks the identities, and reads each
+        head's count back after the plan, with the flags."""
+        if isinstance(metadata, torch.Tensor) and (metadata.is_cuda or metadata.is_pinned()):
+            return self._run_device_grouped(layers, payload, metadata)
         metadata = np.ascontiguousarray(np.asarray(metadata, dtype=np.int64).reshape(-1, 3))
         count = len(metadata)
         if tuple(payload.shape[:2]) != (count, 2):
@@ -180,6 +203,111 @@ class Reinserter:
                               layers.sources if packed else list(layers),
                               DeviceLayout(layout, new_lens))
         caller_buffer = not on_device and source is payload
+        return ReinsertOutcome(merged, new_lens, recalled_rows, count,
+                               payload_ready if caller_buffer else None)
+
+
+    def _run_device_grouped(self, layers, payload, metadata) -> ReinsertOutcome:
+        """run() for identities in device (or pinned host) memory: the table goes up through
+        the host module's staging ring, the grouping (count, prefix, scatter), the plan, the
+        resident rows and the recalled rows run on the current stream, and the host builds its
+        layout from the counts once the plan is done."""
+        if metadata.dtype != torch.int64 or metadata.dim() != 2 or metadata.shape[1] != 3:
+            raise ValueError("Recall metadata must be an int64 [count, 3] array")
+        count = int(metadata.shape[0])
+        if tuple(payload.shape[:2]) != (count, 2):
+            raise ValueError("Recall payload/identity shape mismatch")
+        packed = isinstance(layers, PackedLayers)
+        if packed:
+            tensors = ([layers.keys], [layers.values], [layers.positions])
+            lengths, packed_offsets = layers.kept, layers.offsets
+        else:
+            tensors = ([l.keys for l in layers], [l.values for l in layers],
+                       [l.positions for l in layers])
+            lengths, packed_offsets = [list(l.head_lens) for l in layers], []
+        keys0 = tensors[0][0]
+        dim, dtype, device = keys0.shape[1], keys0.dtype, keys0.device
+        if payload.dtype != dtype or tuple(payload.shape[2:]) != (dim,):
+            raise RuntimeError("Recalled payload must match the cache dtype and head dim")
+        heads = len(lengths[0])
+        slots = len(lengths) * heads
+        current = torch.cuda.current_stream(device)
+        stream = current.cuda_stream
+        from .audit import _native_planner
+        table, resident, max_length = _native_planner().reinsert_table(
+            *tensors, lengths, packed_offsets, stream)
+        out_rows = sum(resident) + count
+        out_keys = torch.empty((out_rows, dim), dtype=dtype, device=device)
+        out_values = torch.empty_like(out_keys)
+        out_positions = torch.empty((out_rows,), dtype=torch.float32, device=device)
+        recalled_rows = torch.empty((count,), dtype=torch.int64, device=device)
+        workspace = torch.empty((3 * max(count, 1),), dtype=torch.int64, device=device)
+        grouped = torch.empty((2 * max(count, 1),), dtype=torch.int64, device=device)
+        flag = torch.zeros((1,), dtype=torch.int64, device=device)
+        layout = torch.empty((slots + len(lengths) * (heads + 1),), dtype=torch.int32,
+                             device=device)
+
+        # copies in, on the side stream: host metadata first (small), then a host payload
+        side = self._side_stream(device)
+        on_device = payload.is_cuda
+        if on_device:
+            payload_device = payload.contiguous()
+        meta_device = metadata.contiguous() if metadata.is_cuda else None
+        meta_ready = payload_ready = None
+        source = None
+        if meta_device is None or not on_device:
+            with torch.cuda.stream(side):
+                if meta_device is None:
+                    meta_device = metadata.to(device, non_blocking=True)
+                    meta_ready = torch.cuda.Event()
+                    meta_ready.record(side)
+                if not on_device:
+                    source = payload if payload.is_pinned() else payload.pin_memory()
+                    payload_device = source.to(device, non_blocking=True)
+                    payload_ready = torch.cuda.Event()
+                    payload_ready.record(side)
+            if meta_ready is not None:
+                meta_device.record_stream(current)
+            if payload_ready is not None:
+                payload_device.record_stream(current)
+        if meta_ready is not None:
+            current.wait_event(meta_ready)
+
+        host_flag = self._host_flag(device)
+        host_counts = self._host_counts(device, slots)
+        _lib.call("lr_reinsert_group", table.data_ptr(), slots, heads,
+                  meta_device.data_ptr() if count else None, count, grouped.data_ptr(),
+                  host_counts, flag.data_ptr(), stream)
+        _lib.call("lr_reinsert_plan_layout", table.data_ptr(), slots,
+                  grouped.data_ptr() if count else None, count, workspace.data_ptr(),
+                  _lib.ptr(recalled_rows), flag.data_ptr(), heads, layout.data_ptr(),
+                  layout.data_ptr() + 4 * slots, stream)
+        _lib.call("lr_copy_words", flag.data_ptr(), host_flag, 1, stream)
+        planned = torch.cuda.Event()
+        planned.record(current)
+        _lib.call("lr_reinsert_resident", table.data_ptr(), slots, workspace.data_ptr(), count,
+                  max_length, dim, keys0.element_size(), out_rows, out_keys.data_ptr(),
+                  out_values.data_ptr(), out_positions.data_ptr(), stream)
+        if payload_ready is not None:
+            current.wait_event(payload_ready)
+        _lib.call("lr_reinsert_recalled", workspace.data_ptr(), count, _lib.ptr(payload_device),
+                  dim, keys0.element_size(), out_rows, out_keys.data_ptr(),
+                  out_values.data_ptr(), out_positions.data_ptr(), stream)
+        planned.synchronize()  # the grouping and the plan only; the merges may still run
+        word = ctypes.c_int64.from_address(host_flag).value
+        if word & _FLAG_IDENTITY:
+            raise ValueError("Invalid recall identity")
+        if word & _FLAG_DUPLICATE:
+            raise ValueError("Cannot merge duplicate physical KV identities")
+        if word & _FLAG_HEAD_LIMIT:
+            raise ValueError("Too many recalled rows for one head")
+        counts = np.ctypeslib.as_array((ctypes.c_int64 * slots).from_address(host_counts)).copy()
+        new_lens = (np.asarray(lengths, dtype=np.int64) + counts.reshape(-1, heads)).tolist()
+        offsets = np.concatenate(([0], np.cumsum([sum(row) for row in new_lens]))).tolist()
+        merged = PackedLayers(out_keys, out_values, out_positions, new_lens, offsets,
+                              layers.sources if packed else list(layers),
+                              DeviceLayout(layout, new_lens))
+        caller_buffer = source is not None and source is payload
         return ReinsertOutcome(merged, new_lens, recalled_rows, count,
                                payload_ready if caller_buffer else None)
 

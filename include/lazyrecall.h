@@ -368,6 +368,19 @@ int lr_queue_evict_plan(const int64_t* quotas, const int64_t* offsets,
 #define LR_REINSERT_MAX_PER_HEAD 4096
 int lr_reinsert_plan(const int64_t* table, int64_t slots, const int64_t* grouped, int64_t count,
                      int64_t* workspace, int64_t* recalled_rows, int32_t* flag, void* stream);
+/* Device grouping for a reinsertion whose identities are in device memory: the host's
+ * grouping and counting of reinsert_prepare (merge_plan's per-head runs, src/lazy_recall/
+ * recall/planning.py:34-52) done by three launches on `stream`, so that the host never walks
+ * the identities. table: DEVICE, LR_REINSERT_WORDS per slot with words [0..3] filled and [4..7]
+ * zero; metadata: DEVICE i64 [count, 3] (layer, head, position). Fills table words [4] (first
+ * entry of the slot's run), [5] (recalled rows of the slot) and [6] (first output row), and
+ * grouped = DEVICE i64 [2 * count] as lr_reinsert_plan takes it (runs in any order inside).
+ * host_counts (host-coherent, lr_staging_alloc, or NULL) receives each slot's recalled rows
+ * for the host's layout. flag as lr_reinsert_plan's, plus bit 2: an identity outside the
+ * layers, heads or [0, 2^31) (left out of every run). */
+int lr_reinsert_group(int64_t* table, int64_t slots, int64_t heads, const int64_t* metadata,
+                      int64_t count, int64_t* grouped, int64_t* host_counts, int32_t* flag,
+                      void* stream);
 /* lr_reinsert_plan plus the merged layers' metadata on the device, written by the same
  * launch (LazyRecallCache.insert_payload's replace_head_lens, src/lazy_recall/cache.py:246,
  * without its host-to-device copies): head_lens i32 [slots] and cumulative i32

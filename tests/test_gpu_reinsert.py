@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from code_for_iclr27_amd import audit, reinsert, workloads
+from code_for_iclr27_amd import _lib, audit, reinsert, workloads
 from code_for_iclr27_amd.scoring import LayerState
 from oracle import kv_ops
 
@@ -69,11 +69,21 @@ def check(outcome, layers, payload, meta):
             assert recalled_rows[rows[local]] == out_row - bounds[head]
 
 
+def metadata_as(meta, form, device):
+    """The identities as the host path takes them (numpy) or as the device-grouped path does
+    (an int64 tensor in device or pinned host memory)."""
+    if form == "host":
+        return meta
+    tensor = torch.from_numpy(np.ascontiguousarray(meta))
+    return tensor.to(device) if form == "device" else tensor.pin_memory()
+
+
+@pytest.mark.parametrize("meta_form", ["host", "device", "pinned"])
 @pytest.mark.parametrize("on_device,grouped", [(False, False), (True, False), (False, True)])
-def test_reinsert_matches_merge_plan(device, on_device, grouped):
+def test_reinsert_matches_merge_plan(device, on_device, grouped, meta_form):
     """Identities in any order, or already grouped by (layer, head) in slot order (the host
     planner then copies instead of scattering them), with empty slots and a layer without
-    recalls."""
+    recalls; grouped on the host or, from device or pinned metadata, on the device."""
     head_lengths = [[300, 41, 280, 1], [170, 300, 33, 299], [64, 200, 310, 90]]
     layers, payload, meta = make_case(device, head_lengths, [17, 0, 5, 129, 1], 128, seed=3,
                                       skip_layer=1)
@@ -81,7 +91,7 @@ def test_reinsert_matches_merge_plan(device, on_device, grouped):
         order = np.argsort(meta[:, 0] * 4 + meta[:, 1], kind="stable")
         meta, payload = meta[order], payload[torch.from_numpy(order)]
     source = payload.to(device) if on_device else payload.pin_memory()
-    outcome = reinsert.Reinserter().run(layers, source, meta)
+    outcome = reinsert.Reinserter().run(layers, source, metadata_as(meta, meta_form, device))
     torch.cuda.synchronize()
     assert outcome.inserted == len(meta)
     check(outcome, layers, payload, meta)
@@ -113,21 +123,39 @@ def test_reinsert_into_packed_layers_and_empty_batch(device):
         assert torch.equal(empty.layers[l].positions, merged.layers[l].positions)
 
 
-def test_reinsert_refuses_duplicates_and_bad_identities(device):
+@pytest.mark.parametrize("meta_form", ["host", "device"])
+def test_reinsert_refuses_duplicates_and_bad_identities(device, meta_form):
     layers, payload, meta = make_case(device, [[100, 80]], [5], 64, seed=6)
     resident = int(layers[0].positions[3].item())
     bad = np.concatenate((meta, [[0, 0, resident]]))
     extra = torch.cat((payload, payload[:1]))
+    runner = reinsert.Reinserter()
     with pytest.raises(ValueError, match="duplicate physical KV identities"):
-        reinsert.Reinserter().run(layers, extra.pin_memory(), bad)
+        runner.run(layers, extra.pin_memory(), metadata_as(bad, meta_form, device))
     repeated = np.concatenate((meta, meta[:1]))
     with pytest.raises(ValueError, match="duplicate physical KV identities"):
-        reinsert.Reinserter().run(layers, extra.pin_memory(), repeated)
-    with pytest.raises(ValueError, match="Invalid recall identity"):
-        reinsert.Reinserter().run(layers, payload.pin_memory(),
-                                  np.concatenate((meta[:-1], [[0, 2, 5]])))
+        runner.run(layers, extra.pin_memory(), metadata_as(repeated, meta_form, device))
+    for wrong in ([0, 2, 5], [1, 0, 5], [0, 0, -3]):
+        with pytest.raises(ValueError, match="Invalid recall identity"):
+            runner.run(layers, payload.pin_memory(),
+                       metadata_as(np.concatenate((meta[:-1], [wrong])), meta_form, device))
     with pytest.raises(ValueError, match="shape mismatch"):
-        reinsert.Reinserter().run(layers, payload[:-1].pin_memory(), meta)
+        runner.run(layers, payload[:-1].pin_memory(), metadata_as(meta, meta_form, device))
+    # the same runner still merges correctly after the refusals
+    outcome = runner.run(layers, payload.pin_memory(), metadata_as(meta, meta_form, device))
+    torch.cuda.synchronize()
+    check(outcome, layers, payload, meta)
+
+
+def test_reinsert_device_grouped_head_limit(device):
+    """More than LR_REINSERT_MAX_PER_HEAD recalled rows for one head: refused from the device
+    flag, with every launch staying inside its buffers."""
+    limit = _lib.LR_REINSERT_MAX_PER_HEAD
+    layers, payload, meta = make_case(device, [[64, 32]], [limit + 3, 2], 64, seed=8)
+    with pytest.raises(ValueError, match="Too many recalled rows for one head"):
+        reinsert.Reinserter().run(layers, payload.pin_memory(),
+                                  metadata_as(meta, "device", device))
+    torch.cuda.synchronize()
 
 
 def test_reinsert_full_size_cfg3(device):
@@ -151,7 +179,8 @@ def test_reinsert_full_size_cfg3(device):
         layers.append(LayerState(keys, values, positions, [T] * H, None, None, None))
     meta = np.asarray(meta, np.int64)
     payload = torch.randn((len(meta), 2, d), generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
-    outcome = reinsert.Reinserter().run(layers, payload.pin_memory(), meta)
+    outcome = reinsert.Reinserter().run(layers, payload.pin_memory(),
+                                        torch.from_numpy(meta).pin_memory())
     torch.cuda.synchronize()
     assert outcome.head_lens == [[T + M] * H] * L
     for l in range(L):
