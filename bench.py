@@ -348,6 +348,13 @@ def _op_line(workload, calls, device_us, nbytes, wall_ms):
             "wall_ms_per_step": round(wall_ms, 3)}
 
 
+def nbytes_append_layer(rows, heads, dim):
+    """Algorithmic bytes of one layer's one-token append: K and V read and written, the
+    positions read and written, the new rows read."""
+    return (2 * rows * dim * 2 + 2 * (rows + heads) * dim * 2 + rows * 4 + (rows + heads) * 4
+            + 2 * heads * dim * 2)
+
+
 def ops_bench(torch, seed, reps=5):
     """The scope table's data-movement rows outside the audit step, on their own shapes:
     decode-time appends (cfg1 layer, cfg2 static batch), the legacy flat-cache ops, the per-layer
@@ -400,7 +407,7 @@ def ops_bench(torch, seed, reps=5):
     device, wall = measure(lambda: [
         (lambda l=l: _C.append(keys[l], values[l], positions, new_k, new_v, cumulative,
                                T, T)) for l in range(L)], L)
-    nbytes = 2 * rows * d * 2 + 2 * (rows + H) * d * 2 + rows * 4 + (rows + H) * 4 + 2 * H * d * 2
+    nbytes = nbytes_append_layer(rows, H, d)
     out["append"] = _op_line("cfg1 layer: 8 heads x 2250 rows + 1 token per head, bf16 d128", L,
                              device, nbytes, wall)
 
@@ -503,6 +510,38 @@ def ops_bench(torch, seed, reps=5):
         nbytes = 2 * total * d * 2 + 2 * requests * H * 4 * d * 2 + (requests * H + 1) * 4
         out["packed_attention_" + label[:4]] = _op_line(label, L, device, nbytes, wall)
         del layer_k, layer_v
+
+    # one cfg1 decode step's appends and attention over 32 layers, as the reference runs it
+    # (per layer: _C.append, then attention over the appended cache; cache.py:33-52 then
+    # attention.py:15-35) and with the appends deferred (per layer: attention with the step's
+    # token pending; then one _C.append_layers for every layer)
+    step_k = [randn(rows, d) for _ in range(L)]
+    step_v = [randn(rows, d) for _ in range(L)]
+    step_q = randn(1, H * 4, 1, d)
+    step_pos = torch.arange(T, dtype=torch.float32, device=dev).repeat(H)[:, None].contiguous()
+    step_cu = torch.arange(0, rows + 1, T, dtype=torch.int32, device=dev)
+    decode_q = torch.arange(H + 1, dtype=torch.int32, device=dev)
+    cached_meta = SimpleNamespace(cu_seqlens_k=step_cu, max_seqlen_k=T, decoding_cu_seqlens_q=decode_q)
+
+    def eager_step():
+        for l in range(L):
+            k, v, _, cu, _ = _C.append(step_k[l], step_v[l], step_pos, new_k, new_v, step_cu, T, T)
+            packed_attention(step_q, k, v, SimpleNamespace(cu_seqlens_k=cu, max_seqlen_k=T + 1,
+                                                           decoding_cu_seqlens_q=decode_q), 1, H)
+
+    def deferred_step():
+        for l in range(L):
+            packed_attention(step_q, step_k[l], step_v[l], cached_meta, 1, H, pending=(new_k, new_v))
+        _C.append_layers(step_k, step_v, [step_pos] * L, [new_k] * L, [new_v] * L, [step_cu] * L,
+                         [T] * L, T)
+
+    step_bytes = L * (nbytes_append_layer(rows, H, d) + 2 * (rows + H) * d * 2)
+    for name, step_fn in (("decode_step_cfg1_append_then_attend", eager_step),
+                          ("decode_step_cfg1_deferred_appends", deferred_step)):
+        device, wall = measure(lambda: [step_fn for _ in range(4)], 1)
+        out[name] = _op_line("cfg1 decode step, 32 layers: appends of one token per head and "
+                             "decode attention (G4)", 1, device, step_bytes, wall)
+    del step_k, step_v
 
     # the audit's margin helpers at the Llama-3.1-8B head (vocab 128,256 x hidden 4096, bf16)
     # and its 32 o_proj matrices [4096, 4096] (_core/scoring.py:34-76, scoring.py:228-237)

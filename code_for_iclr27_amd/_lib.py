@@ -84,6 +84,9 @@ SIGNATURES = {
     "lr_packed_attention_workspace_bytes": [_I64, _I64, _I64, _I64, _I64],
     "lr_packed_attention": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
                             _I, _I64, _F, _P, _P, _SZ, _P],
+    "lr_packed_attention_pending_workspace_bytes": [_I64, _I64, _I64, _I64],
+    "lr_packed_attention_pending": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _I64,
+                                    _I64, _I, _I64, _F, _P, _P, _P, _P, _SZ, _P],
     "lr_packed_attention_scratch_bytes": [],
     "lr_packed_attention_noalloc": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _I64, _I64,
                                     _I64, _I64, _I, _I64, _F, _P, _P],
@@ -100,6 +103,7 @@ _RESTYPES = {"lr_last_error": ctypes.c_char_p, "lr_score_workspace_bytes": ctype
              "lr_select_workspace_bytes": ctypes.c_size_t,
              "lr_packed_attention_workspace_bytes": ctypes.c_size_t,
              "lr_packed_attention_scratch_bytes": ctypes.c_size_t,
+             "lr_packed_attention_pending_workspace_bytes": ctypes.c_size_t,
              "lr_row_sum_workspace_bytes": ctypes.c_size_t,
              "lr_margin_stats_workspace_bytes": ctypes.c_size_t,
              "lr_pre_gradient_layers_workspace_bytes": ctypes.c_size_t}

@@ -39,12 +39,14 @@ def _native():
         library = _lib.load()
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_attention(address("lr_packed_attention"),
-                               address("lr_packed_attention_workspace_bytes"))
+                               address("lr_packed_attention_workspace_bytes"),
+                               address("lr_packed_attention_pending"),
+                               address("lr_packed_attention_pending_workspace_bytes"))
         _native_module = planner
     return _native_module
 
 
-def packed_attention(queries, keys, values, metadata, length, kv_heads):
+def packed_attention(queries, keys, values, metadata, length, kv_heads, pending=None):
     """attention.py:15-35 -> [batch, length, query_heads * dim] in the queries' dtype.
 
     ``queries`` [batch, query_heads, length, dim] (any strides with dim contiguous), ``keys`` and
@@ -53,10 +55,18 @@ def packed_attention(queries, keys, values, metadata, length, kv_heads):
     ``decoding_cu_seqlens_q`` ([batch*kv_heads + 1]; every segment has ``length`` queries).
     The checks (flash_attn's messages), the output and workspace allocation and the launch of
     ``lr_packed_attention`` run in the C++ host module (csrc/host_plan.cpp attention_launch).
+
+    ``pending`` (decode only, ``length`` 1): ``(new_keys, new_values)``, each
+    ``[batch, kv_heads, 1, dim]``, the step's own tokens not yet appended. Each segment then
+    attends over its cached rows and its pending row, which sits where the append would put it
+    (after the cached rows), so the result equals the call on the appended cache bit for bit;
+    ``metadata`` describes the cache without them. The step's appends can then wait for one
+    ``_C.append_layers`` launch after every layer's attention.
     """
     if torch.is_grad_enabled() and queries.requires_grad:
         raise RuntimeError("packed_attention: the deterministic attention backward is not "
                            "implemented on the HIP path (forward only)")
+    new_keys, new_values = (None, None) if pending is None else pending
     return (_native_module or _native()).packed_attention(
         queries, keys, values, metadata.cu_seqlens_k, metadata.decoding_cu_seqlens_q.numel(),
-        int(metadata.max_seqlen_k), int(length), int(kv_heads))
+        int(metadata.max_seqlen_k), int(length), int(kv_heads), new_keys, new_values)

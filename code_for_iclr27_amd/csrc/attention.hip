@@ -75,6 +75,8 @@ struct AttnArgs {
   void* out;                // [B, L, kv_heads * G, D]
   float* part_o;            // [units * splits, R, D]
   float* part_ml;           // [units * splits, R, 2]
+  const void* pending_keys;    // NULL, or [segments, D]: a row after each segment's cached rows
+  const void* pending_values;  // with pending_keys
 };
 
 template <typename T>
@@ -166,10 +168,13 @@ __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attenti
   const int64_t row0 = tile * R;
   const int64_t rows_here = rows - row0 < R ? rows - row0 : R;
 
-  // Segment bounds, clamped into the key buffer.
+  // Segment bounds, clamped into the key buffer. A pending row (the decode step's own token,
+  // not yet appended) is key `cached` of the segment, after its cached rows.
   int64_t key0 = a.cu[seg], n = static_cast<int64_t>(a.cu[seg + 1]) - key0;
   key0 = key0 < 0 ? 0 : (key0 > a.key_rows ? a.key_rows : key0);
   n = n < 0 ? 0 : (n > a.key_rows - key0 ? a.key_rows - key0 : n);
+  const int64_t cached = n;
+  if (a.pending_keys != nullptr) ++n;
   const int64_t shift = n - a.length;  // query i sees keys j <= i + shift
   const int64_t last_query = (row0 + rows_here - 1) / a.groups;
   int64_t key_end = last_query + shift + 1;
@@ -207,6 +212,12 @@ __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attenti
   if (nk > 0) {
     const T* kbase = static_cast<const T*>(a.keys) + (key0 + kb) * D;
     const T* vbase = static_cast<const T*>(a.values) + (key0 + kb) * D;
+    // row of wave key `key` (< nk): a cached row, or the segment's pending row
+    const int64_t cached_here = cached - kb;
+    auto key_row = [&](const T* base, const void* pending, int key) -> const T* {
+      return key < cached_here ? base + static_cast<int64_t>(key) * D
+                               : static_cast<const T*>(pending) + seg * D;
+    };
     // Every load of the wave is issued before the first use: queries (A operand, row m = lane
     // & 15, k chunk j = lane >> 4), K rows (B operand, key m of each 16-key block), V slices.
     X8 qop[KS];
@@ -231,7 +242,7 @@ __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attenti
     for (int blk = 0; blk < NB; ++blk) {
       int key = blk * 16 + m;
       key = key < nk ? key : nk - 1;  // clamped in-range row; its score is masked below
-      const T* kp = kbase + static_cast<int64_t>(key) * D + 8 * j;
+      const T* kp = key_row(kbase, a.pending_keys, key) + 8 * j;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kraw[blk][ks] = load16(kp + 32 * ks);
     }
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attenti
     for (int u = 0; u < VL; ++u) {
       int key = kg + u * KPI;
       key = key < nk ? key : nk - 1;
-      vraw[u] = load16(vbase + static_cast<int64_t>(key) * D + 8 * c);
+      vraw[u] = load16(key_row(vbase, a.pending_values, key) + 8 * c);
     }
 
     // QK^T. D layout: lane holds key 16 * blk + (lane & 15) for rows 4j + r.
@@ -386,6 +397,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs 
   int64_t key0 = a.cu[seg], n = static_cast<int64_t>(a.cu[seg + 1]) - key0;
   key0 = key0 < 0 ? 0 : (key0 > a.key_rows ? a.key_rows : key0);
   n = n < 0 ? 0 : (n > a.key_rows - key0 ? a.key_rows - key0 : n);
+  if (a.pending_keys != nullptr) ++n;  // the pending row, as in the first launch
   const int64_t last_query = (row0 + rows_here - 1) / a.groups;
   int64_t key_end = last_query + n - a.length + 1;
   key_end = key_end < 0 ? 0 : (key_end > n ? n : key_end);
@@ -526,9 +538,13 @@ int packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head
                      int64_t key_rows, const int32_t* cu_seqlens_k, int64_t batch,
                      int64_t kv_heads, int64_t groups, int64_t length, int64_t dim, int dtype,
                      int64_t max_keys, float scale, void* out, void* workspace,
-                     size_t workspace_size, size_t scratch_limit, void* stream) {
+                     size_t workspace_size, size_t scratch_limit, void* stream,
+                     const void* pending_keys = nullptr, const void* pending_values = nullptr) {
   LR_REQUIRE(dtype == LR_DTYPE_BF16 || dtype == LR_DTYPE_F16,
              "FlashAttention only supports fp16 and bf16 data type");
+  LR_REQUIRE((pending_keys == nullptr) == (pending_values == nullptr),
+             "Pending keys and values go together");
+  LR_REQUIRE(pending_keys == nullptr || length == 1, "Pending rows need one query per segment");
   LR_REQUIRE(dim == 64 || dim == 128 || dim == 256, "Head dimension must be 64, 128 or 256");
   LR_REQUIRE(batch > 0 && kv_heads > 0 && groups > 0 && length > 0, "Empty attention dimensions");
   LR_REQUIRE(key_rows >= 0 && max_keys >= 0, "Invalid key lengths");
@@ -538,10 +554,13 @@ int packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head
                               reinterpret_cast<uintptr_t>(keys) |
                               reinterpret_cast<uintptr_t>(values) |
                               reinterpret_cast<uintptr_t>(out) |
+                              reinterpret_cast<uintptr_t>(pending_keys) |
+                              reinterpret_cast<uintptr_t>(pending_values) |
                               static_cast<uintptr_t>((q_batch_stride | q_head_stride |
                                                       q_query_stride) * 2);
   LR_REQUIRE(alignment % 16 == 0, "Attention operands must be 16-byte aligned");
   const int64_t segments = batch * kv_heads;
+  if (pending_keys != nullptr) ++max_keys;  // every segment's pending row
   const AttnPlan plan = plan_attention(segments, groups, length, max_keys, dim);
   const size_t needed = workspace_bytes(plan, dim);
   if (scratch_limit) {
@@ -573,6 +592,8 @@ int packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_head
   args.splits = plan.splits;
   args.scale = scale;
   args.out = out;
+  args.pending_keys = pending_keys;
+  args.pending_values = pending_values;
   if (needed) {
     args.part_ml = static_cast<float*>(workspace);
     args.part_o = args.part_ml + plan.units * plan.splits * plan.rows_per_tile * 2;
@@ -638,6 +659,28 @@ extern "C" int lr_packed_attention(const void* queries, int64_t q_batch_stride,
   return packed_attention(queries, q_batch_stride, q_head_stride, q_query_stride, keys, values,
                           key_rows, cu_seqlens_k, batch, kv_heads, groups, length, dim, dtype,
                           max_keys, scale, out, workspace, workspace_size, 0, stream);
+}
+
+extern "C" size_t lr_packed_attention_pending_workspace_bytes(int64_t segments, int64_t groups,
+                                                              int64_t max_keys, int64_t dim) {
+  return lr_packed_attention_workspace_bytes(segments, groups, 1, max_keys + 1, dim);
+}
+
+extern "C" int lr_packed_attention_pending(const void* queries, int64_t q_batch_stride,
+                                           int64_t q_head_stride, int64_t q_query_stride,
+                                           const void* keys, const void* values,
+                                           int64_t key_rows, const int32_t* cu_seqlens_k,
+                                           int64_t batch, int64_t kv_heads, int64_t groups,
+                                           int64_t dim, int dtype, int64_t max_keys, float scale,
+                                           const void* pending_keys, const void* pending_values,
+                                           void* out, void* workspace, size_t workspace_size,
+                                           void* stream) {
+  clear_error();
+  LR_REQUIRE(pending_keys != nullptr && pending_values != nullptr, "Invalid attention buffers");
+  return packed_attention(queries, q_batch_stride, q_head_stride, q_query_stride, keys, values,
+                          key_rows, cu_seqlens_k, batch, kv_heads, groups, 1, dim, dtype,
+                          max_keys, scale, out, workspace, workspace_size, 0, stream,
+                          pending_keys, pending_values);
 }
 
 extern "C" size_t lr_packed_attention_scratch_bytes(void) { return kAttentionScratchBytes; }

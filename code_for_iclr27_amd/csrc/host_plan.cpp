@@ -235,6 +235,8 @@ struct Library {
   decltype(&lr_append_layers) append_layers = nullptr;
   decltype(&lr_packed_attention) packed_attention = nullptr;
   decltype(&lr_packed_attention_workspace_bytes) attention_workspace_bytes = nullptr;
+  decltype(&lr_packed_attention_pending) packed_attention_pending = nullptr;
+  decltype(&lr_packed_attention_pending_workspace_bytes) pending_workspace_bytes = nullptr;
   decltype(&lr_last_error) last_error = nullptr;
   decltype(&lr_staging_alloc) staging_alloc = nullptr;
   decltype(&lr_staging_free) staging_free = nullptr;
@@ -274,9 +276,12 @@ void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers) 
   bind_one(library.append_layers, append_layers);
 }
 
-void bind_attention(int64_t packed_attention, int64_t workspace_bytes) {
+void bind_attention(int64_t packed_attention, int64_t workspace_bytes, int64_t pending,
+                    int64_t pending_workspace_bytes) {
   bind_one(library.packed_attention, packed_attention);
   bind_one(library.attention_workspace_bytes, workspace_bytes);
+  bind_one(library.packed_attention_pending, pending);
+  bind_one(library.pending_workspace_bytes, pending_workspace_bytes);
 }
 
 void check_call(int status) {
@@ -1054,7 +1059,8 @@ void* current_stream(const torch::Device& device);
 torch::Tensor attention_launch(const torch::Tensor& queries, const torch::Tensor& keys_in,
                                const torch::Tensor& values_in, const torch::Tensor& cumulative,
                                int64_t decoding_count, int64_t max_keys, int64_t length,
-                               int64_t kv_heads) {
+                               int64_t kv_heads, const py::object& pending_keys_in,
+                               const py::object& pending_values_in) {
   require(library.packed_attention != nullptr, "library entry points are not bound");
   require(queries.dim() == 4, "Query length differs from the queries tensor");
   const int64_t batch = queries.size(0), query_heads = queries.size(1), dim = queries.size(3);
@@ -1084,13 +1090,41 @@ torch::Tensor attention_launch(const torch::Tensor& queries, const torch::Tensor
   require(decoding_count == segments + 1, "cu_seqlens_q must have shape (batch_size + 1)");
   require(max_keys >= 0, "Invalid max_seqlen_k");
   const c10::DeviceGuard guard(queries.device());
+  // The decode step's own tokens, attended to before they are appended ([batch, kv_heads, 1,
+  // dim] each, one per segment)
+  const bool pending = !pending_keys_in.is_none();
+  require(pending == !pending_values_in.is_none(), "Pending keys and values go together");
+  torch::Tensor pending_keys, pending_values;
+  if (pending) {
+    pending_keys = pending_keys_in.cast<torch::Tensor>();
+    pending_values = pending_values_in.cast<torch::Tensor>();
+    for (const torch::Tensor* t : {&pending_keys, &pending_values}) {
+      require(t->is_cuda() && t->device() == queries.device(), "CUDA devices differ");
+      require(t->is_contiguous() && t->scalar_type() == dtype &&
+                  t->sizes() == torch::IntArrayRef({batch, kv_heads, 1, dim}),
+              "Pending keys and values must be contiguous [batch, kv_heads, 1, head_dim]");
+    }
+    require(length == 1, "Pending rows need one query per segment");
+  }
   torch::Tensor out = torch::empty({batch, length, query_heads, dim}, queries.options());
-  const size_t size = library.attention_workspace_bytes(segments, groups, length, max_keys, dim);
+  const size_t size =
+      pending ? library.pending_workspace_bytes(segments, groups, max_keys, dim)
+              : library.attention_workspace_bytes(segments, groups, length, max_keys, dim);
   torch::Tensor workspace;
   if (size)
     workspace = torch::empty({static_cast<int64_t>(size)},
                              queries.options().dtype(torch::kUInt8));
   const float scale = static_cast<float>(std::pow(static_cast<double>(dim), -0.5));
+  if (pending) {
+    check_call(library.packed_attention_pending(
+        queries.data_ptr(), queries.stride(0), queries.stride(1), queries.stride(2),
+        keys.numel() ? keys.data_ptr() : nullptr, values.numel() ? values.data_ptr() : nullptr,
+        keys.size(0), cumulative.data_ptr<int32_t>(), batch, kv_heads, groups, dim,
+        dtype == torch::kBFloat16 ? LR_DTYPE_BF16 : LR_DTYPE_F16, max_keys, scale,
+        pending_keys.data_ptr(), pending_values.data_ptr(), out.data_ptr(),
+        size ? workspace.data_ptr() : nullptr, size, current_stream(queries.device())));
+    return out.view({batch, length, query_heads * dim});
+  }
   check_call(library.packed_attention(
       queries.data_ptr(), queries.stride(0), queries.stride(1), queries.stride(2),
       keys.numel() ? keys.data_ptr() : nullptr, values.numel() ? values.data_ptr() : nullptr,

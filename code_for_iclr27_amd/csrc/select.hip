@@ -721,62 +721,126 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
 
 // ---------------------------------------------------------------------------------------
 // Queue order. Per segment, both pick lists are put in (key, index) order: the raw picks give
-// the segment's slots, the pooled picks what fills them (transplant). Lists of up to
-// kRankSortMax entries are rank-sorted in LDS (stable: equal keys keep index order); longer ones
-// use the block radix sort in global memory.
-constexpr uint32_t kRankSortMax = 1024;
+// the segment's slots, the pooled picks what fills them (transplant). One 1024-thread
+// workgroup per segment; the sort depends on the list's length n:
+//   n <= kRankSortMax: rank sort in LDS, each entry's rank (entries with a smaller key, or an
+//     equal key at a lower index) counted by four lanes over interleaved quarters of the list
+//     and summed across the quad, so a lane's chain of LDS reads is a quarter as long;
+//   n <= kBitonicMax: a bitonic network over (key << 32 | index) pairs in LDS;
+//   longer lists: the block radix sort in global memory.
+// Both in-LDS sorts keep equal keys in index order.
+constexpr int kSortThreads = 1024;       // segment_sort workgroups
+constexpr uint32_t kRankSortMax = 512;
+constexpr uint32_t kBitonicMax = 4096;
 
-__device__ __forceinline__ void rank_sort_lds(uint32_t* keys, uint32_t* values, uint32_t n,
-                                              uint32_t* lds_keys, uint32_t* lds_values) {
-  for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
-    lds_keys[i] = keys[i];
-    lds_values[i] = values ? values[i] : 0u;
+union SegmentSortLds {
+  struct {
+    uint32_t keys[kRankSortMax + 16];
+    uint32_t values[kRankSortMax];
+  } rank;
+  struct {
+    uint64_t pairs[kBitonicMax];
+    uint32_t local[kBitonicMax];
+  } bitonic;
+  SortLds<kSortThreads> radix;
+};
+
+// keys[0, n) (index order; values[0, n) with them, if given) sorted by (key, index) in place.
+__device__ __forceinline__ void rank_sort_quads(uint32_t* keys, uint32_t* values, uint32_t n,
+                                                SegmentSortLds& lds) {
+  uint32_t* lk = lds.rank.keys;
+  for (uint32_t i = threadIdx.x; i < ((n + 15) & ~15u); i += kSortThreads) {
+    lk[i] = i < n ? keys[i] : 0xffffffffu;
+    if (values != nullptr && i < n) lds.rank.values[i] = values[i];
   }
-  for (uint32_t i = n + threadIdx.x; i < ((n + 3) & ~3u); i += kSegThreads) lds_keys[i] = 0xffffffffu;
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < n; i += kSegThreads) {
-    const uint32_t key = lds_keys[i];
+  const uint32_t quarter = threadIdx.x & 3;
+  // every lane of a quad runs the same trip count (the quad shares its entry)
+  for (uint32_t base = 0; base < n; base += kSortThreads / 4) {
+    const uint32_t i = base + (threadIdx.x >> 2);
+    const uint32_t key = i < n ? lk[i] : 0xffffffffu;
     uint32_t rank = 0;
-    for (uint32_t j = 0; j < n; j += 4) {
-      const uint4 k4 = *reinterpret_cast<const uint4*>(lds_keys + j);
+    for (uint32_t j = 4 * quarter; j < n; j += 16) {
+      // padding keys (0xffffffff at j >= n > i) are never below `key` nor equal at a lower
+      // index
+      const uint4 k4 = *reinterpret_cast<const uint4*>(lk + j);
       rank += (k4.x < key) | ((k4.x == key) & (j < i));
       rank += (k4.y < key) | ((k4.y == key) & (j + 1 < i));
       rank += (k4.z < key) | ((k4.z == key) & (j + 2 < i));
       rank += (k4.w < key) | ((k4.w == key) & (j + 3 < i));
     }
-    // padding keys are 0xffffffff at j >= n > i: never below `key`, never equal at a lower index
-    // unless key is 0xffffffff itself, in which case j < i fails for them
-    keys[rank] = key;
-    if (values) values[rank] = lds_values[i];
+    rank += __shfl_xor(rank, 1, 64);
+    rank += __shfl_xor(rank, 2, 64);
+    if (quarter == 0 && i < n) {
+      keys[rank] = key;
+      if (values != nullptr) values[rank] = lds.rank.values[i];
+    }
   }
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(
+// Ascending sort of a[0, n2), n2 a power of two, by all kSortThreads threads.
+__device__ __forceinline__ void bitonic_sort_lds(uint64_t* a, uint32_t n2) {
+  for (uint32_t size = 2; size <= n2; size <<= 1) {
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      for (uint32_t t = threadIdx.x; t < n2 / 2; t += kSortThreads) {
+        const uint32_t i = 2 * t - (t & (stride - 1));  // lower element of pair t
+        const uint64_t x = a[i], y = a[i + stride];
+        if ((x > y) == ((i & size) == 0)) {
+          a[i] = y;
+          a[i + stride] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ __launch_bounds__(kSortThreads) void segment_sort_kernel(
     const int64_t* __restrict__ quotas, const int64_t* __restrict__ offsets,
     uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_slots,
     uint32_t* __restrict__ refined_keys, uint32_t* __restrict__ refined_local,
     uint32_t* __restrict__ tmp_keys, uint32_t* __restrict__ tmp_values) {
-  __shared__ uint32_t lds_keys[kRankSortMax];
-  __shared__ uint32_t lds_values[kRankSortMax];
-  __shared__ SortLds<kSegThreads> sort_lds;
+  __shared__ SegmentSortLds lds;
   const int64_t s = blockIdx.x;
   const uint32_t quota = static_cast<uint32_t>(quotas[s]);
   if (quota == 0) return;
   const int64_t offset = offsets[s];
   if (quota <= kRankSortMax) {
-    rank_sort_lds(run_keys + offset, nullptr, quota, lds_keys, lds_values);
-    rank_sort_lds(refined_keys + offset, refined_local + offset, quota, lds_keys, lds_values);
-  } else {
-    for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads) run_slots[offset + i] = 0u;
+    rank_sort_quads(run_keys + offset, nullptr, quota, lds);
+    rank_sort_quads(refined_keys + offset, refined_local + offset, quota, lds);
+  } else if (quota <= kBitonicMax) {
+    uint32_t n2 = 1;
+    while (n2 < quota) n2 <<= 1;
+    uint64_t* pairs = lds.bitonic.pairs;
+    for (uint32_t i = threadIdx.x; i < n2; i += kSortThreads)
+      pairs[i] = i < quota ? (static_cast<uint64_t>(run_keys[offset + i]) << 32) | i : ~0ull;
     __syncthreads();
-    block_radix_sort<kSegThreads>(run_keys + offset, run_slots + offset, tmp_keys + offset,
-                                  tmp_values + offset, quota, sort_lds);
-    block_radix_sort<kSegThreads>(refined_keys + offset, refined_local + offset,
-                                  tmp_keys + offset, tmp_values + offset, quota, sort_lds);
+    bitonic_sort_lds(pairs, n2);
+    for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads)
+      run_keys[offset + i] = static_cast<uint32_t>(pairs[i] >> 32);
+    __syncthreads();  // the raw list's readers are done with the LDS
+    for (uint32_t i = threadIdx.x; i < n2; i += kSortThreads) {
+      pairs[i] = i < quota ? (static_cast<uint64_t>(refined_keys[offset + i]) << 32) | i : ~0ull;
+      if (i < quota) lds.bitonic.local[i] = refined_local[offset + i];
+    }
+    __syncthreads();
+    bitonic_sort_lds(pairs, n2);
+    for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads) {
+      const uint64_t pair = pairs[i];
+      refined_keys[offset + i] = static_cast<uint32_t>(pair >> 32);
+      refined_local[offset + i] = lds.bitonic.local[static_cast<uint32_t>(pair)];
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads) run_slots[offset + i] = 0u;
+    __syncthreads();
+    block_radix_sort<kSortThreads>(run_keys + offset, run_slots + offset, tmp_keys + offset,
+                                   tmp_values + offset, quota, lds.radix);
+    block_radix_sort<kSortThreads>(refined_keys + offset, refined_local + offset,
+                                   tmp_keys + offset, tmp_values + offset, quota, lds.radix);
   }
   // Slot payload for the global order: position in the concatenated runs.
-  for (uint32_t i = threadIdx.x; i < quota; i += kSegThreads)
+  for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads)
     run_slots[offset + i] = static_cast<uint32_t>(offset + i);
 }
 
@@ -889,14 +953,17 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
   return check_launch("segment_pick");
 }
 
-int launch_queue(const int64_t* position_starts, int64_t segments, int64_t count,
-                 const SelectWorkspace& w, const int64_t* quotas, const int64_t* offsets,
-                 float* out_values, int64_t* out_segments, int64_t* out_positions,
-                 hipStream_t s) {
-  segment_sort_kernel<<<segments, kSegThreads, 0, s>>>(quotas, offsets, w.run_keys, w.run_slots,
-                                                       w.refined_keys, w.refined_local,
-                                                       w.tmp_keys, w.tmp_values);
-  if (int rc = check_launch("segment_sort")) return rc;
+int launch_runs(int64_t segments, const SelectWorkspace& w, const int64_t* quotas,
+                const int64_t* offsets, hipStream_t s) {
+  segment_sort_kernel<<<segments, kSortThreads, 0, s>>>(quotas, offsets, w.run_keys,
+                                                        w.run_slots, w.refined_keys,
+                                                        w.refined_local, w.tmp_keys, w.tmp_values);
+  return check_launch("segment_sort");
+}
+
+int launch_order(const int64_t* position_starts, int64_t segments, int64_t count,
+                 const SelectWorkspace& w, const int64_t* offsets, float* out_values,
+                 int64_t* out_segments, int64_t* out_positions, hipStream_t s) {
   size_t sort_bytes = w.sort_bytes;
   const hipError_t sorted = rocprim::radix_sort_pairs(
       w.sort_storage, sort_bytes, static_cast<const uint32_t*>(w.run_keys), w.tmp_keys,
@@ -987,8 +1054,10 @@ extern "C" int lr_select_refine_queue(const int64_t* position_starts, int64_t to
              "Expected contiguous CUDA tensor");
   const SelectWorkspace w = carve(workspace, total, segments, count);
   LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
-  return launch_queue(position_starts, segments, count, w, quotas, offsets, out_values,
-                      out_segments, out_positions, as_stream(stream));
+  const hipStream_t s = as_stream(stream);
+  if (int rc = launch_runs(segments, w, quotas, offsets, s)) return rc;
+  return launch_order(position_starts, segments, count, w, offsets, out_values, out_segments,
+                      out_positions, s);
 }
 
 extern "C" int lr_select_refine(const float* raw, const float* pooled, int64_t total,

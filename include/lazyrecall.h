@@ -452,6 +452,26 @@ int lr_packed_attention(const void* queries, int64_t q_batch_stride, int64_t q_h
                         int64_t kv_heads, int64_t groups, int64_t length, int64_t dim, int dtype,
                         int64_t max_keys, float scale, void* out, void* workspace,
                         size_t workspace_size, void* stream);
+/* Decode attention over each segment's cached rows plus one pending row: the step's own new
+ * token of each (request, KV head), not yet appended (no reference counterpart as an entry
+ * point: the reference appends inside each layer's forward, src/lazy_recall/attention.py:63
+ * -> cache.py:33-52, and attends over the appended cache). The pending row is key n of its
+ * segment (n = the cached rows), exactly where the append would put it, so the output equals
+ * lr_packed_attention over the appended cache, bit for bit; a decode step can then append
+ * every layer's tokens afterwards in one lr_append_layers launch. One query per segment
+ * (length 1); pending_keys / pending_values: [batch * kv_heads, dim] in the queries' dtype
+ * (segment s = request b * kv_heads + head h), 16-byte aligned. The workspace is sized by
+ * lr_packed_attention_pending_workspace_bytes; max_keys = the longest cached segment. */
+size_t lr_packed_attention_pending_workspace_bytes(int64_t segments, int64_t groups,
+                                                   int64_t max_keys, int64_t dim);
+int lr_packed_attention_pending(const void* queries, int64_t q_batch_stride,
+                                int64_t q_head_stride, int64_t q_query_stride, const void* keys,
+                                const void* values, int64_t key_rows,
+                                const int32_t* cu_seqlens_k, int64_t batch, int64_t kv_heads,
+                                int64_t groups, int64_t dim, int dtype, int64_t max_keys,
+                                float scale, const void* pending_keys,
+                                const void* pending_values, void* out, void* workspace,
+                                size_t workspace_size, void* stream);
 
 /* Allocation-free packed attention. No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
