@@ -96,7 +96,7 @@ def _native():
         library = _lib.load()
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_data_movement(address("lr_append"), address("lr_compact"),
-                                   address("lr_append_layers"))
+                                   address("lr_append_layers"), address("lr_batch_append"))
         _native_module = planner
     return _native_module
 
@@ -226,20 +226,13 @@ def batch_append(keys: List[torch.Tensor], values: List[torch.Tensor],
     _check(requests > 0 and heads > 0 and len(keys) == requests and len(values) == requests
            and len(positions) == requests and len(lengths) == requests
            and len(logical_positions) == requests, "Request metadata mismatch")
-    elem = _elem_bytes(new_keys, "batch_append")
+    _elem_bytes(new_keys, "batch_append")
     from .audit import _native_planner
+    _native_planner()  # binds the staging entry points
     with torch.cuda.device(new_keys.device):
         # csrc/host_plan.cpp: the reference's descriptor loop (csrc/batch_append.cu:49-80) and
-        # its checks, then an upload through host-coherent staging and a copy kernel on the
-        # current stream (the reference's copy, csrc/batch_append.cu:81, blocks the host)
-        device_descriptors, rows, maximum = _native_planner().plan_batch_append(
-            keys, values, positions, heads, dimension, new_keys.dtype, new_keys.device,
-            lengths, logical_positions, _lib.stream_of(new_keys))
-        output_keys = torch.empty((rows, dimension), dtype=new_keys.dtype, device=new_keys.device)
-        output_values = torch.empty_like(output_keys)
-        output_positions = torch.empty((rows, 1), dtype=torch.float32, device=new_keys.device)
-        _lib.call("lr_batch_append", device_descriptors.data_ptr(), requests * heads,
-                  new_keys.data_ptr(), new_values.data_ptr(), dimension, elem, maximum,
-                  output_keys.data_ptr(), output_values.data_ptr(), output_positions.data_ptr(),
-                  _lib.stream_of(new_keys))
-    return [output_keys, output_values, output_positions]
+        # its checks, the descriptors in host-coherent staging that the kernel reads in place
+        # (the reference's copy, csrc/batch_append.cu:81, blocks the host), allocation, launch
+        return list(_native().batch_append(keys, values, positions, new_keys, new_values,
+                                           lengths, logical_positions,
+                                           _lib.stream_of(new_keys)))

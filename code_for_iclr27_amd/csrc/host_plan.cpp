@@ -9,6 +9,7 @@
 // 113-147: absolute rows of every head). Done from Python it costs ~27 tensor attribute
 // reads per layer at ~0.2 us each; here the whole 32-layer plan takes a few microseconds.
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 #include <torch/extension.h>
 
 #include <algorithm>
@@ -233,6 +234,7 @@ struct Library {
   decltype(&lr_append) append = nullptr;
   decltype(&lr_compact) compact = nullptr;
   decltype(&lr_append_layers) append_layers = nullptr;
+  decltype(&lr_batch_append) batch_append = nullptr;
   decltype(&lr_packed_attention) packed_attention = nullptr;
   decltype(&lr_packed_attention_workspace_bytes) attention_workspace_bytes = nullptr;
   decltype(&lr_packed_attention_pending) packed_attention_pending = nullptr;
@@ -241,6 +243,10 @@ struct Library {
   decltype(&lr_staging_alloc) staging_alloc = nullptr;
   decltype(&lr_staging_free) staging_free = nullptr;
   decltype(&lr_copy_words) copy_words = nullptr;
+  decltype(&lr_reinsert_group) reinsert_group = nullptr;
+  decltype(&lr_reinsert_plan_layout) reinsert_plan_layout = nullptr;
+  decltype(&lr_reinsert_resident) reinsert_resident = nullptr;
+  decltype(&lr_reinsert_recalled) reinsert_recalled = nullptr;
 };
 Library library;
 
@@ -270,10 +276,19 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
   bind_one(library.copy_words, copy_words);
 }
 
-void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers) {
+void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers,
+                        int64_t batch_append) {
   bind_one(library.append, append);
   bind_one(library.compact, compact);
   bind_one(library.append_layers, append_layers);
+  bind_one(library.batch_append, batch_append);
+}
+
+void bind_reinsert(int64_t group, int64_t plan_layout, int64_t resident, int64_t recalled) {
+  bind_one(library.reinsert_group, group);
+  bind_one(library.reinsert_plan_layout, plan_layout);
+  bind_one(library.reinsert_resident, resident);
+  bind_one(library.reinsert_recalled, recalled);
 }
 
 void bind_attention(int64_t packed_attention, int64_t workspace_bytes, int64_t pending,
@@ -307,6 +322,34 @@ struct StagingRing {
   };
   std::vector<Slot> slots{kSlots};
   size_t next = 0;
+
+  // The next buffer, holding `count` words, for a kernel that reads them in place (pinned,
+  // host-coherent memory); release() must follow once that kernel is enqueued.
+  int64_t* stage(const int64_t* words, int64_t count) {
+    Slot& slot = slots[next];
+    if (slot.pending) {
+      slot.done.synchronize();
+      slot.pending = false;
+    }
+    const size_t bytes = static_cast<size_t>(count) * sizeof(int64_t);
+    if (slot.bytes < bytes) {
+      if (slot.host != nullptr) check_call(library.staging_free(slot.host));
+      slot.host = nullptr;
+      slot.bytes = 0;
+      check_call(library.staging_alloc(bytes, &slot.host));
+      slot.bytes = bytes;
+    }
+    std::memcpy(slot.host, words, bytes);
+    return static_cast<int64_t*>(slot.host);
+  }
+  // Marks the buffer stage() returned as in use until the work enqueued so far on the device's
+  // current stream is done, and moves to the next buffer.
+  void release(const torch::Device& device) {
+    Slot& slot = slots[next];
+    slot.done.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+    slot.pending = true;
+    next = (next + 1) % kSlots;
+  }
 
   torch::Tensor upload(const int64_t* words, int64_t count, const torch::Device& device,
                        void* stream) {
@@ -982,12 +1025,24 @@ py::tuple reinsert_prepare(const std::vector<torch::Tensor>& keys,
 // resident row and its length; [4..7] zero) and uploads the table through the staging ring on
 // `stream`. Nothing here depends on the identities. Returns (device table, resident rows of
 // each layer [L], longest resident head).
-py::tuple reinsert_table(const std::vector<torch::Tensor>& keys,
-                         const std::vector<torch::Tensor>& values,
-                         const std::vector<torch::Tensor>& positions,
-                         const std::vector<std::vector<int64_t>>& head_lens,
-                         const std::vector<int64_t>& packed_offsets, int64_t stream_handle) {
-  require(library.copy_words != nullptr, "library entry points are not bound");
+struct ReinsertTable {
+  std::vector<int64_t> words;     // LR_REINSERT_WORDS per slot, words [4..7] zero, then extras
+  std::vector<int64_t> resident;  // resident rows of each layer
+  int64_t max_length = 0, slots = 0, heads = 0, dim = 0;
+  torch::Device device{torch::kCPU};
+  torch::ScalarType dtype = torch::kBFloat16;
+  int64_t elem = 2;
+};
+
+// Checks a reinsertion's layers and fills the table words [0..3] of every slot (the head's
+// first resident row and its length); nothing here depends on the identities.
+ReinsertTable reinsert_table_words(const std::vector<torch::Tensor>& keys,
+                                   const std::vector<torch::Tensor>& values,
+                                   const std::vector<torch::Tensor>& positions,
+                                   const std::vector<std::vector<int64_t>>& head_lens,
+                                   const std::vector<int64_t>& packed_offsets, int64_t extra) {
+  ReinsertTable out;
+
   const bool packed = !packed_offsets.empty();
   const size_t layers = head_lens.size();
   require(layers > 0 && (packed ? packed_offsets.size() == layers + 1 && keys.size() == 1 &&
@@ -1015,9 +1070,12 @@ py::tuple reinsert_table(const std::vector<torch::Tensor>& keys,
             "Position lengths do not match metadata");
   }
   const int64_t slots = static_cast<int64_t>(layers) * heads;
-  std::vector<int64_t> table(static_cast<size_t>(slots * LR_REINSERT_WORDS), 0);
-  py::list resident(layers);
-  int64_t max_length = 0;
+  // the table, then `extra` zero words (the launcher's flag word rides along with the upload)
+  std::vector<int64_t>& table = out.words;
+  table.assign(static_cast<size_t>(slots * LR_REINSERT_WORDS + extra), 0);
+  out.resident.assign(layers, 0);
+  int64_t& max_length = out.max_length;
+  max_length = 0;
   for (size_t l = 0; l < layers; ++l) {
     require(static_cast<int64_t>(head_lens[l].size()) == heads,
             "Every layer must have the same number of KV heads");
@@ -1040,12 +1098,134 @@ py::tuple reinsert_table(const std::vector<torch::Tensor>& keys,
       max_length = std::max(max_length, n);
     }
     require(base == first + layer_rows, "Position lengths do not match metadata");
-    resident[l] = py::int_(layer_rows);
+    out.resident[l] = layer_rows;
   }
+  out.slots = slots;
+  out.heads = heads;
+  out.dim = dim;
+  out.device = device;
+  out.dtype = dtype;
+  out.elem = static_cast<int64_t>(k0.element_size());
+  return out;
+}
+
+// The reinsert table for identities already in device memory, uploaded through the staging
+// ring on `stream` (lr_reinsert_group fills the rest on the device). Returns (device table,
+// resident rows of each layer [L], longest resident head).
+py::tuple reinsert_table(const std::vector<torch::Tensor>& keys,
+                         const std::vector<torch::Tensor>& values,
+                         const std::vector<torch::Tensor>& positions,
+                         const std::vector<std::vector<int64_t>>& head_lens,
+                         const std::vector<int64_t>& packed_offsets, int64_t stream_handle) {
+  require(library.copy_words != nullptr, "library entry points are not bound");
+  const ReinsertTable t = reinsert_table_words(keys, values, positions, head_lens, packed_offsets, 0);
   void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
-  torch::Tensor block = staging_ring(device).upload(table.data(), static_cast<int64_t>(table.size()),
-                                                    device, stream);
-  return py::make_tuple(block, resident, max_length);
+  torch::Tensor block = staging_ring(t.device).upload(t.words.data(),
+                                                      static_cast<int64_t>(t.words.size()),
+                                                      t.device, stream);
+  py::list resident;
+  for (int64_t r : t.resident) resident.append(r);
+  return py::make_tuple(block, resident, t.max_length);
+}
+
+// The whole device-grouped reinsertion (insert_payload for every layer, identities in device
+// memory) from here, so that no Python runs between its launches: the table upload (with a
+// zeroed flag word after it), the grouping, the plan with the merged layers' metadata, the
+// flag's copy to host-coherent memory, then the resident rows, a wait for `payload_ready`
+// (a raw event handle, 0 for none) and the recalled rows, all on `stream`. Waits (without the
+// GIL) for the plan only, then reads the flag and each slot's count. Returns (out keys, out
+// values, out positions, layout block i32, recalled rows i64 [count], new head lengths [L][H],
+// first row of each merged layer [L + 1], flag word).
+py::tuple reinsert_device_launch(const std::vector<torch::Tensor>& keys,
+                                 const std::vector<torch::Tensor>& values,
+                                 const std::vector<torch::Tensor>& positions,
+                                 const std::vector<std::vector<int64_t>>& head_lens,
+                                 const std::vector<int64_t>& packed_offsets,
+                                 const torch::Tensor& payload, const torch::Tensor& metadata,
+                                 int64_t payload_ready, int64_t host_flag, int64_t host_counts,
+                                 int64_t stream_handle) {
+  require(library.reinsert_group != nullptr && library.copy_words != nullptr,
+          "library entry points are not bound");
+  const ReinsertTable t = reinsert_table_words(keys, values, positions, head_lens, packed_offsets, 1);
+  const int64_t count = metadata.size(0);
+  require(metadata.is_cuda() && metadata.device() == t.device && metadata.is_contiguous() &&
+              metadata.scalar_type() == torch::kInt64 && metadata.dim() == 2 &&
+              metadata.size(1) == 3,
+          "Recall metadata must be an int64 [count, 3] array");
+  require(payload.is_cuda() && payload.device() == t.device && payload.is_contiguous() &&
+              payload.scalar_type() == t.dtype && payload.dim() == 3 && payload.size(0) == count &&
+              payload.size(1) == 2 && payload.size(2) == t.dim,
+          "Recalled payload must match the cache dtype and head dim");
+  void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
+  const torch::Device device = t.device;
+  const int64_t slots = t.slots, heads = t.heads, layers = slots / heads;
+  int64_t resident_rows = 0;
+  for (int64_t r : t.resident) resident_rows += r;
+  const int64_t out_rows = resident_rows + count;
+  const auto on_device = torch::TensorOptions().device(device);
+  // table and flag word in one upload; the flag starts at zero
+  torch::Tensor block = staging_ring(device).upload(t.words.data(),
+                                                    static_cast<int64_t>(t.words.size()), device,
+                                                    stream);
+  int64_t* table = block.data_ptr<int64_t>();
+  int32_t* flag = reinterpret_cast<int32_t*>(table + slots * LR_REINSERT_WORDS);
+  // one int64 scratch block: the plan's workspace [3 * count], the grouped runs [2 * count],
+  // the recalled rows [count], the layout (i32)
+  const int64_t n = std::max<int64_t>(count, 1);
+  const int64_t layout_words = (slots + layers * (heads + 1) + 1) / 2;
+  torch::Tensor scratch = torch::empty({6 * n + layout_words}, on_device.dtype(torch::kInt64));
+  int64_t* workspace = scratch.data_ptr<int64_t>();
+  int64_t* grouped = workspace + 3 * n;
+  torch::Tensor recalled_rows = scratch.narrow(0, 5 * n, count);
+  torch::Tensor layout = scratch.narrow(0, 6 * n, layout_words).view(torch::kInt32);
+  int32_t* layout_ptr = layout.data_ptr<int32_t>();
+  torch::Tensor out_keys = torch::empty({out_rows, t.dim}, on_device.dtype(t.dtype));
+  torch::Tensor out_values = torch::empty({out_rows, t.dim}, on_device.dtype(t.dtype));
+  torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
+  int64_t* counts = reinterpret_cast<int64_t*>(static_cast<uintptr_t>(host_counts));
+  int64_t* flag_host = reinterpret_cast<int64_t*>(static_cast<uintptr_t>(host_flag));
+  check_call(library.reinsert_group(table, slots, heads, count ? metadata.data_ptr<int64_t>() : nullptr,
+                                    count, grouped, counts, flag, stream));
+  check_call(library.reinsert_plan_layout(table, slots, count ? grouped : nullptr, count, workspace,
+                                          count ? recalled_rows.data_ptr<int64_t>() : nullptr,
+                                          flag, heads, layout_ptr, layout_ptr + slots, stream));
+  check_call(library.copy_words(reinterpret_cast<const int64_t*>(flag), flag_host, 1, stream));
+  c10::Event planned{c10::DeviceType::CUDA};
+  planned.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+  check_call(library.reinsert_resident(table, slots, workspace, count, t.max_length, t.dim,
+                                       static_cast<int>(t.elem), out_rows, dptr(out_keys),
+                                       dptr(out_values), out_positions.data_ptr<float>(), stream));
+  if (payload_ready != 0) {
+    const hipError_t waited = hipStreamWaitEvent(
+        static_cast<hipStream_t>(stream),
+        reinterpret_cast<hipEvent_t>(static_cast<uintptr_t>(payload_ready)), 0);
+    require(waited == hipSuccess, "hipStreamWaitEvent failed on the payload's copy event");
+  }
+  check_call(library.reinsert_recalled(workspace, count, count ? payload.data_ptr() : nullptr,
+                                       t.dim, static_cast<int>(t.elem), out_rows,
+                                       dptr(out_keys), dptr(out_values),
+                                       out_positions.data_ptr<float>(), stream));
+  {
+    py::gil_scoped_release release;
+    planned.synchronize();  // the grouping and the plan only; the merges may still run
+  }
+  const int64_t word = *flag_host;
+  py::list new_lens(layers), offsets(layers + 1);
+  offsets[0] = py::int_(0);
+  int64_t row = 0;
+  for (int64_t l = 0; l < layers; ++l) {
+    py::list lengths(heads);
+    for (int64_t h = 0; h < heads; ++h) {
+      const int64_t slot = l * heads + h;
+      const int64_t length = head_lens[l][h] + counts[slot];
+      lengths[h] = py::int_(length);
+      row += length;
+    }
+    new_lens[l] = lengths;
+    offsets[l + 1] = py::int_(row);
+  }
+  return py::make_tuple(out_keys, out_values, out_positions, layout, recalled_rows, new_lens,
+                        offsets, word);
 }
 
 void* current_stream(const torch::Device& device);
@@ -1312,14 +1492,24 @@ py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
 // logical position]; same checks, order and messages as the reference's host loop. Returns
 // (descriptors int64 [R*H, 7] already copied to `device` on the current stream (from pinned
 // memory, without blocking the host), total output rows, rows of the longest head + 1).
-py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
-                            const std::vector<torch::Tensor>& values,
-                            const std::vector<torch::Tensor>& positions, int64_t heads,
-                            int64_t dim, torch::ScalarType dtype, const torch::Device& device,
-                            const std::vector<std::vector<int64_t>>& lengths,
-                            const std::vector<int64_t>& logical_positions,
-                            int64_t stream_handle) {
-  require(library.copy_words != nullptr, "library entry points are not bound");
+// _C.batch_append (csrc/batch_append.cu:36-94): the reference's descriptor loop and checks
+// (batch_append.cu:49-80), the output allocation and the launch, all here. The descriptors are
+// written into a pinned, host-coherent staging buffer that the kernel reads in place, so the
+// launch needs neither a copy (the reference's copy, batch_append.cu:81, blocks the host) nor a
+// copy kernel. Returns [keys, values, positions [rows, 1]] packed.
+std::vector<torch::Tensor> batch_append_launch(const std::vector<torch::Tensor>& keys,
+                                               const std::vector<torch::Tensor>& values,
+                                               const std::vector<torch::Tensor>& positions,
+                                               const torch::Tensor& new_keys,
+                                               const torch::Tensor& new_values,
+                                               const std::vector<std::vector<int64_t>>& lengths,
+                                               const std::vector<int64_t>& logical_positions,
+                                               int64_t stream_handle) {
+  require(library.batch_append != nullptr && library.staging_alloc != nullptr,
+          "library entry points are not bound");
+  const int64_t heads = new_keys.size(1), dim = new_keys.size(3);
+  const auto dtype = new_keys.scalar_type();
+  const torch::Device device = new_keys.device();
   const size_t requests = keys.size();
   const int64_t row_bytes = dim * c10::elementSize(dtype);
   int64_t granule = 16;
@@ -1364,10 +1554,19 @@ py::tuple plan_batch_append(const std::vector<torch::Tensor>& keys,
     require(source == k.size(0), "Head lengths do not cover cache rows");
   }
   void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
-  torch::Tensor block = host.empty()
-      ? torch::empty({0}, torch::TensorOptions().device(device).dtype(torch::kInt64))
-      : staging_ring(device).upload(host.data(), static_cast<int64_t>(host.size()), device, stream);
-  return py::make_tuple(block, destination, maximum);
+  const auto options = torch::TensorOptions().device(device);
+  torch::Tensor out_keys = torch::empty({destination, dim}, options.dtype(dtype));
+  torch::Tensor out_values = torch::empty({destination, dim}, options.dtype(dtype));
+  torch::Tensor out_positions = torch::empty({destination, 1}, options.dtype(torch::kFloat32));
+  StagingRing& ring = staging_ring(device);
+  const int64_t* descriptors = ring.stage(host.data(), static_cast<int64_t>(host.size()));
+  check_call(library.batch_append(descriptors, static_cast<int64_t>(requests) * heads,
+                                  new_keys.data_ptr(), new_values.data_ptr(), dim,
+                                  static_cast<int>(c10::elementSize(dtype)), maximum,
+                                  out_keys.data_ptr(), out_values.data_ptr(),
+                                  out_positions.data_ptr<float>(), stream));
+  ring.release(device);
+  return {out_keys, out_values, out_positions};
 }
 
 }  // namespace
@@ -1395,8 +1594,12 @@ PYBIND11_MODULE(_plan, module) {
              "Check a reinsertion and build its pinned table + metadata block");
   module.def("reinsert_table", &reinsert_table,
              "Check a reinsertion's layers and upload its table for lr_reinsert_group");
-  module.def("plan_batch_append", &plan_batch_append,
-             "Validate a batch and upload its batch_append descriptors");
+  module.def("bind_reinsert", &bind_reinsert,
+             "Bind the reinsertion entry points of liblazyrecall_hip.so");
+  module.def("reinsert_device", &reinsert_device_launch,
+             "Enqueue a whole device-grouped reinsertion and wait for its plan");
+  module.def("batch_append", &batch_append_launch,
+             "_C.batch_append: checks, descriptors in host-coherent staging, outputs and launch");
   module.attr("LR_SEG_WORDS") = LR_SEG_WORDS;
   module.attr("LR_HEAD_WORDS") = LR_HEAD_WORDS;
 }

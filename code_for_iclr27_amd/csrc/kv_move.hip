@@ -702,17 +702,37 @@ __device__ __forceinline__ bool recall_identity(const int64_t* metadata, int64_t
   return valid;
 }
 
+// A workgroup's identities usually fall in a few slots (a transport batch comes grouped by
+// slot), so each workgroup first counts in LDS and then adds one total per slot it saw: a
+// few hundred global atomics instead of one per identity on a few hundred counters.
+constexpr int kGroupSlotsLds = 4096;  // slots counted in LDS (more: one global atomic each)
+
 __global__ __launch_bounds__(kThreads) void reinsert_count_kernel(
     const int64_t* __restrict__ metadata, int64_t count, int64_t layers, int64_t heads,
     int64_t* __restrict__ table, int32_t* __restrict__ flag) {
+  __shared__ uint32_t local[kGroupSlotsLds];
+  const int64_t slots = layers * heads;
+  const bool in_lds = slots <= kGroupSlotsLds;
+  if (in_lds)
+    for (int64_t k = threadIdx.x; k < slots; k += kThreads) local[k] = 0;
+  __syncthreads();
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= count) return;
-  int64_t slot, position;
-  if (!recall_identity(metadata, i, layers, heads, &slot, &position)) {
-    atomicOr(flag, 4);
-    return;
+  if (i < count) {
+    int64_t slot, position;
+    if (!recall_identity(metadata, i, layers, heads, &slot, &position)) {
+      atomicOr(flag, 4);
+    } else if (in_lds) {
+      atomicAdd(&local[slot], 1u);
+    } else {
+      atomicAdd(reinterpret_cast<unsigned long long*>(table + slot * LR_REINSERT_WORDS + 5), 1ull);
+    }
   }
-  atomicAdd(reinterpret_cast<unsigned long long*>(table + slot * LR_REINSERT_WORDS + 5), 1ull);
+  __syncthreads();
+  if (in_lds)
+    for (int64_t k = threadIdx.x; k < slots; k += kThreads)
+      if (local[k] != 0)
+        atomicAdd(reinterpret_cast<unsigned long long*>(table + k * LR_REINSERT_WORDS + 5),
+                  static_cast<unsigned long long>(local[k]));
 }
 
 __global__ __launch_bounds__(1024) void reinsert_table_kernel(int64_t* __restrict__ table,
@@ -749,16 +769,37 @@ __global__ __launch_bounds__(1024) void reinsert_table_kernel(int64_t* __restric
   }
 }
 
+// Grouping: each workgroup takes, per slot it saw, one range of that slot's run with a
+// single global atomic (its LDS count), then places its identities inside the range by LDS
+// atomics.
 __global__ __launch_bounds__(kThreads) void reinsert_group_kernel(
     const int64_t* __restrict__ metadata, int64_t count, int64_t layers, int64_t heads,
     int64_t* __restrict__ table, int64_t* __restrict__ grouped) {
+  __shared__ uint32_t local[kGroupSlotsLds];
+  __shared__ int64_t base[kGroupSlotsLds];
+  const int64_t slots = layers * heads;
+  const bool in_lds = slots <= kGroupSlotsLds;
+  if (in_lds)
+    for (int64_t k = threadIdx.x; k < slots; k += kThreads) local[k] = 0;
+  __syncthreads();
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (i >= count) return;
-  int64_t slot, position;
-  if (!recall_identity(metadata, i, layers, heads, &slot, &position)) return;
+  int64_t slot = 0, position = 0;
+  const bool valid = i < count && recall_identity(metadata, i, layers, heads, &slot, &position);
+  uint32_t rank = 0;
+  if (valid && in_lds) rank = atomicAdd(&local[slot], 1u);
+  __syncthreads();
+  if (in_lds)
+    for (int64_t k = threadIdx.x; k < slots; k += kThreads)
+      if (local[k] != 0)
+        base[k] = static_cast<int64_t>(atomicAdd(
+            reinterpret_cast<unsigned long long*>(table + k * LR_REINSERT_WORDS + 7),
+            static_cast<unsigned long long>(local[k])));
+  __syncthreads();
+  if (!valid) return;
   int64_t* entry = table + slot * LR_REINSERT_WORDS;
-  const int64_t at = static_cast<int64_t>(
-      atomicAdd(reinterpret_cast<unsigned long long*>(entry + 7), 1ull));
+  const int64_t at = in_lds ? base[slot] + rank
+                            : static_cast<int64_t>(atomicAdd(
+                                  reinterpret_cast<unsigned long long*>(entry + 7), 1ull));
   if (at >= entry[5]) return;  // cannot happen: the count saw the same identities
   grouped[entry[4] + at] = position;
   grouped[count + entry[4] + at] = i;
