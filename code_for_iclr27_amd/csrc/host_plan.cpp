@@ -1172,16 +1172,15 @@ py::tuple reinsert_device_launch(const std::vector<torch::Tensor>& keys,
   // one int64 scratch block: the plan's workspace [3 * count], the grouped runs [2 * count],
   // the recalled rows [count], the layout (i32)
   const int64_t n = std::max<int64_t>(count, 1);
-  const int64_t layout_words = (slots + layers * (heads + 1) + 1) / 2;
+  const int64_t layout_ints = slots + layers * (heads + 1);
+  const int64_t layout_words = (layout_ints + 1) / 2;
   torch::Tensor scratch = torch::empty({6 * n + layout_words}, on_device.dtype(torch::kInt64));
   int64_t* workspace = scratch.data_ptr<int64_t>();
   int64_t* grouped = workspace + 3 * n;
   torch::Tensor recalled_rows = scratch.narrow(0, 5 * n, count);
-  torch::Tensor layout = scratch.narrow(0, 6 * n, layout_words).view(torch::kInt32);
+  torch::Tensor layout =
+      scratch.narrow(0, 6 * n, layout_words).view(torch::kInt32).narrow(0, 0, layout_ints);
   int32_t* layout_ptr = layout.data_ptr<int32_t>();
-  torch::Tensor out_keys = torch::empty({out_rows, t.dim}, on_device.dtype(t.dtype));
-  torch::Tensor out_values = torch::empty({out_rows, t.dim}, on_device.dtype(t.dtype));
-  torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
   int64_t* counts = reinterpret_cast<int64_t*>(static_cast<uintptr_t>(host_counts));
   int64_t* flag_host = reinterpret_cast<int64_t*>(static_cast<uintptr_t>(host_flag));
   check_call(library.reinsert_group(table, slots, heads, count ? metadata.data_ptr<int64_t>() : nullptr,
@@ -1192,6 +1191,10 @@ py::tuple reinsert_device_launch(const std::vector<torch::Tensor>& keys,
   check_call(library.copy_words(reinterpret_cast<const int64_t*>(flag), flag_host, 1, stream));
   c10::Event planned{c10::DeviceType::CUDA};
   planned.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
+  // the merged buffers are allocated while the grouping and the plan run
+  torch::Tensor out_keys = torch::empty({out_rows, t.dim}, on_device.dtype(t.dtype));
+  torch::Tensor out_values = torch::empty({out_rows, t.dim}, on_device.dtype(t.dtype));
+  torch::Tensor out_positions = torch::empty({out_rows}, on_device.dtype(torch::kFloat32));
   check_call(library.reinsert_resident(table, slots, workspace, count, t.max_length, t.dim,
                                        static_cast<int>(t.elem), out_rows, dptr(out_keys),
                                        dptr(out_values), out_positions.data_ptr<float>(), stream));

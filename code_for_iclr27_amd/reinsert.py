@@ -232,20 +232,6 @@ class Reinserter:
         heads = len(lengths[0])
         slots = len(lengths) * heads
         current = torch.cuda.current_stream(device)
-        stream = current.cuda_stream
-        from .audit import _native_planner
-        table, resident, max_length = _native_planner().reinsert_table(
-            *tensors, lengths, packed_offsets, stream)
-        out_rows = sum(resident) + count
-        out_keys = torch.empty((out_rows, dim), dtype=dtype, device=device)
-        out_values = torch.empty_like(out_keys)
-        out_positions = torch.empty((out_rows,), dtype=torch.float32, device=device)
-        recalled_rows = torch.empty((count,), dtype=torch.int64, device=device)
-        workspace = torch.empty((3 * max(count, 1),), dtype=torch.int64, device=device)
-        grouped = torch.empty((2 * max(count, 1),), dtype=torch.int64, device=device)
-        flag = torch.zeros((1,), dtype=torch.int64, device=device)
-        layout = torch.empty((slots + len(lengths) * (heads + 1),), dtype=torch.int32,
-                             device=device)
 
         # copies in, on the side stream: host metadata first (small), then a host payload
         side = self._side_stream(device)
@@ -273,43 +259,42 @@ class Reinserter:
         if meta_ready is not None:
             current.wait_event(meta_ready)
 
-        host_flag = self._host_flag(device)
-        host_counts = self._host_counts(device, slots)
-        _lib.call("lr_reinsert_group", table.data_ptr(), slots, heads,
-                  meta_device.data_ptr() if count else None, count, grouped.data_ptr(),
-                  host_counts, flag.data_ptr(), stream)
-        _lib.call("lr_reinsert_plan_layout", table.data_ptr(), slots,
-                  grouped.data_ptr() if count else None, count, workspace.data_ptr(),
-                  _lib.ptr(recalled_rows), flag.data_ptr(), heads, layout.data_ptr(),
-                  layout.data_ptr() + 4 * slots, stream)
-        _lib.call("lr_copy_words", flag.data_ptr(), host_flag, 1, stream)
-        planned = torch.cuda.Event()
-        planned.record(current)
-        _lib.call("lr_reinsert_resident", table.data_ptr(), slots, workspace.data_ptr(), count,
-                  max_length, dim, keys0.element_size(), out_rows, out_keys.data_ptr(),
-                  out_values.data_ptr(), out_positions.data_ptr(), stream)
-        if payload_ready is not None:
-            current.wait_event(payload_ready)
-        _lib.call("lr_reinsert_recalled", workspace.data_ptr(), count, _lib.ptr(payload_device),
-                  dim, keys0.element_size(), out_rows, out_keys.data_ptr(),
-                  out_values.data_ptr(), out_positions.data_ptr(), stream)
-        planned.synchronize()  # the grouping and the plan only; the merges may still run
-        word = ctypes.c_int64.from_address(host_flag).value
+        # the table upload, the grouping, the plan and both merges are enqueued by the host
+        # module (csrc/host_plan.cpp reinsert_device_launch), which waits for the plan only
+        (out_keys, out_values, out_positions, layout, recalled_rows, new_lens, offsets,
+         word) = _reinsert_module().reinsert_device(
+            *tensors, lengths, packed_offsets, payload_device, meta_device,
+            payload_ready.cuda_event if payload_ready is not None else 0,
+            self._host_flag(device), self._host_counts(device, slots), current.cuda_stream)
         if word & _FLAG_IDENTITY:
             raise ValueError("Invalid recall identity")
         if word & _FLAG_DUPLICATE:
             raise ValueError("Cannot merge duplicate physical KV identities")
         if word & _FLAG_HEAD_LIMIT:
             raise ValueError("Too many recalled rows for one head")
-        counts = np.ctypeslib.as_array((ctypes.c_int64 * slots).from_address(host_counts)).copy()
-        new_lens = (np.asarray(lengths, dtype=np.int64) + counts.reshape(-1, heads)).tolist()
-        offsets = np.concatenate(([0], np.cumsum([sum(row) for row in new_lens]))).tolist()
         merged = PackedLayers(out_keys, out_values, out_positions, new_lens, offsets,
                               layers.sources if packed else list(layers),
                               DeviceLayout(layout, new_lens))
         caller_buffer = source is not None and source is payload
         return ReinsertOutcome(merged, new_lens, recalled_rows, count,
                                payload_ready if caller_buffer else None)
+
+
+_module = None
+
+
+def _reinsert_module():
+    """The C++ host module with the reinsertion entry points bound (once)."""
+    global _module
+    if _module is None:
+        from .audit import _native_planner
+        planner = _native_planner()
+        library = _lib.load()
+        address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
+        planner.bind_reinsert(address("lr_reinsert_group"), address("lr_reinsert_plan_layout"),
+                              address("lr_reinsert_resident"), address("lr_reinsert_recalled"))
+        _module = planner
+    return _module
 
 
 _default = Reinserter()
