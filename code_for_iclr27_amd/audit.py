@@ -302,7 +302,8 @@ class AuditStep:
         ``immediate`` None (or >= count) removes every selected slot now; the lazy queue
         ``references[immediate:]`` is then empty and the removal sets are all the step needs,
         so the queue order (``outcome.selection.values/segments/positions``) is computed only
-        with ``queue_order=True``, on a side stream, overlapping the compaction.
+        with ``queue_order=True``, on the step's stream between the selection and the
+        compaction (``native=False``: on a side stream beside the compaction).
         ``0 <= immediate < count`` is the lazy form: the queue order is computed, its first
         ``immediate`` slots are removed (with 0 the layers are returned as they are) and the rest
         stay queued on the device as ``outcome.queue`` (an EvictionQueue) for evict_prefix.
@@ -486,34 +487,14 @@ class AuditStep:
         new_layers = PackedLayers(out_keys, out_values, out_positions, new_lens, offsets, layers)
         return AuditOutcome(new_layers, new_lens, raw, pooled, selection, plan, count)
 
-    def _queue_native(self, selection, plan, device_block, select_ws, count, sets_done, device):
-        """lr_select_refine_queue (controller.py:148-158's references order) on the side stream,
-        after the removal sets; fills selection.values/segments/positions."""
-        stream = self._queue_stream(device)
-        values = torch.empty((count,), dtype=torch.float32, device=device)
-        order = torch.empty((2 * count,), dtype=torch.int64, device=device)
-        stream.wait_event(sets_done)
-        starts = plan.part("starts", device_block)
-        _lib.call("lr_select_refine_queue", starts.data_ptr(), plan.total, plan.segment_count,
-                  count, select_ws.data_ptr(), select_ws.numel(), selection.quotas.data_ptr(),
-                  selection.offsets.data_ptr(), values.data_ptr(), order.data_ptr(),
-                  order[count:].data_ptr(), stream.cuda_stream)
-        ready = torch.cuda.Event()
-        ready.record(stream)
-        # memory the side stream uses stays reserved until that stream's work is done
-        for tensor in (select_ws, values, order, selection.quotas, selection.offsets, device_block):
-            tensor.record_stream(stream)
-        selection.values, selection.segments, selection.positions = values, order[:count], order[count:]
-        selection.queue_ready = ready
-
     def _run_native(self, layers, query_positions, margin, count, protect_recent, pool_kernel,
                     denominator_epsilon, check_finite, timer=None, queue_order=False,
                     immediate=-1, transport=None):
         """The step with planning and every launch done by the C++ host module
         (csrc/host_plan.cpp audit_launch): no Python between the launches. With
-        ``queue_order`` the queue half of the selection runs on a side stream after the
-        removal sets (an event recorded between the selection and the compaction), and the
-        current stream joins it before the step's synchronisation."""
+        ``queue_order`` the queue half of the selection follows the removal sets on the same
+        stream, before the compaction: on a side stream its small launches waited for the
+        compaction's workgroups to free the CUs, which cost more than running them first."""
         if len(layers) == 0:
             raise RuntimeError("No layers to score")
         planner = _native_planner()
@@ -521,15 +502,6 @@ class AuditStep:
         sync = self._sync_for(device)
         margin = margin.to(device=device, dtype=torch.float32).reshape(1)
         mark = None if timer is None else timer.mark
-        sets_done = None
-        if queue_order:
-            sets_done = torch.cuda.Event()
-
-            def mark(name, inner=mark):
-                if name == "select":
-                    sets_done.record()
-                if inner is not None:
-                    inner(name)
         (block, meta, segment_info, head_info, scores, info, quotas, offsets, removed, changed,
          out_keys, out_values, out_positions, device_block, select_ws,
          queue_state, layout) = planner.audit_launch(
@@ -540,12 +512,13 @@ class AuditStep:
             int(protect_recent), query_positions, margin, int(count), int(immediate),
             int(pool_kernel), float(denominator_epsilon),
             torch.cuda.current_stream(device).cuda_stream, mark, sync,
-            _archive_hook(transport, layers[0].keys, _removed_now(layers, count, immediate)))
+            _archive_hook(transport, layers[0].keys, _removed_now(layers, count, immediate)),
+            bool(queue_order))
         plan = SegmentPlan(block, meta, segment_info, head_info, len(layers[0].head_lens))
         total = plan.total
         count = min(max(0, int(count)), total)
         selection = None
-        if queue_state is not None:  # the lazy form
+        if queue_state is not None and len(queue_state) == 3:  # the lazy form
             values, order, rank = queue_state
             selection = DeviceSelection(values, order[:count], order[count:], quotas, offsets,
                                         removed, changed, plan.segment_info[:2].T)
@@ -563,12 +536,10 @@ class AuditStep:
         if count:
             selection = DeviceSelection(None, None, None, quotas, offsets, removed, changed,
                                         plan.segment_info[:2].T)
-            if queue_order:
-                self._queue_native(selection, plan, device_block, select_ws, count, sets_done,
-                                   device)
-                selection.wait_queue()  # join the queue order back before the step ends
-                if timer is not None:
-                    timer.mark("queue_join")
+            if queue_state is not None:  # the queue order, computed before the compaction
+                values, order = queue_state
+                selection.values = values
+                selection.segments, selection.positions = order[:count], order[count:]
         # waits for the selection only; the compaction may still run (outputs in stream order)
         kept, offsets = sync.wait(check_finite)
         new_layers = PackedLayers(out_keys, out_values, out_positions, kept, offsets, layers,

@@ -578,7 +578,8 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
                        int64_t protect_recent, const torch::Tensor& query_positions,
                        const torch::Tensor& margin, int64_t count, int64_t immediate,
                        int64_t pool_kernel, double epsilon, int64_t stream_handle,
-                       const py::object& mark, StepSync* sync, const py::object& archive) {
+                       const py::object& mark, StepSync* sync, const py::object& archive,
+                       bool order_queue) {
   require(library.score_segments != nullptr, "library entry points are not bound");
   require(pool_kernel > 0 && pool_kernel % 2 == 1, "pool kernel must be a positive odd integer");
   // with a StepSync the block goes through its staging buffer, so it need not be pinned
@@ -649,6 +650,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   }
   torch::Tensor sets, quotas, offsets, removed, changed, select_ws;
   torch::Tensor queue_values, queue_order, queue_rank, batch;
+  torch::Tensor queue_order_out;  // the eager step's queue order (order_queue)
   torch::Tensor layout;  // device i32: head lengths [slots], then cumulative [layers, H + 1]
   if (lazy) {
     const size_t select_bytes = library.select_workspace_bytes(plan.total, S, count);
@@ -721,6 +723,18 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
         nonfinite, stream));
     stage("select");
     if (sync != nullptr) sync->post(plan, device);
+    if (order_queue) {
+      // the eviction queue's order too (every selected slot leaves now, so the removal sets do
+      // not depend on it): on this stream, before the compaction
+      queue_values = torch::empty({count}, on_device.dtype(torch::kFloat32));
+      queue_order_out = torch::empty({2 * count}, on_device.dtype(torch::kInt64));
+      int64_t* queue_segments = queue_order_out.data_ptr<int64_t>();
+      check_call(library.select_refine_queue(
+          words + plan.starts_at(), plan.total, S, count, dptr(select_ws), select_bytes,
+          quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(), queue_values.data_ptr<float>(),
+          queue_segments, queue_segments + count, stream));
+      stage("queue");
+    }
     try {
       archive_removals(archive, words + plan.heads_at(), plan.slots, plan.slots / plan.layers,
                        quotas.data_ptr<int64_t>(), offsets.data_ptr<int64_t>(),
@@ -752,6 +766,7 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   }
   py::object queue = py::none();
   if (lazy) queue = py::make_tuple(queue_values, queue_order, queue_rank);
+  else if (queue_order_out.defined()) queue = py::make_tuple(queue_values, queue_order_out);
   py::object layout_out = py::none();
   if (layout.defined()) layout_out = py::cast(layout);
   return py::make_tuple(plan.block, plan.meta(), plan.segment_info, plan.head_info, scores, info,
