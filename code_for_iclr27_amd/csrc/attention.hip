@@ -43,7 +43,11 @@ constexpr int kAttnThreads = 64 * kAttnWaves;
 constexpr int wave_keys(int dim) { return dim == 256 ? 32 : 6144 / dim; }
 constexpr int kSmallWaveKeys = 16;
 constexpr int64_t kFewBlocks = 512;
-constexpr int kMergeUnroll = 4;       // partial blocks each merging thread loads at once
+// Partial blocks each merging thread loads at once: four, or twelve where a thread folds more
+// than four blocks (batch-1 decode: cfg1's 36 blocks per unit take one round of loads instead
+// of three; measured 14.9 against 15.3 us per layer, and no better for cfg2's 12 blocks).
+constexpr int kMergeUnroll = 4;
+constexpr int kMergeUnrollWide = 12;
 constexpr float kAttnLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -378,9 +382,10 @@ __global__ __launch_bounds__(kAttnThreads, D == 256 ? 2 : 3) void packed_attenti
 }
 
 // Second launch: one workgroup per (segment, tile) whose keys spanned more than one block merges
-// the blocks' partial states. Thread (part, item) folds blocks part, part + PARTS, ... with the
-// loads of kMergeUnroll blocks in flight at once; the PARTS states then meet in LDS.
-template <typename T, int D, int R, int CH>
+// the blocks' partial states. Thread (part, item) folds blocks part, part + PARTS, ... (in that
+// order, whatever U) with the loads of U blocks in flight at once; the PARTS states then meet
+// in LDS.
+template <typename T, int D, int R, int CH, int U>
 __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs a) {
   constexpr int LPK = D / 8;
   constexpr int ITEMS = R * LPK;
@@ -409,11 +414,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs 
   const int r = item / LPK, cc = item - r * LPK;
   const int64_t first = unit * a.splits * R;
   MergeState total{kNegInf, 0.f, {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};
-  for (int64_t k0 = part; k0 < needed; k0 += PARTS * kMergeUnroll) {
-    float mk[kMergeUnroll], lk[kMergeUnroll];
-    attn_f32x4 lo[kMergeUnroll], hi[kMergeUnroll];
+  for (int64_t k0 = part; k0 < needed; k0 += PARTS * U) {
+    float mk[U], lk[U];
+    attn_f32x4 lo[U], hi[U];
 #pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       int64_t k = k0 + u * PARTS;
       const bool live = k < needed;
       k = live ? k : k0;
@@ -424,7 +429,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_merge_kernel(AttnArgs 
       hi[u] = *reinterpret_cast<const attn_f32x4*>(a.part_o + at * D + 8 * cc + 4);
     }
 #pragma unroll
-    for (int u = 0; u < kMergeUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const float o[8] = {lo[u][0], lo[u][1], lo[u][2], lo[u][3],
                           hi[u][0], hi[u][1], hi[u][2], hi[u][3]};
       merge_into(total, mk[u], lk[u], o);
@@ -485,9 +490,16 @@ int launch_attention(const AttnArgs& args, int64_t blocks, hipStream_t stream) {
                      dim3(kAttnThreads), 0, stream, args);
   if (int status = check_launch("packed_attention")) return status;
   if (args.splits == 1) return LR_OK;
-  hipLaunchKernelGGL((attention_merge_kernel<T, D, R, CH>),
-                     dim3(static_cast<unsigned>(blocks / args.splits)), dim3(kAttnThreads), 0,
-                     stream, args);
+  // blocks each merging thread folds: PARTS = threads / (R * D / 8) threads share a row slice
+  const int64_t per_part = ceil_div(args.splits, int64_t{kAttnThreads / (R * D / 8)});
+  if (per_part > kMergeUnroll)
+    hipLaunchKernelGGL((attention_merge_kernel<T, D, R, CH, kMergeUnrollWide>),
+                       dim3(static_cast<unsigned>(blocks / args.splits)), dim3(kAttnThreads), 0,
+                       stream, args);
+  else
+    hipLaunchKernelGGL((attention_merge_kernel<T, D, R, CH, kMergeUnroll>),
+                       dim3(static_cast<unsigned>(blocks / args.splits)), dim3(kAttnThreads), 0,
+                       stream, args);
   return check_launch("packed_attention merge");
 }
 
