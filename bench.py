@@ -7,7 +7,9 @@ Headline metric: one full audit step on the Llama-3.1-8B cache (cfg1:
 of every layer. value = algorithmic bytes of the step / measured step time (GB/s).
 
 The step removes every selected slot at once, so the eviction queue it leaves is empty and its
-order is not computed (queue_order_ms_per_step times the step with that order computed too).
+order is not computed (queue_order_ms_per_step times the step with that order computed too,
+over as many steps and warm-up steps as the headline, so that the two compare: a shorter run
+carries a larger share of the first step's exposed host work).
 
 Also reported on the same line:
   roofline      the dominant kernel, timed with HIP events on its stream inside the timed loop
@@ -889,9 +891,11 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     dominant_us = average_stages(timers)[dominant]
     # the same step with the eviction-queue order computed too (it is empty here: every
-    # selected slot is removed at once, so the removal sets do not depend on it)
-    queue_steps = max(3, min(args.steps, 20))
-    _, _, queue_elapsed, _ = timed(queue_steps, lambda i: None, True, warmup=3)
+    # selected slot is removed at once, so the removal sets do not depend on it), timed like
+    # the headline (in 20 steps after 3 warm-up ones the first step's exposed host planning
+    # added ~40 us a step)
+    queue_steps = args.steps
+    _, _, queue_elapsed, _ = timed(queue_steps, lambda i: None, True, warmup=args.warmup)
     rows_total = sum(layer.keys.size(0) for layer in layers)
     candidates = int(outcome.scores.numel())
     segments = len(outcome.segments)

@@ -721,23 +721,77 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
 
 // ---------------------------------------------------------------------------------------
 // Queue order. Per segment, both pick lists are put in (key, index) order: the raw picks give
-// the segment's slots, the pooled picks what fills them (transplant). One 1024-thread
-// workgroup per segment; the sort depends on the list's length n:
-//   n <= kRankSortMax: rank sort in LDS, each entry's rank (entries with a smaller key, or an
-//     equal key at a lower index) counted by four lanes over interleaved quarters of the list
-//     and summed across the quad, so a lane's chain of LDS reads is a quarter as long;
-//   n <= kBitonicMax: a bitonic network over (key << 32 | index) pairs in LDS;
+// the segment's slots, the pooled picks what fills them (transplant). Slot j of the global
+// order is then the j-th smallest raw pick over all segments, by (key, index), and takes the
+// pooled pick of its segment at its rank within that segment.
+//
+// Up to kOrderMaxRuns segments, the global order is a bucketed merge of the sorted runs (three
+// launches):
+//   1. order_splitters_kernel: `samples` raw picks at a fixed stride of the concatenated
+//      index-order lists, as (key << 32 | list position) composites. Composites are unique and
+//      their order is the final (key, index) order. Each workgroup counts the rank of
+//      kSplitterSamples of them among all samples in LDS; the sample of rank
+//      ((b + 1) * samples) / buckets - 1 is splitter b, so the splitters cut the picks into
+//      `buckets` ranges.
+//   2. segment_sort_kernel: sorts each segment's two lists in LDS, then binary-searches every
+//      splitter in the sorted raw list: bucket_pos[b][s] = how many of segment s's picks lie
+//      at or below splitter b.
+//   3. order_bucket_kernel (one workgroup per bucket): gathers its bucket's picks (a
+//      contiguous range of every segment's sorted run), sorts them in LDS, and writes each one
+//      at (picks below the bucket) + (rank within it), with its segment and transplanted
+//      position. A bucket larger than LDS holds is sorted in global memory instead.
+// More segments than that: the runs are sorted the same way and rocPRIM's device radix sort
+// orders the concatenation, then emit_kernel writes the slots.
+//
+// Per-segment sorts, by list length n:
+//   n <= kRankSortMax: both lists at once, one half of the workgroup each; each entry's rank
+//     (entries whose (key << 32 | index) composite is smaller: a smaller key, or an equal key
+//     at a lower index) is counted by one, two or four lanes over interleaved parts of the
+//     list in LDS and summed across them;
+//   n <= kBitonicMax: a bitonic network over (key << 32 | index) pairs in LDS, one list after
+//     the other;
 //   longer lists: the block radix sort in global memory.
-// Both in-LDS sorts keep equal keys in index order.
-constexpr int kSortThreads = 1024;       // segment_sort workgroups
-constexpr uint32_t kRankSortMax = 512;
+// Every sort keeps equal keys in index order.
+constexpr int kSortThreads = 1024;       // segment_sort and splitter workgroups
+constexpr uint32_t kRankSortMax = kSortThreads / 2;
 constexpr uint32_t kBitonicMax = 4096;
+constexpr int64_t kOrderMaxRuns = 1024;  // segments the bucketed order takes (LDS run tables)
+constexpr uint32_t kOrderSamples = 2048;
+constexpr int64_t kOrderBucketTarget = 128;  // mean picks per bucket
+constexpr uint32_t kOrderMaxBuckets = 1024;
+constexpr int kBucketThreads = 512;
+constexpr uint32_t kBucketCap = 4096;  // bucket entries sorted in LDS
+
+struct OrderShape {
+  bool bucketed;
+  uint32_t samples, stride, buckets;
+};
+
+// samples >= buckets, so the splitters (sorted samples at indexes ((b + 1) * samples) / buckets
+// - 1) are distinct and increasing.
+inline OrderShape order_shape(int64_t segments, int64_t count) {
+  OrderShape o{};
+  o.bucketed = segments <= kOrderMaxRuns && count > 0;
+  if (!o.bucketed) return o;
+  o.samples = static_cast<uint32_t>(count < kOrderSamples ? count : kOrderSamples);
+  o.stride = static_cast<uint32_t>(count / o.samples);
+  int64_t b = ceil_div(count, kOrderBucketTarget);
+  if (b > kOrderMaxBuckets) b = kOrderMaxBuckets;
+  if (b > o.samples) b = o.samples;
+  o.buckets = static_cast<uint32_t>(b < 1 ? 1 : b);
+  return o;
+}
+
+constexpr uint32_t kSplitterSamples = 64;  // samples ranked per splitter workgroup
+
+struct RankLds {
+  alignas(16) uint64_t composite[2][kRankSortMax];  // (key << 32 | index), padded with ~0
+  uint32_t values[kRankSortMax];
+  uint64_t sorted[kRankSortMax];  // the raw list's (key << 32 | offset + index) at their ranks
+};
 
 union SegmentSortLds {
-  struct {
-    uint32_t keys[kRankSortMax + 16];
-    uint32_t values[kRankSortMax];
-  } rank;
+  RankLds rank;
   struct {
     uint64_t pairs[kBitonicMax];
     uint32_t local[kBitonicMax];
@@ -745,45 +799,57 @@ union SegmentSortLds {
   SortLds<kSortThreads> radix;
 };
 
-// keys[0, n) (index order; values[0, n) with them, if given) sorted by (key, index) in place.
-__device__ __forceinline__ void rank_sort_quads(uint32_t* keys, uint32_t* values, uint32_t n,
-                                                SegmentSortLds& lds) {
-  uint32_t* lk = lds.rank.keys;
-  for (uint32_t i = threadIdx.x; i < ((n + 15) & ~15u); i += kSortThreads) {
-    lk[i] = i < n ? keys[i] : 0xffffffffu;
-    if (values != nullptr && i < n) lds.rank.values[i] = values[i];
+// Both lists of a segment (n <= kRankSortMax each) sorted by (key, index) in place: threads
+// [0, kRankSortMax) rank the raw keys, the rest the pooled picks (keys, with their local
+// indexes). With `composites`, the raw list's (key << 32 | offset + index) are left at their
+// ranks in lds.sorted.
+__device__ __forceinline__ void rank_sort_lists(uint32_t* raw_keys, uint32_t* pooled_keys,
+                                                uint32_t* pooled_local, uint32_t n,
+                                                uint32_t offset, bool composites,
+                                                RankLds& lds) {
+  const uint32_t list = threadIdx.x / kRankSortMax, t = threadIdx.x % kRankSortMax;
+  const uint32_t n2 = (n + 1) & ~1u;
+  uint64_t* lc = lds.composite[list];
+  const uint32_t* src = list == 0 ? raw_keys : pooled_keys;
+  for (uint32_t i = t; i < n2; i += kRankSortMax) {
+    lc[i] = i < n ? (static_cast<uint64_t>(src[i]) << 32) | i : ~0ull;
+    if (list == 1 && i < n) lds.values[i] = pooled_local[i];
   }
   __syncthreads();
-  const uint32_t quarter = threadIdx.x & 3;
-  // every lane of a quad runs the same trip count (the quad shares its entry)
-  for (uint32_t base = 0; base < n; base += kSortThreads / 4) {
-    const uint32_t i = base + (threadIdx.x >> 2);
-    const uint32_t key = i < n ? lk[i] : 0xffffffffu;
-    uint32_t rank = 0;
-    for (uint32_t j = 4 * quarter; j < n; j += 16) {
-      // padding keys (0xffffffff at j >= n > i) are never below `key` nor equal at a lower
-      // index
-      const uint4 k4 = *reinterpret_cast<const uint4*>(lk + j);
-      rank += (k4.x < key) | ((k4.x == key) & (j < i));
-      rank += (k4.y < key) | ((k4.y == key) & (j + 1 < i));
-      rank += (k4.z < key) | ((k4.z == key) & (j + 2 < i));
-      rank += (k4.w < key) | ((k4.w == key) & (j + 3 < i));
-    }
-    rank += __shfl_xor(rank, 1, 64);
-    rank += __shfl_xor(rank, 2, 64);
-    if (quarter == 0 && i < n) {
-      keys[rank] = key;
-      if (values != nullptr) values[rank] = lds.rank.values[i];
+  // lanes per entry (uniform): every lane of a group runs the same trip count
+  const uint32_t lanes = n <= kRankSortMax / 4 ? 4u : n <= kRankSortMax / 2 ? 2u : 1u;
+  const uint32_t i = t / lanes, part = t % lanes;
+  const uint64_t mine = i < n ? lc[i] : ~0ull;
+  uint32_t rank = 0;
+  // composites are unique; the padding (~0) is never below a real one. Unrolled so that
+  // several LDS reads are in flight (the loop is bound by their latency, not by VALU issue).
+#pragma unroll 8
+  for (uint32_t j = 2 * part; j < n2; j += 2 * lanes) {
+    const ulonglong2 c2 = *reinterpret_cast<const ulonglong2*>(lc + j);
+    rank += c2.x < mine;
+    rank += c2.y < mine;
+  }
+  if (lanes >= 2) rank += __shfl_xor(rank, 1, 64);
+  if (lanes == 4) rank += __shfl_xor(rank, 2, 64);
+  if (part == 0 && i < n) {
+    const uint32_t key = static_cast<uint32_t>(mine >> 32);
+    if (list == 0) {
+      raw_keys[rank] = key;
+      if (composites) lds.sorted[rank] = mine + offset;
+    } else {
+      pooled_keys[rank] = key;
+      pooled_local[rank] = lds.values[i];
     }
   }
   __syncthreads();
 }
 
-// Ascending sort of a[0, n2), n2 a power of two, by all kSortThreads threads.
+// Ascending sort of a[0, n2), n2 a power of two, by all BLOCK threads.
+template <int BLOCK>
 __device__ __forceinline__ void bitonic_sort_lds(uint64_t* a, uint32_t n2) {
   for (uint32_t size = 2; size <= n2; size <<= 1) {
     for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-      for (uint32_t t = threadIdx.x; t < n2 / 2; t += kSortThreads) {
+      for (uint32_t t = threadIdx.x; t < n2 / 2; t += BLOCK) {
         const uint32_t i = 2 * t - (t & (stride - 1));  // lower element of pair t
         const uint64_t x = a[i], y = a[i + stride];
         if ((x > y) == ((i & size) == 0)) {
@@ -796,61 +862,282 @@ __device__ __forceinline__ void bitonic_sort_lds(uint64_t* a, uint32_t n2) {
   }
 }
 
+// bucket_pos[b * segments + s] for splitter b = threadIdx.x (its value in `split`): the number
+// of entries r of the sorted run with composite(r) <= split (binary search).
+template <typename CompositeAt>
+__device__ __forceinline__ void partition_run(uint32_t n, CompositeAt composite, uint64_t split,
+                                              uint32_t buckets, int64_t s, int64_t segments,
+                                              uint32_t* __restrict__ bucket_pos) {
+  const uint32_t b = threadIdx.x;
+  if (b + 1 >= buckets) return;
+  uint32_t lo = 0, hi = n;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (composite(mid) <= split) lo = mid + 1;
+    else hi = mid;
+  }
+  bucket_pos[b * segments + s] = lo;
+}
+
+// One workgroup per segment. In the bucketed order (buckets > 0) it also partitions the sorted
+// raw run by the buckets - 1 splitters; otherwise it writes each slot's position in the
+// concatenated runs for the device radix sort.
 __global__ __launch_bounds__(kSortThreads) void segment_sort_kernel(
     const int64_t* __restrict__ quotas, const int64_t* __restrict__ offsets,
     uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_slots,
     uint32_t* __restrict__ refined_keys, uint32_t* __restrict__ refined_local,
-    uint32_t* __restrict__ tmp_keys, uint32_t* __restrict__ tmp_values) {
+    uint32_t* __restrict__ tmp_keys, uint32_t* __restrict__ tmp_values,
+    const uint64_t* __restrict__ splitters, uint32_t buckets, uint32_t* __restrict__ bucket_pos,
+    int64_t segments) {
+  static_assert(kOrderMaxBuckets <= kSortThreads, "one splitter per thread");
   __shared__ SegmentSortLds lds;
   const int64_t s = blockIdx.x;
+  const bool order = buckets > 0;  // the bucketed order (buckets == 1: no splitters)
+  // independent loads, issued together: thread b's splitter, the segment's list
+  const uint64_t split = threadIdx.x + 1 < buckets ? splitters[threadIdx.x] : 0ull;
   const uint32_t quota = static_cast<uint32_t>(quotas[s]);
-  if (quota == 0) return;
-  const int64_t offset = offsets[s];
+  const uint32_t offset = static_cast<uint32_t>(offsets[s]);
+  if (quota == 0) {
+    if (threadIdx.x + 1 < buckets) bucket_pos[threadIdx.x * segments + s] = 0u;
+    return;
+  }
+  uint32_t* keys = run_keys + offset;
   if (quota <= kRankSortMax) {
-    rank_sort_quads(run_keys + offset, nullptr, quota, lds);
-    rank_sort_quads(refined_keys + offset, refined_local + offset, quota, lds);
+    rank_sort_lists(keys, refined_keys + offset, refined_local + offset, quota, offset, order,
+                    lds.rank);
+    if (order)
+      partition_run(quota, [&](uint32_t r) { return lds.rank.sorted[r]; }, split, buckets, s,
+                    segments, bucket_pos);
   } else if (quota <= kBitonicMax) {
     uint32_t n2 = 1;
     while (n2 < quota) n2 <<= 1;
     uint64_t* pairs = lds.bitonic.pairs;
     for (uint32_t i = threadIdx.x; i < n2; i += kSortThreads)
-      pairs[i] = i < quota ? (static_cast<uint64_t>(run_keys[offset + i]) << 32) | i : ~0ull;
+      pairs[i] = i < quota ? (static_cast<uint64_t>(keys[i]) << 32) | i : ~0ull;
     __syncthreads();
-    bitonic_sort_lds(pairs, n2);
+    bitonic_sort_lds<kSortThreads>(pairs, n2);
     for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads)
-      run_keys[offset + i] = static_cast<uint32_t>(pairs[i] >> 32);
+      keys[i] = static_cast<uint32_t>(pairs[i] >> 32);
+    if (order)
+      partition_run(quota, [&](uint32_t r) { return pairs[r] + offset; }, split, buckets, s,
+                    segments, bucket_pos);
     __syncthreads();  // the raw list's readers are done with the LDS
     for (uint32_t i = threadIdx.x; i < n2; i += kSortThreads) {
       pairs[i] = i < quota ? (static_cast<uint64_t>(refined_keys[offset + i]) << 32) | i : ~0ull;
       if (i < quota) lds.bitonic.local[i] = refined_local[offset + i];
     }
     __syncthreads();
-    bitonic_sort_lds(pairs, n2);
+    bitonic_sort_lds<kSortThreads>(pairs, n2);
     for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads) {
       const uint64_t pair = pairs[i];
       refined_keys[offset + i] = static_cast<uint32_t>(pair >> 32);
       refined_local[offset + i] = lds.bitonic.local[static_cast<uint32_t>(pair)];
     }
   } else {
-    for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads) run_slots[offset + i] = 0u;
+    // payload: each raw pick's index in the segment's list
+    for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads) run_slots[offset + i] = i;
     __syncthreads();
-    block_radix_sort<kSortThreads>(run_keys + offset, run_slots + offset, tmp_keys + offset,
+    block_radix_sort<kSortThreads>(keys, run_slots + offset, tmp_keys + offset,
                                    tmp_values + offset, quota, lds.radix);
+    if (order) {
+      const uint32_t* index = run_slots + offset;
+      partition_run(quota,
+                    [&](uint32_t r) {
+                      return (static_cast<uint64_t>(keys[r]) << 32) | (offset + index[r]);
+                    },
+                    split, buckets, s, segments, bucket_pos);
+    }
     block_radix_sort<kSortThreads>(refined_keys + offset, refined_local + offset,
                                    tmp_keys + offset, tmp_values + offset, quota, lds.radix);
   }
-  // Slot payload for the global order: position in the concatenated runs.
-  for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads)
-    run_slots[offset + i] = static_cast<uint32_t>(offset + i);
+  if (!order) {
+    __syncthreads();
+    // slot payload for the device radix sort: position in the concatenated runs
+    for (uint32_t i = threadIdx.x; i < quota; i += kSortThreads) run_slots[offset + i] = offset + i;
+  }
 }
 
-// Global slot order: the runs are concatenated in segment (= index) order and each is sorted
-// by (key, index), so a stable radix sort of the concatenation by key alone gives the
-// (key, index) order of torch.topk(largest=False, sorted=True). It is rocPRIM's device radix
-// sort (a plain library sort of `count` key/slot pairs).
-size_t order_sort_bytes(int64_t count) {
+// Splitters of the bucketed order from the index-order raw picks (before segment_sort sorts
+// them): sample j is the pick at list position j * stride. Workgroup w ranks samples
+// [w * kSplitterSamples, ...), each by kSortThreads / kSplitterSamples lanes over interleaved
+// parts of all samples in LDS.
+__global__ __launch_bounds__(kSortThreads) void order_splitters_kernel(
+    const uint32_t* __restrict__ run_keys, uint32_t samples, uint32_t stride, uint32_t buckets,
+    uint64_t* __restrict__ splitters) {
+  constexpr uint32_t kLanes = kSortThreads / kSplitterSamples;
+  static_assert(kLanes <= 64 && 64 % kLanes == 0, "a sample's lanes share a wave");
+  __shared__ uint64_t all[kOrderSamples];
+  for (uint32_t j = threadIdx.x; j < samples; j += kSortThreads) {
+    const uint32_t at = j * stride;
+    all[j] = (static_cast<uint64_t>(run_keys[at]) << 32) | at;
+  }
+  __syncthreads();
+  const uint32_t j = blockIdx.x * kSplitterSamples + threadIdx.x / kLanes;
+  const uint32_t part = threadIdx.x % kLanes;
+  const uint64_t mine = j < samples ? all[j] : ~0ull;
+  uint32_t rank = 0;
+#pragma unroll 8
+  for (uint32_t k = part; k < samples; k += kLanes) rank += all[k] < mine;
+#pragma unroll
+  for (uint32_t o = 1; o < kLanes; o <<= 1) rank += __shfl_xor(rank, o, 64);
+  if (part != 0 || j >= samples) return;
+  // splitter b is the sample of rank ((b + 1) * samples) / buckets - 1; samples >= buckets, so
+  // at most one b maps to a rank: the least m = b + 1 with (m * samples) / buckets > rank
+  const uint64_t m = ((static_cast<uint64_t>(rank) + 1) * buckets + samples - 1) / samples;
+  if (m >= 1 && m < buckets && (m * samples) / buckets - 1 == rank) splitters[m - 1] = mine;
+}
+
+struct BucketLds {
+  uint32_t lo[kOrderMaxRuns];         // the bucket's first entry in each sorted run
+  uint32_t start[kOrderMaxRuns + 1];  // exclusive prefix of the runs' shares
+  uint32_t offset[kOrderMaxRuns];     // each run's position in the concatenation
+  uint32_t wave_sums[kBucketThreads / 64][2];
+  union alignas(16) {
+    uint64_t pairs[kBucketCap];
+    SortLds<kBucketThreads> radix;
+  };
+};
+
+// Bucket b: the picks above splitter b - 1 and at or below splitter b (composite order). Each
+// gathered entry e carries (key << 32 | e); e runs over the segments in order and within a run
+// in sorted order, so for equal keys e order is index order and (key, e) order is the final
+// order. Entries of buckets larger than kBucketCap go through spill_* (global, disjoint
+// ranges per bucket) and the block radix sort.
+__global__ __launch_bounds__(kBucketThreads) void order_bucket_kernel(
+    const uint32_t* __restrict__ run_keys, const int64_t* __restrict__ quotas,
+    const int64_t* __restrict__ offsets, const uint32_t* __restrict__ bucket_pos,
+    int64_t segments, uint32_t buckets, const int64_t* __restrict__ position_starts,
+    const uint32_t* __restrict__ refined_local, uint32_t* __restrict__ spill_keys,
+    uint32_t* __restrict__ spill_entries, uint32_t* __restrict__ spill_keys2,
+    uint32_t* __restrict__ spill_entries2, float* __restrict__ out_values,
+    int64_t* __restrict__ out_segments, int64_t* __restrict__ out_positions) {
+  __shared__ BucketLds lds;
+  const uint32_t b = blockIdx.x;
+  const int S = static_cast<int>(segments);
+  constexpr int kPer = (kOrderMaxRuns + kBucketThreads - 1) / kBucketThreads;
+  // each thread's runs [first, first + kPer): shares in this bucket, and picks below it
+  const int first = threadIdx.x * kPer;
+  uint32_t share[kPer], share_sum = 0, below_sum = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int s = first + k;
+    share[k] = 0;
+    if (s < S) {
+      const uint32_t lo = b == 0 ? 0u : bucket_pos[static_cast<int64_t>(b - 1) * S + s];
+      const uint32_t hi = b + 1 == buckets ? static_cast<uint32_t>(quotas[s])
+                                           : bucket_pos[static_cast<int64_t>(b) * S + s];
+      lds.lo[s] = lo;
+      lds.offset[s] = static_cast<uint32_t>(offsets[s]);
+      share[k] = hi - lo;
+      share_sum += hi - lo;
+      below_sum += lo;
+    }
+  }
+  uint32_t before, unused, size, base;
+  block_scan_pair<kBucketThreads>(share_sum, below_sum, lds.wave_sums, before, unused, size, base);
+  if (size == 0) return;  // uniform
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int s = first + k;
+    if (s < S) lds.start[s] = before;
+    before += share[k];
+  }
+  if (threadIdx.x == 0) lds.start[S] = size;
+  __syncthreads();
+  // the run holding entry e: the last s with start[s] <= e (that run is not empty)
+  auto run_of = [&](uint32_t e) {
+    int lo = 0, hi = S;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (lds.start[mid] <= e) lo = mid;
+      else hi = mid;
+    }
+    return lo;
+  };
+  // entry e's segment and its slot in the concatenated sorted runs
+  auto locate = [&](uint32_t e, int& seg, uint32_t& slot) {
+    seg = run_of(e);
+    slot = lds.offset[seg] + lds.lo[seg] + (e - lds.start[seg]);
+  };
+  auto emit = [&](uint32_t r, uint32_t key, uint32_t e) {
+    int seg;
+    uint32_t slot;
+    locate(e, seg, slot);
+    const int64_t j = static_cast<int64_t>(base) + r;
+    out_values[j] = key_float(key);
+    out_segments[j] = seg;
+    out_positions[j] = position_starts[seg] + refined_local[slot];
+  };
+  auto key_of = [&](uint32_t e) {
+    int seg;
+    uint32_t slot;
+    locate(e, seg, slot);
+    return run_keys[slot];
+  };
+  if (size <= kBucketCap) {
+    uint64_t* pairs = lds.pairs;
+    if (size <= kBucketThreads) {
+      // one entry per thread, its outputs loaded with its key; rank among the bucket's
+      // (unique) composites
+      const uint32_t e = threadIdx.x, n2 = (size + 1) & ~1u;
+      uint64_t mine = ~0ull;
+      int seg = 0;
+      int64_t position = 0;
+      if (e < size) {
+        uint32_t slot;
+        locate(e, seg, slot);
+        mine = (static_cast<uint64_t>(run_keys[slot]) << 32) | e;
+        position = position_starts[seg] + refined_local[slot];
+      }
+      if (e < n2) pairs[e] = mine;
+      __syncthreads();
+      if (e < size) {
+        uint32_t rank = 0;
+#pragma unroll 8
+        for (uint32_t k = 0; k < n2; k += 2) {
+          const ulonglong2 c2 = *reinterpret_cast<const ulonglong2*>(pairs + k);
+          rank += c2.x < mine;
+          rank += c2.y < mine;
+        }
+        const int64_t j = static_cast<int64_t>(base) + rank;
+        out_values[j] = key_float(static_cast<uint32_t>(mine >> 32));
+        out_segments[j] = seg;
+        out_positions[j] = position;
+      }
+      return;
+    }
+    uint32_t n2 = 1;
+    while (n2 < size) n2 <<= 1;
+    for (uint32_t e = threadIdx.x; e < n2; e += kBucketThreads)
+      pairs[e] = e < size ? (static_cast<uint64_t>(key_of(e)) << 32) | e : ~0ull;
+    __syncthreads();
+    bitonic_sort_lds<kBucketThreads>(pairs, n2);
+    for (uint32_t r = threadIdx.x; r < size; r += kBucketThreads)
+      emit(r, static_cast<uint32_t>(pairs[r] >> 32), static_cast<uint32_t>(pairs[r]));
+    return;
+  }
+  uint32_t* keys = spill_keys + base;
+  uint32_t* entries = spill_entries + base;
+  for (uint32_t e = threadIdx.x; e < size; e += kBucketThreads) {
+    keys[e] = key_of(e);
+    entries[e] = e;
+  }
+  __threadfence_block();
+  __syncthreads();
+  // stable by key over entries in e order: (key, e) order
+  block_radix_sort<kBucketThreads>(keys, entries, spill_keys2 + base, spill_entries2 + base, size,
+                                   lds.radix);
+  for (uint32_t r = threadIdx.x; r < size; r += kBucketThreads) emit(r, keys[r], entries[r]);
+}
+
+// Global slot order for more than kOrderMaxRuns segments: the runs are concatenated in segment
+// (= index) order and each is sorted by (key, index), so a stable radix sort of the
+// concatenation by key alone gives the (key, index) order of torch.topk(largest=False,
+// sorted=True). It is rocPRIM's device radix sort (a plain library sort of `count` key/slot
+// pairs).
+size_t order_sort_bytes(int64_t segments, int64_t count) {
   size_t bytes = 0;
-  if (count > 0)
+  if (count > 0 && !order_shape(segments, count).bucketed)
     (void)rocprim::radix_sort_pairs(nullptr, bytes, static_cast<const uint32_t*>(nullptr),
                                     static_cast<uint32_t*>(nullptr),
                                     static_cast<const uint32_t*>(nullptr),
@@ -893,6 +1180,10 @@ struct SelectWorkspace {
   uint32_t* low_prefix;  // [segments][kLowRow]
   uint32_t* take_equal;
   uint32_t *run_keys, *run_slots, *refined_keys, *refined_local, *tmp_keys, *tmp_values;
+  OrderShape order;
+  uint64_t* splitters;   // [buckets - 1]
+  uint32_t* bucket_pos;  // [buckets - 1][segments]
+  uint32_t *spill_keys, *spill_entries;  // ping-pong of an oversized bucket's global sort
   void* sort_storage;  // rocPRIM's temporary storage for the global order
   size_t sort_bytes;
   size_t bytes;
@@ -920,7 +1211,13 @@ inline SelectWorkspace carve(void* base, int64_t total, int64_t segments, int64_
   w.refined_local = reinterpret_cast<uint32_t*>(take(count * 4));
   w.tmp_keys = reinterpret_cast<uint32_t*>(take(count * 4));
   w.tmp_values = reinterpret_cast<uint32_t*>(take(count * 4));
-  w.sort_bytes = order_sort_bytes(count);
+  w.order = order_shape(segments, count);
+  const size_t cuts = w.order.bucketed ? w.order.buckets - 1 : 0;
+  w.splitters = reinterpret_cast<uint64_t*>(take(cuts * 8));
+  w.bucket_pos = reinterpret_cast<uint32_t*>(take(cuts * segments * 4));
+  w.spill_keys = reinterpret_cast<uint32_t*>(take(w.order.bucketed ? count * 4 : 0));
+  w.spill_entries = reinterpret_cast<uint32_t*>(take(w.order.bucketed ? count * 4 : 0));
+  w.sort_bytes = order_sort_bytes(segments, count);
   w.sort_storage = take(w.sort_bytes);
   w.bytes = off;
   return w;
@@ -953,17 +1250,34 @@ int launch_sets(const float* raw, const float* pooled, int64_t total, const int6
   return check_launch("segment_pick");
 }
 
-int launch_runs(int64_t segments, const SelectWorkspace& w, const int64_t* quotas,
-                const int64_t* offsets, hipStream_t s) {
-  segment_sort_kernel<<<segments, kSortThreads, 0, s>>>(quotas, offsets, w.run_keys,
-                                                        w.run_slots, w.refined_keys,
-                                                        w.refined_local, w.tmp_keys, w.tmp_values);
-  return check_launch("segment_sort");
-}
-
-int launch_order(const int64_t* position_starts, int64_t segments, int64_t count,
-                 const SelectWorkspace& w, const int64_t* offsets, float* out_values,
-                 int64_t* out_segments, int64_t* out_positions, hipStream_t s) {
+// The queue order from the removal sets' pick lists (see the queue-order section above).
+int launch_queue(const int64_t* position_starts, int64_t segments, int64_t count,
+                 const SelectWorkspace& w, const int64_t* quotas, const int64_t* offsets,
+                 float* out_values, int64_t* out_segments, int64_t* out_positions,
+                 hipStream_t s) {
+  const OrderShape& o = w.order;
+  if (o.bucketed) {
+    if (o.buckets > 1) {
+      const unsigned groups = static_cast<unsigned>(ceil_div(o.samples, kSplitterSamples));
+      order_splitters_kernel<<<groups, kSortThreads, 0, s>>>(w.run_keys, o.samples, o.stride,
+                                                             o.buckets, w.splitters);
+      if (int rc = check_launch("order_splitters")) return rc;
+    }
+    segment_sort_kernel<<<segments, kSortThreads, 0, s>>>(
+        quotas, offsets, w.run_keys, w.run_slots, w.refined_keys, w.refined_local, w.tmp_keys,
+        w.tmp_values, w.splitters, o.buckets, w.bucket_pos, segments);
+    if (int rc = check_launch("segment_sort")) return rc;
+    order_bucket_kernel<<<o.buckets, kBucketThreads, 0, s>>>(
+        w.run_keys, quotas, offsets, w.bucket_pos, segments, o.buckets, position_starts,
+        w.refined_local, w.tmp_keys, w.tmp_values, w.spill_keys, w.spill_entries, out_values,
+        out_segments, out_positions);
+    return check_launch("order_bucket");
+  }
+  segment_sort_kernel<<<segments, kSortThreads, 0, s>>>(quotas, offsets, w.run_keys, w.run_slots,
+                                                        w.refined_keys, w.refined_local,
+                                                        w.tmp_keys, w.tmp_values, nullptr, 0u,
+                                                        nullptr, segments);
+  if (int rc = check_launch("segment_sort")) return rc;
   size_t sort_bytes = w.sort_bytes;
   const hipError_t sorted = rocprim::radix_sort_pairs(
       w.sort_storage, sort_bytes, static_cast<const uint32_t*>(w.run_keys), w.tmp_keys,
@@ -1054,10 +1368,8 @@ extern "C" int lr_select_refine_queue(const int64_t* position_starts, int64_t to
              "Expected contiguous CUDA tensor");
   const SelectWorkspace w = carve(workspace, total, segments, count);
   LR_REQUIRE(workspace_bytes >= w.bytes, "Workspace too small");
-  const hipStream_t s = as_stream(stream);
-  if (int rc = launch_runs(segments, w, quotas, offsets, s)) return rc;
-  return launch_order(position_starts, segments, count, w, offsets, out_values, out_segments,
-                      out_positions, s);
+  return launch_queue(position_starts, segments, count, w, quotas, offsets, out_values,
+                      out_segments, out_positions, as_stream(stream));
 }
 
 extern "C" int lr_select_refine(const float* raw, const float* pooled, int64_t total,

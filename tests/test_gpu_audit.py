@@ -221,6 +221,33 @@ def test_select_random_configurations(device, seed):
     compare(result, expect, ends)
 
 
+@pytest.mark.parametrize("crowd", ["lds_network", "global_sort"])
+def test_queue_order_crowded_bucket(device, crowd):
+    """The queue order cuts the picks into buckets at sampled splitters (every 8th pick here:
+    16,384 picks, 2,048 samples). Picks that share one value and sit only between sampled
+    positions all land in one bucket: 2,048 of them (sorted by the bucket's LDS network) or
+    14,336 (more than a bucket holds in LDS: sorted in global memory). Ties among them go by
+    index, across the segment boundary too. Identical to the oracle, every pick selected."""
+    rng = np.random.default_rng(31 if crowd == "lds_network" else 37)
+    lengths = [5000, 8192, 3192]
+    ends = np.cumsum(lengths)
+    total = int(ends[-1])
+    raw = rng.random(total).astype(np.float32) * 2.0
+    at = np.arange(total)
+    crowded = (at % 8 == 1) if crowd == "lds_network" else (at % 8 != 0)
+    raw[crowded] = 1.0
+    pooled = np.empty_like(raw)
+    start = 0
+    for end in ends:
+        pooled[start:end] = kv_ops.pool(raw[start:end], [0, end - start], 7)
+        start = end
+    starts = [0, 17, 40]
+    for count in (total, total - 3000):
+        result = run_select(device, raw, pooled, ends, starts, count)
+        expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+        compare(result, expect, ends)
+
+
 def test_select_all_equal_scores(device):
     lengths = [50, 60, 70]
     raw = np.full(180, 0.25, np.float32)
