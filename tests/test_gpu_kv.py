@@ -312,6 +312,42 @@ def test_batch_append_over_packed_views(device, dtype):
         lengths = new_lengths
 
 
+def test_batch_append_staging_ring_reuse(device):
+    """batch_append's descriptors go through a ring of 64 host-coherent buffers, one event per up
+    to 8 consecutive buffers of one stream. 150 calls while the device is held, switching
+    between two streams every 5 calls, so the host reuses buffers whose readers are still queued
+    and must wait for the right event. Every call has the same lengths (a stale descriptor would
+    only point at another call's inputs), and every output is bit-exact for its own inputs."""
+    heads, dim, calls = 2, 64, 150
+    lengths = [[5, 3], [0, 7]]
+    rows = [int(sum(l)) for l in lengths]
+    inputs = []
+    for i in range(calls):
+        keys = [rand((n, dim), torch.bfloat16, device, 1000 + 4 * i + r) for r, n in enumerate(rows)]
+        values = [rand((n, dim), torch.bfloat16, device, 2000 + 4 * i + r) for r, n in enumerate(rows)]
+        positions = [(torch.arange(n).float() + i).to(device)[:, None] for n in rows]
+        nk = rand((2, heads, 1, dim), torch.bfloat16, device, 3000 + i)
+        nv = rand((2, heads, 1, dim), torch.bfloat16, device, 4000 + i)
+        inputs.append((keys, values, positions, nk, nv, [100 + i, 200 + i]))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.current_stream(device), torch.cuda.Stream(device)]
+    for stream in streams:
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(5_000_000)
+    outputs = []
+    for i, (keys, values, positions, nk, nv, logical) in enumerate(inputs):
+        with torch.cuda.stream(streams[(i // 5) % 2]):
+            outputs.append(_C.batch_append(keys, values, positions, nk, nv, lengths, logical))
+    torch.cuda.synchronize()
+    for (keys, values, positions, nk, nv, logical), (pk, pv, pp) in zip(inputs, outputs):
+        ek, ev, ep = kv_ops.batch_append([bits(k) for k in keys], [bits(v) for v in values],
+                                         [p.cpu().numpy() for p in positions], bits(nk), bits(nv),
+                                         lengths, logical)
+        np.testing.assert_array_equal(bits(pk), ek)
+        np.testing.assert_array_equal(bits(pv), ev)
+        np.testing.assert_array_equal(pp.cpu().numpy(), ep)
+
+
 @pytest.mark.parametrize("width", [1, 3, 7, 9, 4099])
 def test_pool(device, width):
     rng = np.random.default_rng(width)
