@@ -313,18 +313,25 @@ inline void* dptr(const torch::Tensor& t) { return t.data_ptr(); }
 // behind the work that reads it, which for a ring this long has long completed. One event
 // covers up to kGroup consecutive buffers used on one stream (recorded behind the last of them):
 // an event per call put an extra barrier between every two dependent kernels (batch_append
-// 34.4 against 30.2 us per call on a held stream). The rings live until the process ends (their
-// pinned memory is released with it), so no buffer is freed while the runtime shuts down.
+// 34.4 against 30.2 us per call on a held stream). The buffers start as 64 KB shares of one
+// allocation made at the ring's first use (a pinned allocation costs 75-85 us of host time, and a
+// per-slot first allocation put one on the critical path of each of the first 64 calls); a
+// larger block gets a buffer of its own, grown to at least twice the old size. The rings live
+// until the process ends (their pinned memory is released with it), so no buffer is freed while
+// the runtime shuts down.
 struct StagingRing {
   static constexpr size_t kSlots = 64;
   static constexpr size_t kGroup = 8;
+  static constexpr size_t kSlotBytes = size_t{64} << 10;
   struct Slot {
     void* host = nullptr;
     size_t bytes = 0;
+    bool owned = false;    // a buffer of its own (else a share of `shared`)
     c10::Event done{c10::DeviceType::CUDA};
     bool pending = false;  // enqueued work may still read the buffer
     size_t cover = 0;      // the slot whose `done` event follows that work
   };
+  void* shared = nullptr;  // kSlots * kSlotBytes
   std::vector<Slot> slots{kSlots};
   size_t next = 0;
   // Pending slots that no recorded event follows yet, in ring order, all used on `open_stream`.
@@ -358,15 +365,25 @@ struct StagingRing {
     if (open.size() >= kGroup) cover();
   }
   void* fill(size_t i, const int64_t* words, int64_t count) {
+    if (shared == nullptr) {
+      check_call(library.staging_alloc(kSlots * kSlotBytes, &shared));
+      for (size_t j = 0; j < kSlots; ++j) {
+        slots[j].host = static_cast<char*>(shared) + j * kSlotBytes;
+        slots[j].bytes = kSlotBytes;
+      }
+    }
     Slot& slot = slots[i];
     settle(i);
     const size_t bytes = static_cast<size_t>(count) * sizeof(int64_t);
     if (slot.bytes < bytes) {
-      if (slot.host != nullptr) check_call(library.staging_free(slot.host));
+      const size_t grown = std::max(bytes, 2 * slot.bytes);
+      if (slot.owned) check_call(library.staging_free(slot.host));
       slot.host = nullptr;
       slot.bytes = 0;
-      check_call(library.staging_alloc(bytes, &slot.host));
-      slot.bytes = bytes;
+      slot.owned = false;
+      check_call(library.staging_alloc(grown, &slot.host));
+      slot.bytes = grown;
+      slot.owned = true;
     }
     std::memcpy(slot.host, words, bytes);
     return slot.host;

@@ -348,6 +348,28 @@ def test_batch_append_staging_ring_reuse(device):
         np.testing.assert_array_equal(pp.cpu().numpy(), ep)
 
 
+def test_batch_append_descriptors_beyond_a_staging_share(device):
+    """1,200 (request, head) descriptors (67 KB, more than a staging buffer's first 64 KB share)
+    in two consecutive calls: the buffers grow on their own, outputs bit-exact."""
+    heads, dim, requests = 8, 16, 150
+    rng = np.random.default_rng(12)
+    for call in range(2):
+        lengths = [list(rng.integers(0, 4, heads)) for _ in range(requests)]
+        keys = [rand((int(sum(l)), dim), torch.bfloat16, device, 500 + r) for r, l in enumerate(lengths)]
+        values = [rand((int(sum(l)), dim), torch.bfloat16, device, 700 + r) for r, l in enumerate(lengths)]
+        positions = [torch.arange(int(sum(l))).float().to(device)[:, None] for l in lengths]
+        nk = rand((requests, heads, 1, dim), torch.bfloat16, device, 900 + call)
+        nv = rand((requests, heads, 1, dim), torch.bfloat16, device, 901 + call)
+        logical = [50 + r for r in range(requests)]
+        pk, pv, pp = _C.batch_append(keys, values, positions, nk, nv, lengths, logical)
+        ek, ev, ep = kv_ops.batch_append([bits(k) for k in keys], [bits(v) for v in values],
+                                         [p.cpu().numpy() for p in positions], bits(nk), bits(nv),
+                                         lengths, logical)
+        np.testing.assert_array_equal(bits(pk), ek)
+        np.testing.assert_array_equal(bits(pv), ev)
+        np.testing.assert_array_equal(pp.cpu().numpy(), ep)
+
+
 @pytest.mark.parametrize("width", [1, 3, 7, 9, 4099])
 def test_pool(device, width):
     rng = np.random.default_rng(width)
