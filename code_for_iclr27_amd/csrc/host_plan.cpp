@@ -1182,9 +1182,10 @@ py::tuple reinsert_table(const std::vector<torch::Tensor>& keys,
 
 // The whole device-grouped reinsertion (insert_payload for every layer, identities in device
 // memory) from here, so that no Python runs between its launches: the table upload (with a
-// zeroed flag word after it), the grouping, the plan with the merged layers' metadata, the
-// flag's copy to host-coherent memory, then the resident rows, a wait for `payload_ready`
-// (a raw event handle, 0 for none) and the recalled rows, all on `stream`. Waits (without the
+// zeroed flag word after it), a wait for `metadata_ready` (the identities' copy: a raw event
+// handle, 0 for none), the grouping, the plan with the merged layers' metadata, the flag's copy
+// to host-coherent memory, then the resident rows, a wait for `payload_ready` (likewise) and the
+// recalled rows, all on `stream`. Waits (without the
 // GIL) for the plan only, then reads the flag and each slot's count. Returns (out keys, out
 // values, out positions, layout block i32, recalled rows i64 [count], new head lengths [L][H],
 // first row of each merged layer [L + 1], flag word).
@@ -1194,8 +1195,8 @@ py::tuple reinsert_device_launch(const std::vector<torch::Tensor>& keys,
                                  const std::vector<std::vector<int64_t>>& head_lens,
                                  const std::vector<int64_t>& packed_offsets,
                                  const torch::Tensor& payload, const torch::Tensor& metadata,
-                                 int64_t payload_ready, int64_t host_flag, int64_t host_counts,
-                                 int64_t stream_handle) {
+                                 int64_t metadata_ready, int64_t payload_ready, int64_t host_flag,
+                                 int64_t host_counts, int64_t stream_handle) {
   require(library.reinsert_group != nullptr && library.copy_words != nullptr,
           "library entry points are not bound");
   const ReinsertTable t = reinsert_table_words(keys, values, positions, head_lens, packed_offsets, 1);
@@ -1215,10 +1216,17 @@ py::tuple reinsert_device_launch(const std::vector<torch::Tensor>& keys,
   for (int64_t r : t.resident) resident_rows += r;
   const int64_t out_rows = resident_rows + count;
   const auto on_device = torch::TensorOptions().device(device);
-  // table and flag word in one upload; the flag starts at zero
+  // table and flag word in one upload; the flag starts at zero. The upload does not read the
+  // identities, so it goes ahead of the wait for their copy.
   torch::Tensor block = staging_ring(device).upload(t.words.data(),
                                                     static_cast<int64_t>(t.words.size()), device,
                                                     stream);
+  if (metadata_ready != 0) {
+    const hipError_t waited = hipStreamWaitEvent(
+        static_cast<hipStream_t>(stream),
+        reinterpret_cast<hipEvent_t>(static_cast<uintptr_t>(metadata_ready)), 0);
+    require(waited == hipSuccess, "hipStreamWaitEvent failed on the identities' copy event");
+  }
   int64_t* table = block.data_ptr<int64_t>();
   int32_t* flag = reinterpret_cast<int32_t*>(table + slots * LR_REINSERT_WORDS);
   // one int64 scratch block: the plan's workspace [3 * count], the grouped runs [2 * count],

@@ -256,14 +256,14 @@ class Reinserter:
                 meta_device.record_stream(current)
             if payload_ready is not None:
                 payload_device.record_stream(current)
-        if meta_ready is not None:
-            current.wait_event(meta_ready)
 
-        # the table upload, the grouping, the plan and both merges are enqueued by the host
-        # module (csrc/host_plan.cpp reinsert_device_launch), which waits for the plan only
+        # the table upload, the waits for the copies, the grouping, the plan and both merges are
+        # enqueued by the host module (csrc/host_plan.cpp reinsert_device_launch), which waits
+        # for the plan only
         (out_keys, out_values, out_positions, layout, recalled_rows, new_lens, offsets,
          word) = _reinsert_module().reinsert_device(
             *tensors, lengths, packed_offsets, payload_device, meta_device,
+            meta_ready.cuda_event if meta_ready is not None else 0,
             payload_ready.cuda_event if payload_ready is not None else 0,
             self._host_flag(device), self._host_counts(device, slots), current.cuda_stream)
         if word & _FLAG_IDENTITY:
