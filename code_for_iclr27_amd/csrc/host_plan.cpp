@@ -448,11 +448,11 @@ torch::Tensor new_layout(int64_t layers, int64_t heads, const torch::Device& dev
 }
 
 // The host side of an audit step's two copies and its one wait.
-//  - upload(): the metadata block goes through this object's pinned, host-coherent staging
-//    buffer and a copy kernel (lr_copy_words) on the step's stream, so the upload costs one small
-//    kernel between the previous work and the step's first kernel, not a copy-engine round trip
-//    (measured ~19 us of idle GPU between two steps). The staging buffer is rewritten only after
-//    the previous copy kernel has finished (`uploaded`).
+//  - upload(): the metadata block goes through the device's staging ring (pinned, host-coherent
+//    buffers, one event per group of buffers) and a copy kernel (lr_copy_words) on the step's
+//    stream, so the upload costs one small kernel between the previous work and the step's
+//    first kernel, not a copy-engine round trip (measured ~19 us of idle GPU between two
+//    steps), and no event of its own between that kernel and the next.
 //  - info_buffer() / post(): the per-segment quotas and the non-finite score count are final
 //    once the selection kernels are done; the selection's plan workgroup writes them straight
 //    into this object's host-coherent `info` buffer (no copy), and post() records `ready`
@@ -461,10 +461,6 @@ torch::Tensor new_layout(int64_t layers, int64_t heads, const torch::Device& dev
 // runs. One object serves one step at a time (an AuditStep keeps one per device); each step's
 // wait() must return before the next audit_launch with the same object.
 struct StepSync {
-  c10::Event uploaded{c10::DeviceType::CUDA};
-  bool upload_pending = false;
-  void* staging = nullptr;
-  size_t staging_bytes = 0;
   c10::Event ready{c10::DeviceType::CUDA};
   int64_t* info = nullptr;  // host-coherent int64 [segments + 1], written by the device
   size_t info_bytes = 0;
@@ -477,9 +473,7 @@ struct StepSync {
   StepSync(const StepSync&) = delete;
   StepSync& operator=(const StepSync&) = delete;
   ~StepSync() {
-    if (upload_pending) uploaded.synchronize();
     if (pending) ready.synchronize();
-    if (staging != nullptr) library.staging_free(staging);
     if (info != nullptr) library.staging_free(info);
   }
 
@@ -501,26 +495,7 @@ struct StepSync {
   }
 
   torch::Tensor upload(const torch::Tensor& words, const torch::Device& device, void* stream) {
-    const size_t bytes = static_cast<size_t>(words.numel()) * sizeof(int64_t);
-    if (upload_pending) {
-      uploaded.synchronize();  // normally long done: the previous step waited for its selection
-      upload_pending = false;
-    }
-    if (staging_bytes < bytes) {
-      if (staging != nullptr) check_call(library.staging_free(staging));
-      staging = nullptr;
-      staging_bytes = 0;
-      check_call(library.staging_alloc(bytes, &staging));
-      staging_bytes = bytes;
-    }
-    std::memcpy(staging, words.data_ptr<int64_t>(), bytes);
-    torch::Tensor block = torch::empty({words.numel()},
-                                       torch::TensorOptions().device(device).dtype(torch::kInt64));
-    check_call(library.copy_words(static_cast<const int64_t*>(staging), block.data_ptr<int64_t>(),
-                                  words.numel(), stream));
-    uploaded.record(c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getStream(device));
-    upload_pending = true;
-    return block;
+    return staging_ring(device).upload(words.data_ptr<int64_t>(), words.numel(), device, stream);
   }
 
   // Records `ready` and keeps what wait() needs: each head slot's segment (or -1) and length.
@@ -633,13 +608,13 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   void* stream = reinterpret_cast<void*>(static_cast<uintptr_t>(stream_handle));
   const auto on_device = torch::TensorOptions().device(device);
   const int64_t S = plan.segments;
-  torch::Tensor block = sync != nullptr ? sync->upload(plan.block, device, stream)
-                                        : plan.block.to(device, /*non_blocking=*/true);
-  const int64_t* words = block.data_ptr<int64_t>();
   count = std::min(std::max<int64_t>(count, 0), plan.total);
   // controller.py:151-153: the selection must cover the slots the budget removes now
   require(immediate <= count, "Not enough unprotected candidates to enforce the budget");
 
+  // The step's first buffers are allocated before the upload, so that its copy kernel and the
+  // first scorer kernel are launched back to back (the copy takes less time than the host
+  // between the two launches otherwise).
   // quotas (written for every segment by the selection) and the non-finite count (cleared by
   // the first scorer kernel) come back in one small copy
   torch::Tensor info = count > 0 ? torch::empty({S + 1}, on_device.dtype(torch::kInt64))
@@ -652,6 +627,9 @@ py::tuple audit_launch(const std::vector<torch::Tensor>& keys,
   torch::Tensor scores = torch::empty({2 * plan.total}, on_device.dtype(torch::kFloat32));
   float* raw = scores.data_ptr<float>();
   float* pooled = raw + plan.total;
+  torch::Tensor block = sync != nullptr ? sync->upload(plan.block, device, stream)
+                                        : plan.block.to(device, /*non_blocking=*/true);
+  const int64_t* words = block.data_ptr<int64_t>();
   const bool timed = !mark.is_none();
   auto stage = [&](const char* name) {
     if (timed) mark(name);
