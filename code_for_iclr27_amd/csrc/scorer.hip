@@ -9,7 +9,8 @@
 //   score[t]  = f32(max(risk64(min_w drop), risk64(max_w drop)))     (f64 Bernoulli risk)
 // The reference materialises z and p for every (query, group, key) in HBM. Here neither ever
 // leaves the chip:
-//   1. projected_values_kernel: pv for every key of every segment (VALU, reads V once).
+//   1. projected_values_kernel: pv for every key of every segment (VALU, reads V once), and
+//      once the margin's terms of the risk (sigmoid and softplus of the margin, f64).
 //   2. row_stats_kernel: for each (g, w) row, an online pass over all keys: Q.K^T on MFMA
 //      (v_mfma_f32_32x32x16_bf16), the bf16 double rounding, running max / sum / pv-sum.
 //      Writes 16 bytes of statistics per row.
@@ -146,6 +147,16 @@ __device__ __forceinline__ f32x16 mfma_tile_zero() {
 
 __device__ __forceinline__ double softplus64(double v) { return v > 20.0 ? v : log1p(exp(v)); }
 
+// The margin's terms of the risk, the same for every candidate: p = sigmoid(m) and
+// softplus(m). The first scorer kernel computes them once into the workspace.
+struct RiskTerms {
+  double probability, base_softplus;
+};
+__device__ __forceinline__ RiskTerms risk_terms(float margin) {
+  const double m = static_cast<double>(margin);
+  return RiskTerms{1.0 / (1.0 + exp(-m)), softplus64(m)};
+}
+
 __device__ __forceinline__ double risk64(double margin, double probability, double base_softplus,
                                          float drop) {
   const double compared = margin - static_cast<double>(drop);
@@ -199,7 +210,9 @@ template <int D>
 __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __restrict__ table,
                                                                int64_t groups64,
                                                                float* __restrict__ pv,
-                                                               int* __restrict__ nonfinite) {
+                                                               int* __restrict__ nonfinite,
+                                                               const float* __restrict__ margin,
+                                                               RiskTerms* __restrict__ terms) {
   constexpr int LPR = D / 8;          // lanes per row (a power of two, 8..32)
   constexpr int LOG_LPR = LPR == 8 ? 3 : LPR == 16 ? 4 : 5;
   static_assert(LPR == (1 << LOG_LPR), "D must be 64, 128 or 256");
@@ -212,7 +225,10 @@ __global__ __launch_bounds__(256) void projected_values_kernel(const int64_t* __
   __shared__ float grad[kMaxGroups * D];
   const Segment seg = load_segment(table, blockIdx.y);
   const int groups = static_cast<int>(groups64);
-  if (nonfinite != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *nonfinite = 0;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    if (nonfinite != nullptr) *nonfinite = 0;
+    *terms = risk_terms(margin[0]);
+  }
   for (int i = threadIdx.x; i < groups * D; i += 256) grad[i] = seg.gradient[i];
   const int lane = threadIdx.x % LPR;
   const int length = static_cast<int>(seg.length);
@@ -622,7 +638,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
     const int64_t* __restrict__ table, int64_t groups64, int64_t window64, int64_t query_stride,
     const int64_t* __restrict__ query_positions, const float* __restrict__ margin, float scale,
     int64_t tiles_per_segment, const float* __restrict__ pv, const float4* __restrict__ stats,
-    float* __restrict__ scores, int* __restrict__ nonfinite) {
+    const RiskTerms* __restrict__ terms, float* __restrict__ scores, int* __restrict__ nonfinite) {
   constexpr int KS = D / 16;
   constexpr int KT = column_key_tiles<D>();
   const float lg = log2e_per_input<P2>(scale);  // logit input -> exp2 argument
@@ -955,8 +971,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(column_wave
   __syncthreads();
   const bool any_row_bad = rowbad_lds != 0;
   const double m = static_cast<double>(margin[0]);
-  const double p = 1.0 / (1.0 + exp(-m));
-  const double base = softplus64(m);
+  const double p = terms->probability, base = terms->base_softplus;
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
     // Combine the two reducer lanes of each key, then part 0 takes the risk of the minimum and
@@ -1021,8 +1036,8 @@ template <int D>
 int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t window,
                  int64_t max_length, int64_t max_candidates, int64_t query_stride,
                  const int64_t* query_positions, const float* margin, float scale, float eps,
-                 float4* stats, float* pv, float* scores, int* nonfinite, int stages,
-                 bool general_scale, hipStream_t stream) {
+                 float4* stats, float* pv, RiskTerms* terms, float* scores, int* nonfinite,
+                 int stages, bool general_scale, hipStream_t stream) {
   int scale_exponent = 0;
   const bool p2 = !general_scale && scale > 0.0f && std::isfinite(scale) &&
                   std::frexp(scale, &scale_exponent) == 0.5f && scale_exponent > -60;
@@ -1032,7 +1047,8 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
     constexpr int rows_per_block = 256 / (D / 8);
     const int64_t steps = ceil_div(max_length, kProjectedRowsPerLane * rows_per_block);
     dim3 pv_grid(static_cast<unsigned>(ceil_div(steps, int64_t{6})), static_cast<unsigned>(segments));
-    projected_values_kernel<D><<<pv_grid, 256, 0, stream>>>(table, groups, pv, nonfinite);
+    projected_values_kernel<D><<<pv_grid, 256, 0, stream>>>(table, groups, pv, nonfinite, margin,
+                                                            terms);
     if (int rc = check_launch("projected_values")) return rc;
   }
   if (stages & 2) {
@@ -1053,11 +1069,11 @@ int launch_score(const int64_t* table, int64_t segments, int64_t groups, int64_t
     if (p2)
       column_scores_kernel<D, true><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
           table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
-          scores, nonfinite);
+          terms, scores, nonfinite);
     else
       column_scores_kernel<D, false><<<static_cast<unsigned>(segments * tiles), 256, 0, stream>>>(
           table, groups, window, query_stride, query_positions, margin, scale, tiles, pv, stats,
-          scores, nonfinite);
+          terms, scores, nonfinite);
     if (int rc = check_launch("column_scores")) return rc;
   }
   return LR_OK;
@@ -1072,7 +1088,8 @@ extern "C" size_t lr_score_workspace_bytes(int64_t segments, int64_t groups, int
                                            int64_t projected_floats) {
   if (segments < 0 || groups < 0 || window < 0 || projected_floats < 0) return 0;
   return align256(static_cast<size_t>(segments * groups * window) * sizeof(float4)) +
-         align256(static_cast<size_t>(projected_floats) * sizeof(float));
+         align256(static_cast<size_t>(projected_floats) * sizeof(float)) +
+         align256(sizeof(RiskTerms));
 }
 
 extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments, int64_t groups,
@@ -1103,6 +1120,8 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
   LR_REQUIRE(workspace_bytes >= need, "Workspace too small");
   float4* stats = static_cast<float4*>(workspace);
   float* pv = reinterpret_cast<float*>(static_cast<char*>(workspace) + stats_bytes);
+  RiskTerms* terms = reinterpret_cast<RiskTerms*>(
+      static_cast<char*>(workspace) + need - align256(sizeof(RiskTerms)));
   const hipStream_t s = as_stream(stream);
   const float eps = static_cast<float>(epsilon);
   const bool general_scale = (stages & 8) != 0;
@@ -1111,15 +1130,15 @@ extern "C" int lr_score_segments(const int64_t* segment_table, int64_t segments,
     case 64:
       return launch_score<64>(segment_table, segments, groups, window, max_length, max_candidates,
                               query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                              scores, nonfinite, run, general_scale, s);
+                              terms, scores, nonfinite, run, general_scale, s);
     case 128:
       return launch_score<128>(segment_table, segments, groups, window, max_length, max_candidates,
                                query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                               scores, nonfinite, run, general_scale, s);
+                               terms, scores, nonfinite, run, general_scale, s);
     default:
       return launch_score<256>(segment_table, segments, groups, window, max_length, max_candidates,
                                query_group_stride, query_positions, margin, scale, eps, stats, pv,
-                               scores, nonfinite, run, general_scale, s);
+                               terms, scores, nonfinite, run, general_scale, s);
   }
 }
 
