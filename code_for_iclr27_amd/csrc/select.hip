@@ -620,6 +620,14 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
     lo = min(m, threadIdx.x * per);
     hi = min(m, lo + per);
   };
+  // The run's keys (at most kRunMax) into registers with every LDS read issued at once, read
+  // once for both passes over the run (a loop of dependent-latency reads otherwise).
+  constexpr uint32_t kRunMax = kPickStaged / kPickThreads;
+  static_assert(kPickStaged % kPickThreads == 0, "whole runs per chunk");
+  auto load_run = [](const uint32_t* keys, uint32_t lo, uint32_t m, uint32_t (&out)[kRunMax]) {
+#pragma unroll
+    for (uint32_t k = 0; k < kRunMax; ++k) out[k] = keys[min(lo + k, m - 1)];
+  };
 
   // raw picks in index order
   const uint32_t threshold = states[3].prefix, take = take_equal[s];
@@ -634,22 +642,29 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
       }
       uint32_t lo, hi;
       run_of(m, lo, hi);
+      uint32_t rk[kRunMax];
+      load_run(raw_keys, lo, m, rk);
       uint32_t lt = 0, eq = 0;
-      for (uint32_t i = lo; i < hi; ++i) {
-        const uint32_t key = raw_keys[i];
-        lt += key < threshold;
-        eq += key == threshold;
+#pragma unroll
+      for (uint32_t k = 0; k < kRunMax; ++k) {
+        if (lo + k < hi) {
+          lt += rk[k] < threshold;
+          eq += rk[k] == threshold;
+        }
       }
       uint32_t lt_before, eq_before, lt_total, eq_total;
       block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
       const uint32_t take_left = take > carry_equal ? take - carry_equal : 0u;
       uint32_t rank = carry_rank + lt_before + min(take_left, eq_before);
       uint32_t seen = eq_before;
-      for (uint32_t i = lo; i < hi; ++i) {
-        const uint32_t key = raw_keys[i];
-        bool picked = key < threshold;
-        if (key == threshold) picked = seen++ < take_left;
-        if (picked) run_keys[offset + rank++] = key;
+#pragma unroll
+      for (uint32_t k = 0; k < kRunMax; ++k) {
+        if (lo + k < hi) {
+          const uint32_t key = rk[k];
+          bool picked = key < threshold;
+          if (key == threshold) picked = seen++ < take_left;
+          if (picked) run_keys[offset + rank++] = key;
+        }
       }
       carry_rank += lt_total + min(take_left, eq_total);
       carry_equal += eq_total;
@@ -677,12 +692,17 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
       }
       uint32_t lo, hi;
       run_of(m, lo, hi);
+      uint32_t rk[kRunMax], pk[kRunMax];
+      load_run(raw_keys, lo, m, rk);
+      load_run(pooled_keys, lo, m, pk);
       uint32_t lt = 0, eq = 0, raw_eq = 0;
-      for (uint32_t i = lo; i < hi; ++i) {
-        const uint32_t key = pooled_keys[i];
-        lt += key < pthreshold;
-        eq += key == pthreshold;
-        raw_eq += raw_keys[i] == threshold;
+#pragma unroll
+      for (uint32_t k = 0; k < kRunMax; ++k) {
+        if (lo + k < hi) {
+          lt += pk[k] < pthreshold;
+          eq += pk[k] == pthreshold;
+          raw_eq += rk[k] == threshold;
+        }
       }
       uint32_t lt_before, eq_before, lt_total, eq_total;
       block_scan_pair<kPickThreads>(lt, eq, wave_sums, lt_before, eq_before, lt_total, eq_total);
@@ -693,12 +713,15 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
       const uint32_t raw_take_left = take > carry_raw_equal ? take - carry_raw_equal : 0u;
       uint32_t rank = carry_rank + lt_before + min(take_left, eq_before);
       uint32_t seen = eq_before, raw_seen = raw_eq_before;
-      for (uint32_t i = lo; i < hi; ++i) {
+#pragma unroll
+      for (uint32_t k = 0; k < kRunMax; ++k) {
+        if (lo + k >= hi) continue;
+        const uint32_t i = lo + k;
         // the raw rule again, in index order, tells whether slot i was a raw pick
-        const uint32_t rkey = raw_keys[i];
+        const uint32_t rkey = rk[k];
         bool raw_picked = rkey < threshold;
         if (rkey == threshold) raw_picked = raw_seen++ < raw_take_left;
-        const uint32_t key = pooled_keys[i];
+        const uint32_t key = pk[k];
         bool picked = key < pthreshold;
         if (key == pthreshold) picked = seen++ < take_left;
         if (picked) {
