@@ -748,8 +748,8 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
 // order is then the j-th smallest raw pick over all segments, by (key, index), and takes the
 // pooled pick of its segment at its rank within that segment.
 //
-// Up to kOrderMaxRuns segments, the global order is a bucketed merge of the sorted runs (three
-// launches):
+// Up to kOrderMaxRuns segments and kOrderMaxCount picks (buckets of 512 picks on average), the
+// global order is a bucketed merge of the sorted runs (three launches):
 //   1. order_splitters_kernel: `samples` raw picks at a fixed stride of the concatenated
 //      index-order lists, as (key << 32 | list position) composites. Composites are unique and
 //      their order is the final (key, index) order. Each workgroup counts the rank of
@@ -763,8 +763,8 @@ __global__ __launch_bounds__(kPickThreads) void segment_pick_kernel(
 //      contiguous range of every segment's sorted run), sorts them in LDS, and writes each one
 //      at (picks below the bucket) + (rank within it), with its segment and transplanted
 //      position. A bucket larger than LDS holds is sorted in global memory instead.
-// More segments than that: the runs are sorted the same way and rocPRIM's device radix sort
-// orders the concatenation, then emit_kernel writes the slots.
+// More segments or picks than that: the runs are sorted the same way and rocPRIM's device radix
+// sort orders the concatenation, then emit_kernel writes the slots.
 //
 // Per-segment sorts, by list length n:
 //   n <= kRankSortMax: both lists at once, one half of the workgroup each; each entry's rank
@@ -782,6 +782,7 @@ constexpr int64_t kOrderMaxRuns = 1024;  // segments the bucketed order takes (L
 constexpr uint32_t kOrderSamples = 2048;
 constexpr int64_t kOrderBucketTarget = 128;  // mean picks per bucket
 constexpr uint32_t kOrderMaxBuckets = 1024;
+constexpr int64_t kOrderMaxCount = int64_t{kOrderMaxBuckets} * 512;
 constexpr int kBucketThreads = 512;
 constexpr uint32_t kBucketCap = 4096;  // bucket entries sorted in LDS
 
@@ -794,7 +795,7 @@ struct OrderShape {
 // - 1) are distinct and increasing.
 inline OrderShape order_shape(int64_t segments, int64_t count) {
   OrderShape o{};
-  o.bucketed = segments <= kOrderMaxRuns && count > 0;
+  o.bucketed = segments <= kOrderMaxRuns && count > 0 && count <= kOrderMaxCount;
   if (!o.bucketed) return o;
   o.samples = static_cast<uint32_t>(count < kOrderSamples ? count : kOrderSamples);
   o.stride = static_cast<uint32_t>(count / o.samples);

@@ -248,6 +248,19 @@ def test_queue_order_crowded_bucket(device, crowd):
         compare(result, expect, ends)
 
 
+def test_select_large_count_radix_path(device):
+    """More than 524,288 picks over few segments: the queue order takes the device radix sort
+    of the concatenated runs instead of the bucketed merge; identical to the oracle."""
+    rng = np.random.default_rng(41)
+    lengths = [250_000, 180_000, 5, 220_000]
+    raw, pooled, ends = tables(rng, lengths, ties=True)
+    starts = [0, 3, 9, 27]
+    count = 600_000
+    result = run_select(device, raw, pooled, ends, starts, count)
+    expect = oselection.refine_arrays(raw, pooled, ends, starts, count, tie="canonical")
+    compare(result, expect, ends)
+
+
 def test_select_all_equal_scores(device):
     lengths = [50, 60, 70]
     raw = np.full(180, 0.25, np.float32)
