@@ -96,7 +96,8 @@ def _native():
         library = _lib.load()
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_data_movement(address("lr_append"), address("lr_compact"),
-                                   address("lr_append_layers"), address("lr_batch_append"))
+                                   address("lr_append_layers"), address("lr_batch_append"),
+                                   address("lr_batch_append_host"))
         _native_module = planner
     return _native_module
 
@@ -231,8 +232,9 @@ def batch_append(keys: List[torch.Tensor], values: List[torch.Tensor],
     _native_planner()  # binds the staging entry points
     with torch.cuda.device(new_keys.device):
         # csrc/host_plan.cpp: the reference's descriptor loop (csrc/batch_append.cu:49-80) and
-        # its checks, the descriptors in host-coherent staging that the kernel reads in place
-        # (the reference's copy, csrc/batch_append.cu:81, blocks the host), allocation, launch
+        # its checks, the descriptors in the launch's kernel arguments (up to 64 segments) or
+        # in host-coherent staging that the kernel reads in place (the reference's copy,
+        # csrc/batch_append.cu:81, blocks the host), allocation, launch
         return list(_native().batch_append(keys, values, positions, new_keys, new_values,
                                            lengths, logical_positions,
                                            _lib.stream_of(new_keys)))

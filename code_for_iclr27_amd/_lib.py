@@ -46,6 +46,7 @@ SIGNATURES = {
     "lr_merge": [_P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I, _P, _P, _P, _P],
     "lr_pack": [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _I64, _P, _P, _P],
     "lr_batch_append": [_P, _I64, _P, _P, _I64, _I, _I64, _P, _P, _P, _P],
+    "lr_batch_append_host": [_P, _I64, _P, _P, _I64, _I, _I64, _P, _P, _P, _P],
     "lr_pack_layers": [_P, _I64, _P, _I64, _I64, _P, _P, _P],
     "lr_pack_heads": [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P],
     "lr_group_mean_queries": [_P, _I64, _I64, _I64, _I64, _I, _P, _P],

@@ -235,6 +235,7 @@ struct Library {
   decltype(&lr_compact) compact = nullptr;
   decltype(&lr_append_layers) append_layers = nullptr;
   decltype(&lr_batch_append) batch_append = nullptr;
+  decltype(&lr_batch_append_host) batch_append_host = nullptr;
   decltype(&lr_packed_attention) packed_attention = nullptr;
   decltype(&lr_packed_attention_workspace_bytes) attention_workspace_bytes = nullptr;
   decltype(&lr_packed_attention_pending) packed_attention_pending = nullptr;
@@ -277,11 +278,12 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
 }
 
 void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers,
-                        int64_t batch_append) {
+                        int64_t batch_append, int64_t batch_append_host) {
   bind_one(library.append, append);
   bind_one(library.compact, compact);
   bind_one(library.append_layers, append_layers);
   bind_one(library.batch_append, batch_append);
+  bind_one(library.batch_append_host, batch_append_host);
 }
 
 void bind_reinsert(int64_t group, int64_t plan_layout, int64_t resident, int64_t recalled) {
@@ -1528,16 +1530,20 @@ py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
   return py::make_tuple(out_keys, out_values, out_positions, out_cumulative, out_lengths, firsts);
 }
 
+// The most batch_append segments whose descriptors lr_batch_append_host takes in the launch.
+constexpr int64_t kInlineDescriptorSegments = 64;
+
 // The batch_append descriptors of csrc/batch_append.cu:49-80, one 7-word row per (request,
 // head): [keys ptr, values ptr, positions ptr, first source row, old length, destination row,
 // logical position]; same checks, order and messages as the reference's host loop. Returns
 // (descriptors int64 [R*H, 7] already copied to `device` on the current stream (from pinned
 // memory, without blocking the host), total output rows, rows of the longest head + 1).
 // _C.batch_append (csrc/batch_append.cu:36-94): the reference's descriptor loop and checks
-// (batch_append.cu:49-80), the output allocation and the launch, all here. The descriptors are
-// written into a pinned, host-coherent staging buffer that the kernel reads in place, so the
-// launch needs neither a copy (the reference's copy, batch_append.cu:81, blocks the host) nor a
-// copy kernel. Returns [keys, values, positions [rows, 1]] packed.
+// (batch_append.cu:49-80), the output allocation and the launch, all here. Up to 64 (request,
+// head) descriptors travel in the launch's kernel arguments; larger tables are written into a
+// pinned, host-coherent staging buffer that the kernel reads in place. Either way the launch
+// needs neither a copy (the reference's copy, batch_append.cu:81, blocks the host) nor a copy
+// kernel. Returns [keys, values, positions [rows, 1]] packed.
 std::vector<torch::Tensor> batch_append_launch(const std::vector<torch::Tensor>& keys,
                                                const std::vector<torch::Tensor>& values,
                                                const std::vector<torch::Tensor>& positions,
@@ -1599,11 +1605,19 @@ std::vector<torch::Tensor> batch_append_launch(const std::vector<torch::Tensor>&
   torch::Tensor out_keys = torch::empty({destination, dim}, options.dtype(dtype));
   torch::Tensor out_values = torch::empty({destination, dim}, options.dtype(dtype));
   torch::Tensor out_positions = torch::empty({destination, 1}, options.dtype(torch::kFloat32));
+  const int64_t segments = static_cast<int64_t>(requests) * heads;
+  const int elem_bytes = static_cast<int>(c10::elementSize(dtype));
+  if (segments <= kInlineDescriptorSegments) {
+    check_call(library.batch_append_host(host.data(), segments, new_keys.data_ptr(),
+                                         new_values.data_ptr(), dim, elem_bytes, maximum,
+                                         out_keys.data_ptr(), out_values.data_ptr(),
+                                         out_positions.data_ptr<float>(), stream));
+    return {out_keys, out_values, out_positions};
+  }
   StagingRing& ring = staging_ring(device);
   const int64_t* descriptors = ring.stage(host.data(), static_cast<int64_t>(host.size()));
-  check_call(library.batch_append(descriptors, static_cast<int64_t>(requests) * heads,
-                                  new_keys.data_ptr(), new_values.data_ptr(), dim,
-                                  static_cast<int>(c10::elementSize(dtype)), maximum,
+  check_call(library.batch_append(descriptors, segments, new_keys.data_ptr(),
+                                  new_values.data_ptr(), dim, elem_bytes, maximum,
                                   out_keys.data_ptr(), out_values.data_ptr(),
                                   out_positions.data_ptr<float>(), stream));
   ring.release(device);

@@ -7,6 +7,8 @@
 //   - each lane group walks R consecutive output rows, so per-row index work (a binary search
 //     in compaction, a descriptor read in batch append) is amortised or incremental;
 //   - every index read from device memory is bounds-checked before it is dereferenced.
+#include <cstring>
+
 #include "lr_common.hpp"
 
 namespace lr {
@@ -420,16 +422,21 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
 // ---------------------------------------------------------------------------------------
 // batch_append (csrc/batch_append.cu:8-34): blockIdx.y = (request, head) segment with the
 // reference's 7-word descriptor; the segment's old rows then its one new row are written
-// contiguously from the destination row.
+// contiguously from the destination row. The descriptor comes either from memory (a device or
+// host-coherent array) or from the launch's kernel arguments (batches of up to
+// kInlineSegments segments, read with scalar loads from the kernel-argument segment).
+constexpr int kInlineSegments = 64;
+struct InlineDescriptors {
+  int64_t words[kInlineSegments * 7];
+};
+
 template <int G>
-__global__ __launch_bounds__(kThreads) void batch_append_kernel(
-    const int64_t* __restrict__ descriptors, const uint8_t* __restrict__ new_keys,
-    const uint8_t* __restrict__ new_values, int64_t max_rows, RowLayout layout,
+__device__ __forceinline__ void batch_append_segment(
+    const int64_t (&d)[7], int64_t segment, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, const RowLayout& layout,
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
   const GroupCoord gc = group_coord(layout.lanes_log2);
-  const int64_t segment = blockIdx.y;
-  const int64_t* d = descriptors + segment * 7;
   const uint8_t* keys = reinterpret_cast<const uint8_t*>(d[0]);
   const uint8_t* values = reinterpret_cast<const uint8_t*>(d[1]);
   const float* positions = reinterpret_cast<const float*>(d[2]);
@@ -473,6 +480,34 @@ __global__ __launch_bounds__(kThreads) void batch_append_kernel(
       }
     }
   }
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void batch_append_kernel(
+    const int64_t* __restrict__ descriptors, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions) {
+  const int64_t segment = blockIdx.y;
+  int64_t d[7];
+#pragma unroll
+  for (int i = 0; i < 7; ++i) d[i] = descriptors[segment * 7 + i];
+  batch_append_segment<G>(d, segment, new_keys, new_values, max_rows, layout, out_keys,
+                          out_values, out_positions);
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void batch_append_inline_kernel(
+    const InlineDescriptors descriptors, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, RowLayout layout,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions) {
+  const int64_t segment = blockIdx.y;
+  int64_t d[7];
+#pragma unroll
+  for (int i = 0; i < 7; ++i) d[i] = descriptors.words[segment * 7 + i];
+  batch_append_segment<G>(d, segment, new_keys, new_values, max_rows, layout, out_keys,
+                          out_values, out_positions);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1005,15 +1040,18 @@ extern "C" int lr_pack(const void* keys, const void* values, const float* positi
   });
 }
 
-extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
-                               const void* new_keys, const void* new_values, int64_t dim,
-                               int elem_bytes, int64_t max_rows, void* out_keys,
-                               void* out_values, float* out_positions, void* stream) {
-  clear_error();
+namespace {
+
+// The checks and launch shape shared by both batch_append entry points; `launch` gets the
+// granule, the row layout and the grid.
+template <typename Launch>
+int batch_append_launch(int64_t segments, const void* new_keys, const void* new_values,
+                        int64_t dim, int elem_bytes, int64_t max_rows, void* out_keys,
+                        void* out_values, float* out_positions, Launch&& launch) {
   LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Only batched one-token append is supported");
   LR_REQUIRE(segments > 0 && segments <= 65535, "Request metadata mismatch");
   LR_REQUIRE(max_rows >= 1, "Invalid head length");
-  LR_REQUIRE(descriptors && new_keys && new_values && out_keys && out_values && out_positions,
+  LR_REQUIRE(new_keys && new_values && out_keys && out_values && out_positions,
              "Contiguous CUDA states required");
   const int64_t row_bytes = dim * elem_bytes;
   // Descriptor pointers are required to share the alignment of the row size (a whole
@@ -1023,13 +1061,46 @@ extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
   const RowLayout layout = make_layout(row_bytes, g, max_rows * segments, 8);
   int64_t bx = ceil_div(ceil_div(max_rows, layout.rows_per_group), kThreads >> layout.lanes_log2);
   if (bx < 1) bx = 1;
-  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(segments));
-  return dispatch_granule(g, [&]<int G>() {
-    batch_append_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
-        descriptors, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
-        bytes(out_values), out_positions);
-    return check_launch("batch_append");
-  });
+  const dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(segments));
+  return dispatch_granule(g, [&]<int G>() { return launch.template operator()<G>(layout, grid); });
+}
+
+}  // namespace
+
+extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
+                               const void* new_keys, const void* new_values, int64_t dim,
+                               int elem_bytes, int64_t max_rows, void* out_keys,
+                               void* out_values, float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(descriptors != nullptr, "Contiguous CUDA states required");
+  return batch_append_launch(
+      segments, new_keys, new_values, dim, elem_bytes, max_rows, out_keys, out_values,
+      out_positions, [&]<int G>(const RowLayout& layout, dim3 grid) {
+        batch_append_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+            descriptors, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
+            bytes(out_values), out_positions);
+        return check_launch("batch_append");
+      });
+}
+
+extern "C" int lr_batch_append_host(const int64_t* host_descriptors, int64_t segments,
+                                    const void* new_keys, const void* new_values, int64_t dim,
+                                    int elem_bytes, int64_t max_rows, void* out_keys,
+                                    void* out_values, float* out_positions, void* stream) {
+  clear_error();
+  LR_REQUIRE(host_descriptors != nullptr, "Request metadata mismatch");
+  LR_REQUIRE(segments <= kInlineSegments, "Too many segments for descriptors in the launch");
+  InlineDescriptors words{};
+  if (segments > 0)
+    std::memcpy(words.words, host_descriptors, static_cast<size_t>(segments) * 7 * sizeof(int64_t));
+  return batch_append_launch(
+      segments, new_keys, new_values, dim, elem_bytes, max_rows, out_keys, out_values,
+      out_positions, [&]<int G>(const RowLayout& layout, dim3 grid) {
+        batch_append_inline_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+            words, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
+            bytes(out_values), out_positions);
+        return check_launch("batch_append");
+      });
 }
 
 extern "C" int lr_compact_heads_layout(const int64_t* head_table, int64_t heads,

@@ -122,6 +122,16 @@ int lr_batch_append(const int64_t* descriptors, int64_t segments, const void* ne
                     const void* new_values, int64_t dim, int elem_bytes, int64_t max_rows,
                     void* out_keys, void* out_values, float* out_positions, void* stream);
 
+/* batch_append with the descriptors in HOST memory (the reference's host-built table before
+ * its copy to the device, csrc/batch_append.cu:49-81): the table is read during the call and
+ * travels in the launch's kernel arguments, so the call needs no device copy of it and the
+ * caller may reuse the table as soon as the call returns. At most 64 segments (the kernel
+ * argument space); the other arguments and the result are those of lr_batch_append. */
+int lr_batch_append_host(const int64_t* host_descriptors, int64_t segments,
+                         const void* new_keys, const void* new_values, int64_t dim,
+                         int elem_bytes, int64_t max_rows, void* out_keys, void* out_values,
+                         float* out_positions, void* stream);
+
 /* All-layer pack of one eviction batch: the per-layer _C.pack calls of record_evicted
  * (src/lazy_recall/recall/transport.py:150-167, csrc/recall.cu:30-47) in one launch.
  * layer_table: DEVICE [layers, 4] i64 = (keys ptr, values ptr, positions ptr (f32), rows) per

@@ -313,22 +313,23 @@ def test_batch_append_over_packed_views(device, dtype):
 
 
 def test_batch_append_staging_ring_reuse(device):
-    """batch_append's descriptors go through a ring of 64 host-coherent buffers, one event per up
-    to 8 consecutive buffers of one stream. 150 calls while the device is held, switching
-    between two streams every 5 calls, so the host reuses buffers whose readers are still queued
-    and must wait for the right event. Every call has the same lengths (a stale descriptor would
-    only point at another call's inputs), and every output is bit-exact for its own inputs."""
-    heads, dim, calls = 2, 64, 150
-    lengths = [[5, 3], [0, 7]]
+    """Tables of more than 64 (request, head) descriptors go through a ring of 64 host-coherent
+    buffers, one event per up to 8 consecutive buffers of one stream. 150 calls of 72 segments
+    while the device is held, switching between two streams every 5 calls, so the host reuses
+    buffers whose readers are still queued and must wait for the right event. Every call has the
+    same lengths (a stale descriptor would only point at another call's inputs), and every
+    output is bit-exact for its own inputs."""
+    heads, dim, calls, requests = 8, 16, 150, 9
+    lengths = [[(3 * r + h) % 6 for h in range(heads)] for r in range(requests)]
     rows = [int(sum(l)) for l in lengths]
     inputs = []
     for i in range(calls):
-        keys = [rand((n, dim), torch.bfloat16, device, 1000 + 4 * i + r) for r, n in enumerate(rows)]
-        values = [rand((n, dim), torch.bfloat16, device, 2000 + 4 * i + r) for r, n in enumerate(rows)]
+        keys = [rand((n, dim), torch.bfloat16, device, 100000 + 16 * i + r) for r, n in enumerate(rows)]
+        values = [rand((n, dim), torch.bfloat16, device, 200000 + 16 * i + r) for r, n in enumerate(rows)]
         positions = [(torch.arange(n).float() + i).to(device)[:, None] for n in rows]
-        nk = rand((2, heads, 1, dim), torch.bfloat16, device, 3000 + i)
-        nv = rand((2, heads, 1, dim), torch.bfloat16, device, 4000 + i)
-        inputs.append((keys, values, positions, nk, nv, [100 + i, 200 + i]))
+        nk = rand((requests, heads, 1, dim), torch.bfloat16, device, 3000 + i)
+        nv = rand((requests, heads, 1, dim), torch.bfloat16, device, 4000 + i)
+        inputs.append((keys, values, positions, nk, nv, [100 * r + i for r in range(requests)]))
     torch.cuda.synchronize()
     streams = [torch.cuda.current_stream(device), torch.cuda.Stream(device)]
     for stream in streams:
@@ -343,6 +344,66 @@ def test_batch_append_staging_ring_reuse(device):
         ek, ev, ep = kv_ops.batch_append([bits(k) for k in keys], [bits(v) for v in values],
                                          [p.cpu().numpy() for p in positions], bits(nk), bits(nv),
                                          lengths, logical)
+        np.testing.assert_array_equal(bits(pk), ek)
+        np.testing.assert_array_equal(bits(pv), ev)
+        np.testing.assert_array_equal(pp.cpu().numpy(), ep)
+
+
+def _descriptor_table(keys, values, positions, lengths, logical):
+    """The 7-word rows of csrc/batch_append.cu:49-80 for device inputs."""
+    table, destination = [], 0
+    for r, head_lengths in enumerate(lengths):
+        source = 0
+        for n in head_lengths:
+            table.append([keys[r].data_ptr(), values[r].data_ptr(), positions[r].data_ptr(),
+                          source, int(n), destination, logical[r]])
+            source += int(n)
+            destination += int(n) + 1
+    return np.asarray(table, dtype=np.int64), destination
+
+
+@pytest.mark.parametrize("requests,heads", [(1, 1), (8, 8)])
+def test_batch_append_host_descriptors_through_the_abi(device, requests, heads):
+    """lr_batch_append_host (descriptors in the launch's kernel arguments) against
+    lr_batch_append (the same table in device memory) and the oracle, bit-exact. The host table
+    is overwritten right after the call while the device is still held: the overwrite describes
+    a second, valid set of inputs of the same shape, so a late read of the table would show up
+    as that set's rows."""
+    dim = 128
+    rng = np.random.default_rng(requests * 100 + heads)
+    lengths = [list(rng.integers(0, 40, heads)) for _ in range(requests)]
+    sets = []
+    for k in range(2):
+        keys = [rand((int(sum(l)), dim), torch.bfloat16, device, 10 * k + r) for r, l in enumerate(lengths)]
+        values = [rand((int(sum(l)), dim), torch.bfloat16, device, 50 + 10 * k + r) for r, l in enumerate(lengths)]
+        positions = [(torch.arange(int(sum(l))).float() + 0.5 + k).to(device)[:, None] for l in lengths]
+        logical = [300 + r + k for r in range(requests)]
+        sets.append((keys, values, positions, logical))
+    nk = rand((requests, heads, 1, dim), torch.bfloat16, device, 90)
+    nv = rand((requests, heads, 1, dim), torch.bfloat16, device, 91)
+    keys, values, positions, logical = sets[0]
+    table, rows = _descriptor_table(keys, values, positions, lengths, logical)
+    other, _ = _descriptor_table(*sets[1][:3], lengths, sets[1][3])
+    segments = requests * heads
+    max_rows = max(int(n) + 1 for l in lengths for n in l)
+    outs = [(torch.empty((rows, dim), dtype=torch.bfloat16, device=device),
+             torch.empty((rows, dim), dtype=torch.bfloat16, device=device),
+             torch.empty((rows, 1), dtype=torch.float32, device=device)) for _ in range(2)]
+    stream = _lib.stream_of(nk)
+    device_table = torch.from_numpy(table.copy()).to(device)
+    _lib.call("lr_batch_append", device_table.data_ptr(), segments, nk.data_ptr(), nv.data_ptr(),
+              dim, 2, max_rows, outs[0][0].data_ptr(), outs[0][1].data_ptr(),
+              outs[0][2].data_ptr(), stream)
+    torch.cuda._sleep(5_000_000)
+    _lib.call("lr_batch_append_host", table.ctypes.data, segments, nk.data_ptr(), nv.data_ptr(),
+              dim, 2, max_rows, outs[1][0].data_ptr(), outs[1][1].data_ptr(),
+              outs[1][2].data_ptr(), stream)
+    table[...] = other
+    torch.cuda.synchronize()
+    ek, ev, ep = kv_ops.batch_append([bits(k) for k in keys], [bits(v) for v in values],
+                                     [p.cpu().numpy() for p in positions], bits(nk), bits(nv),
+                                     lengths, logical)
+    for pk, pv, pp in outs:
         np.testing.assert_array_equal(bits(pk), ek)
         np.testing.assert_array_equal(bits(pv), ev)
         np.testing.assert_array_equal(pp.cpu().numpy(), ep)

@@ -5,6 +5,7 @@ modules expose the reference's function names and reject CPU tensors like the re
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -81,6 +82,18 @@ def test_pre_gradient_layers_width_bound_matches_per_layer_check():
     library = _lib.load()
     status = library.lr_pre_gradient_layers(None, 2, 16, 8200, _lib.LR_DTYPE_BF16, None, 0, None)
     assert status == 1 and "at most 8192" in _lib.last_error()
+
+
+def test_batch_append_host_bounds_the_descriptor_table():
+    """Descriptors in the launch's kernel arguments: at most 64 segments, rejected on the host
+    before anything touches the device."""
+    library = _lib.load()
+    table = np.zeros(65 * 7, dtype=np.int64)
+    address = table.ctypes.data
+    status = library.lr_batch_append_host(address, 65, 1, 1, 8, 2, 1, 1, 1, 1, None)
+    assert status == 1 and "Too many segments" in _lib.last_error()
+    status = library.lr_batch_append_host(None, 1, 1, 1, 8, 2, 1, 1, 1, 1, None)
+    assert status == 1 and "Request metadata mismatch" in _lib.last_error()
 
 
 def test_zero_work_calls_succeed_without_launching():
