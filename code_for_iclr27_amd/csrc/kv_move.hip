@@ -425,7 +425,13 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
 // contiguously from the destination row. The descriptor comes either from memory (a device or
 // host-coherent array) or from the launch's kernel arguments (batches of up to
 // kInlineSegments segments, read with scalar loads from the kernel-argument segment).
+//
+// A segment's old rows are contiguous in the source cache and in the output, so K and V are
+// each one flat copy of old rows x row bytes: every thread moves kAppendUnroll granules of
+// each at a stride of the segment's whole grid row, all loads issued before the stores, and
+// every wave instruction touches one contiguous span. The new row and the positions follow.
 constexpr int kInlineSegments = 64;
+constexpr int kAppendUnroll = 8;
 struct InlineDescriptors {
   int64_t words[kInlineSegments * 7];
 };
@@ -433,80 +439,93 @@ struct InlineDescriptors {
 template <int G>
 __device__ __forceinline__ void batch_append_segment(
     const int64_t (&d)[7], int64_t segment, const uint8_t* __restrict__ new_keys,
-    const uint8_t* __restrict__ new_values, int64_t max_rows, const RowLayout& layout,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, int64_t row_bytes,
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
-  const GroupCoord gc = group_coord(layout.lanes_log2);
-  const uint8_t* keys = reinterpret_cast<const uint8_t*>(d[0]);
-  const uint8_t* values = reinterpret_cast<const uint8_t*>(d[1]);
-  const float* positions = reinterpret_cast<const float*>(d[2]);
+  using T = typename RawGranule<G>::type;
   const int64_t source = d[3], old_length = d[4], destination = d[5], logical = d[6];
   int64_t total = old_length + 1;
   if (total > max_rows) total = max_rows;
-  const int64_t R = layout.rows_per_group;
-  const int64_t rb = layout.row_bytes;
-  for (int64_t first = (static_cast<int64_t>(blockIdx.x) * gc.groups_per_block + gc.group) * R;
-       first < total;
-       first += static_cast<int64_t>(gridDim.x) * gc.groups_per_block * R) {
-    const int64_t end = first + R < total ? first + R : total;
-    for (int64_t p0 = first; p0 < end; p0 += kBatch) {
-      RowBatch<true> b;
+  const int64_t old_rows = old_length < total ? old_length : total;
+  const int64_t granules = old_rows * row_bytes / G;  // per tensor
+  const T* __restrict__ ks = reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(d[0]) + source * row_bytes);
+  const T* __restrict__ vs = reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(d[1]) + source * row_bytes);
+  T* __restrict__ kd = reinterpret_cast<T*>(out_keys + destination * row_bytes);
+  T* __restrict__ vd = reinterpret_cast<T*>(out_values + destination * row_bytes);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  int64_t i = first;
+  for (; i + (kAppendUnroll - 1) * stride < granules; i += kAppendUnroll * stride) {
+    T k[kAppendUnroll], v[kAppendUnroll];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int64_t p = p0 + u, dst = destination + p;
-        const bool ok = p < end;
-        const bool old = ok && p < old_length;
-        b.ok[u] = ok;
-        // rows past the end (and the new row) read the segment's new row
-        b.src[u] = old ? keys + (source + p) * rb : new_keys + segment * rb;
-        b.src2[u] = old ? values + (source + p) * rb : new_values + segment * rb;
-        b.dst[u] = out_keys + dst * rb;
-        b.dst2[u] = out_values + dst * rb;
+    for (int u = 0; u < kAppendUnroll; ++u) {
+      k[u] = ks[i + u * stride];
+      v[u] = vs[i + u * stride];
+    }
+#pragma unroll
+    for (int u = 0; u < kAppendUnroll; ++u) {
+      kd[i + u * stride] = k[u];
+      vd[i + u * stride] = v[u];
+    }
+  }
+  {  // the rest: fewer than kAppendUnroll granules per thread, loads still issued together
+    T k[kAppendUnroll], v[kAppendUnroll];
+#pragma unroll
+    for (int u = 0; u < kAppendUnroll; ++u) {
+      if (i + u * stride < granules) {
+        k[u] = ks[i + u * stride];
+        v[u] = vs[i + u * stride];
       }
-      float position[kBatch];
+    }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int64_t p = p0 + u;
-        const bool old = p < end && p < old_length;
-        // rows without an old position read the first one (only when the segment has old rows)
-        const float loaded = old_length > 0 ? positions[source + (old ? p : 0)] : 0.0f;
-        position[u] = old ? loaded : static_cast<float>(logical);
-      }
-      copy_batch<G, true>(b, layout.chunks, gc.lane, gc.lanes);
-      if (gc.lane == 0) {
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-          if (b.ok[u]) out_positions[destination + p0 + u] = position[u];
+    for (int u = 0; u < kAppendUnroll; ++u) {
+      if (i + u * stride < granules) {
+        kd[i + u * stride] = k[u];
+        vd[i + u * stride] = v[u];
       }
     }
   }
+  if (old_rows < total) {  // the new row (only when the clamp left room for it)
+    const int64_t row_granules = row_bytes / G;
+    const T* __restrict__ nk = reinterpret_cast<const T*>(new_keys + segment * row_bytes);
+    const T* __restrict__ nv = reinterpret_cast<const T*>(new_values + segment * row_bytes);
+    T* __restrict__ rk = reinterpret_cast<T*>(out_keys + (destination + old_rows) * row_bytes);
+    T* __restrict__ rv = reinterpret_cast<T*>(out_values + (destination + old_rows) * row_bytes);
+    for (int64_t j = first; j < row_granules; j += stride) {
+      rk[j] = nk[j];
+      rv[j] = nv[j];
+    }
+  }
+  const float* __restrict__ positions = reinterpret_cast<const float*>(d[2]);
+  for (int64_t p = first; p < total; p += stride)
+    out_positions[destination + p] = p < old_rows ? positions[source + p] : static_cast<float>(logical);
 }
 
 template <int G>
 __global__ __launch_bounds__(kThreads) void batch_append_kernel(
     const int64_t* __restrict__ descriptors, const uint8_t* __restrict__ new_keys,
-    const uint8_t* __restrict__ new_values, int64_t max_rows, RowLayout layout,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, int64_t row_bytes,
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
   const int64_t segment = blockIdx.y;
   int64_t d[7];
 #pragma unroll
   for (int i = 0; i < 7; ++i) d[i] = descriptors[segment * 7 + i];
-  batch_append_segment<G>(d, segment, new_keys, new_values, max_rows, layout, out_keys,
+  batch_append_segment<G>(d, segment, new_keys, new_values, max_rows, row_bytes, out_keys,
                           out_values, out_positions);
 }
 
 template <int G>
 __global__ __launch_bounds__(kThreads) void batch_append_inline_kernel(
     const InlineDescriptors descriptors, const uint8_t* __restrict__ new_keys,
-    const uint8_t* __restrict__ new_values, int64_t max_rows, RowLayout layout,
+    const uint8_t* __restrict__ new_values, int64_t max_rows, int64_t row_bytes,
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions) {
   const int64_t segment = blockIdx.y;
   int64_t d[7];
 #pragma unroll
   for (int i = 0; i < 7; ++i) d[i] = descriptors.words[segment * 7 + i];
-  batch_append_segment<G>(d, segment, new_keys, new_values, max_rows, layout, out_keys,
+  batch_append_segment<G>(d, segment, new_keys, new_values, max_rows, row_bytes, out_keys,
                           out_values, out_positions);
 }
 
@@ -1058,11 +1077,12 @@ int batch_append_launch(int64_t segments, const void* new_keys, const void* new_
   // number of rows from a 16-byte aligned allocation), so only the row size and the
   // pointers seen here bound the granule.
   const int g = granule_for(row_bytes, {new_keys, new_values, out_keys, out_values});
-  const RowLayout layout = make_layout(row_bytes, g, max_rows * segments, 8);
-  int64_t bx = ceil_div(ceil_div(max_rows, layout.rows_per_group), kThreads >> layout.lanes_log2);
+  // workgroups per segment: one pass of kAppendUnroll granules per thread over the longest
+  // segment's old rows
+  int64_t bx = ceil_div(ceil_div(max_rows * row_bytes, g), int64_t{kThreads} * kAppendUnroll);
   if (bx < 1) bx = 1;
   const dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(segments));
-  return dispatch_granule(g, [&]<int G>() { return launch.template operator()<G>(layout, grid); });
+  return dispatch_granule(g, [&]<int G>() { return launch.template operator()<G>(row_bytes, grid); });
 }
 
 }  // namespace
@@ -1075,10 +1095,10 @@ extern "C" int lr_batch_append(const int64_t* descriptors, int64_t segments,
   LR_REQUIRE(descriptors != nullptr, "Contiguous CUDA states required");
   return batch_append_launch(
       segments, new_keys, new_values, dim, elem_bytes, max_rows, out_keys, out_values,
-      out_positions, [&]<int G>(const RowLayout& layout, dim3 grid) {
+      out_positions, [&]<int G>(int64_t row_bytes, dim3 grid) {
         batch_append_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
-            descriptors, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
-            bytes(out_values), out_positions);
+            descriptors, bytes(new_keys), bytes(new_values), max_rows, row_bytes,
+            bytes(out_keys), bytes(out_values), out_positions);
         return check_launch("batch_append");
       });
 }
@@ -1095,9 +1115,9 @@ extern "C" int lr_batch_append_host(const int64_t* host_descriptors, int64_t seg
     std::memcpy(words.words, host_descriptors, static_cast<size_t>(segments) * 7 * sizeof(int64_t));
   return batch_append_launch(
       segments, new_keys, new_values, dim, elem_bytes, max_rows, out_keys, out_values,
-      out_positions, [&]<int G>(const RowLayout& layout, dim3 grid) {
+      out_positions, [&]<int G>(int64_t row_bytes, dim3 grid) {
         batch_append_inline_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
-            words, bytes(new_keys), bytes(new_values), max_rows, layout, bytes(out_keys),
+            words, bytes(new_keys), bytes(new_values), max_rows, row_bytes, bytes(out_keys),
             bytes(out_values), out_positions);
         return check_launch("batch_append");
       });
