@@ -77,12 +77,14 @@ struct GroupCoord {
   int lane, lanes, group, groups_per_block;
 };
 
+// Every row kernel runs with kThreads threads per block; the constant spares each kernel a
+// dependent load of the block size at its start.
 __device__ __forceinline__ GroupCoord group_coord(int lanes_log2) {
   GroupCoord g;
   g.lanes = 1 << lanes_log2;
   g.lane = threadIdx.x & (g.lanes - 1);
   g.group = threadIdx.x >> lanes_log2;
-  g.groups_per_block = blockDim.x >> lanes_log2;
+  g.groups_per_block = kThreads >> lanes_log2;
   return g;
 }
 
@@ -142,6 +144,56 @@ __device__ __forceinline__ void copy_batch(const RowBatch<kTwo>& b, int64_t chun
   }
 }
 
+// Granules [0, count) of one or two flat ranges (K and V), `U` granules per thread at a
+// stride of the whole grid row (`first` = the thread's index in that row), every load of a
+// round issued before its stores, each wave instruction on one contiguous span.
+template <int U, int P, bool kTwo, typename V>
+__device__ __forceinline__ void flat_copy(const V* src, V* dst, const V* src2, V* dst2,
+                                          int64_t count, int64_t first, int64_t stride) {
+  const auto s1 = global_ptr(src);
+  const auto s2 = global_ptr(src2);
+  const auto d1 = global_ptr(dst);
+  const auto d2 = global_ptr(dst2);
+  auto load = [](auto p) {
+    if constexpr ((P & 1) != 0) return __builtin_nontemporal_load(p);
+    else return *p;
+  };
+  auto store = [](auto p, V v) {
+    if constexpr ((P & 2) != 0) __builtin_nontemporal_store(v, p);
+    else *p = v;
+  };
+  const int64_t end = count;
+  int64_t i = first;
+  for (; i + (U - 1) * stride < end; i += U * stride) {
+    V x[U], y[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      x[u] = load(s1 + i + u * stride);
+      if constexpr (kTwo) y[u] = load(s2 + i + u * stride);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      store(d1 + i + u * stride, x[u]);
+      if constexpr (kTwo) store(d2 + i + u * stride, y[u]);
+    }
+  }
+  V x[U], y[U];  // the rest: fewer than U granules for this thread
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (i + u * stride < end) {
+      x[u] = load(s1 + i + u * stride);
+      if constexpr (kTwo) y[u] = load(s2 + i + u * stride);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (i + u * stride < end) {
+      store(d1 + i + u * stride, x[u]);
+      if constexpr (kTwo) store(d2 + i + u * stride, y[u]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Compaction of one row range: output rows [d0, d0 + n) of a head of `length` rows minus the
 // sorted removal list `removed` land at out_start + d0... Output d takes input d + j,
@@ -165,7 +217,7 @@ __device__ __forceinline__ void compact_block(const uint8_t* keys, const uint8_t
   __shared__ int64_t source[kCompactRows];
   const bool in_lds = removed_count <= kCompactStaged;
   if (in_lds)
-    for (int64_t i = threadIdx.x; i < removed_count; i += blockDim.x)
+    for (int64_t i = threadIdx.x; i < removed_count; i += kThreads)
       staged[i] = static_cast<int32_t>(removed[i]);
   __syncthreads();
   if (static_cast<int>(threadIdx.x) < n) {
@@ -295,19 +347,93 @@ __device__ __forceinline__ void head_append(
   }
 }
 
-template <int G, bool kWithPositions>
-__global__ __launch_bounds__(kThreads) void head_append_kernel(
+// The same append as flat copies: a head's old rows are one contiguous run in the cache and
+// in the output (and its new rows one run in new_keys), so the rows the checks above admit form
+// one interval per run, copied granule by granule with `U` granules per thread in flight. The
+// positions and the output metadata follow the row form exactly.
+template <int G, bool kWithPositions, int P, int U, int kBlock>
+__device__ __forceinline__ void head_append_flat(
     const uint8_t* __restrict__ cache_keys, const uint8_t* __restrict__ cache_values,
     const float* __restrict__ positions, int64_t rows_in, const uint8_t* __restrict__ new_keys,
     const uint8_t* __restrict__ new_values, const int32_t* __restrict__ starts,
     const int32_t* __restrict__ lengths_or_next, int lengths_are_cumulative, int64_t heads,
-    int64_t added, int64_t covered_rows, int64_t logical_start, RowLayout layout,
+    int64_t added, int64_t covered_rows, int64_t logical_start, int64_t row_bytes,
     uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
     float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
     int32_t* __restrict__ out_lengths) {
-  head_append<G, kWithPositions, kCached>(
+  constexpr bool kTwo = kWithPositions;  // the legacy single-tensor form has no values
+  using V = typename RawGranule<G>::type;
+  const int64_t head = blockIdx.y;
+  const int64_t old_start = starts[head];
+  const int64_t old_length = lengths_are_cumulative ? lengths_or_next[head + 1] - old_start
+                                                    : lengths_or_next[head];
+  const int64_t new_start = old_start + head * added;
+  if (out_cumulative != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    out_cumulative[head] = static_cast<int32_t>(new_start);
+    out_lengths[head] = static_cast<int32_t>(old_length + added);
+    if (head == heads - 1)
+      out_cumulative[heads] = static_cast<int32_t>(lengths_or_next[heads] + heads * added);
+  }
+  int64_t total = old_length + added;
+  if (total > covered_rows) total = covered_rows;
+  const int64_t rows_out = rows_in + heads * added;
+  const int64_t rg = row_bytes / G;  // granules per row
+  // the block size as a constant: blockDim would be one more dependent load at the start
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  // rows p with a destination in the output: [-new_start, rows_out - new_start)
+  const int64_t dst_lo = -new_start, dst_hi = rows_out - new_start;
+  // old rows: p < old_length with the source row inside the cache
+  int64_t lo = max(max(int64_t{0}, dst_lo), -old_start);
+  int64_t hi = min(min(old_length, total), min(dst_hi, rows_in - old_start));
+  auto out_k = [&](int64_t p) { return reinterpret_cast<V*>(out_keys) + (new_start + p) * rg; };
+  auto out_v = [&](int64_t p) {
+    return kTwo ? reinterpret_cast<V*>(out_values) + (new_start + p) * rg : nullptr;
+  };
+  if (lo < hi)
+    flat_copy<U, P, kTwo>(
+        reinterpret_cast<const V*>(cache_keys) + (old_start + lo) * rg, out_k(lo),
+        kTwo ? reinterpret_cast<const V*>(cache_values) + (old_start + lo) * rg : nullptr,
+        out_v(lo), (hi - lo) * rg, first, stride);
+  // new rows: p in [old_length, total), row head * added + (p - old_length) of the new rows
+  lo = max(max(int64_t{0}, dst_lo), old_length);
+  hi = min(total, dst_hi);
+  if (lo < hi) {
+    const int64_t row = head * added + (lo - old_length);
+    flat_copy<1, P, kTwo>(reinterpret_cast<const V*>(new_keys) + row * rg, out_k(lo),
+                          kTwo ? reinterpret_cast<const V*>(new_values) + row * rg : nullptr,
+                          out_v(lo), (hi - lo) * rg, first, stride);
+  }
+  if constexpr (kWithPositions) {
+    for (int64_t p = first; p < total; p += stride) {
+      const int64_t dst = new_start + p;
+      const bool old = p < old_length;
+      const int64_t src = old_start + p;
+      if (dst < 0 || dst >= rows_out || (old && (src < 0 || src >= rows_in))) continue;
+      out_positions[dst] = old ? positions[src] : static_cast<float>(logical_start + (p - old_length));
+    }
+  }
+}
+
+// The per-layer appends (one layer, tens of MB: a single round of copies over the chip) in
+// two-wave workgroups of two granules per thread and tensor (measured fastest of 64-256
+// threads with 1-8 granules for a cfg1 layer).
+constexpr int kAppendThreads = 128;
+constexpr int kAppendLayerUnroll = 2;
+
+template <int G, bool kWithPositions>
+__global__ __launch_bounds__(kAppendThreads) void head_append_kernel(
+    const uint8_t* __restrict__ cache_keys, const uint8_t* __restrict__ cache_values,
+    const float* __restrict__ positions, int64_t rows_in, const uint8_t* __restrict__ new_keys,
+    const uint8_t* __restrict__ new_values, const int32_t* __restrict__ starts,
+    const int32_t* __restrict__ lengths_or_next, int lengths_are_cumulative, int64_t heads,
+    int64_t added, int64_t covered_rows, int64_t logical_start, int64_t row_bytes,
+    uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
+    int32_t* __restrict__ out_lengths) {
+  head_append_flat<G, kWithPositions, kCached, kAppendLayerUnroll, kAppendThreads>(
       cache_keys, cache_values, positions, rows_in, new_keys, new_values, starts, lengths_or_next,
-      lengths_are_cumulative, heads, added, covered_rows, logical_start, layout, out_keys,
+      lengths_are_cumulative, heads, added, covered_rows, logical_start, row_bytes, out_keys,
       out_values, out_positions, out_cumulative, out_lengths);
 }
 
@@ -447,56 +573,21 @@ __device__ __forceinline__ void batch_append_segment(
   int64_t total = old_length + 1;
   if (total > max_rows) total = max_rows;
   const int64_t old_rows = old_length < total ? old_length : total;
-  const int64_t granules = old_rows * row_bytes / G;  // per tensor
-  const T* __restrict__ ks = reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(d[0]) + source * row_bytes);
-  const T* __restrict__ vs = reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(d[1]) + source * row_bytes);
-  T* __restrict__ kd = reinterpret_cast<T*>(out_keys + destination * row_bytes);
-  T* __restrict__ vd = reinterpret_cast<T*>(out_values + destination * row_bytes);
+  const int64_t rg = row_bytes / G;  // granules per row
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  int64_t i = first;
-  for (; i + (kAppendUnroll - 1) * stride < granules; i += kAppendUnroll * stride) {
-    T k[kAppendUnroll], v[kAppendUnroll];
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      k[u] = ks[i + u * stride];
-      v[u] = vs[i + u * stride];
-    }
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      kd[i + u * stride] = k[u];
-      vd[i + u * stride] = v[u];
-    }
-  }
-  {  // the rest: fewer than kAppendUnroll granules per thread, loads still issued together
-    T k[kAppendUnroll], v[kAppendUnroll];
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      if (i + u * stride < granules) {
-        k[u] = ks[i + u * stride];
-        v[u] = vs[i + u * stride];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kAppendUnroll; ++u) {
-      if (i + u * stride < granules) {
-        kd[i + u * stride] = k[u];
-        vd[i + u * stride] = v[u];
-      }
-    }
-  }
-  if (old_rows < total) {  // the new row (only when the clamp left room for it)
-    const int64_t row_granules = row_bytes / G;
-    const T* __restrict__ nk = reinterpret_cast<const T*>(new_keys + segment * row_bytes);
-    const T* __restrict__ nv = reinterpret_cast<const T*>(new_values + segment * row_bytes);
-    T* __restrict__ rk = reinterpret_cast<T*>(out_keys + (destination + old_rows) * row_bytes);
-    T* __restrict__ rv = reinterpret_cast<T*>(out_values + (destination + old_rows) * row_bytes);
-    for (int64_t j = first; j < row_granules; j += stride) {
-      rk[j] = nk[j];
-      rv[j] = nv[j];
-    }
-  }
-  const float* __restrict__ positions = reinterpret_cast<const float*>(d[2]);
+  flat_copy<kAppendUnroll, kCached, true>(
+      reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(d[0]) + source * row_bytes),
+      reinterpret_cast<T*>(out_keys + destination * row_bytes),
+      reinterpret_cast<const T*>(reinterpret_cast<const uint8_t*>(d[1]) + source * row_bytes),
+      reinterpret_cast<T*>(out_values + destination * row_bytes), old_rows * rg, first, stride);
+  if (old_rows < total)  // the new row (only when the clamp left room for it)
+    flat_copy<1, kCached, true>(
+        reinterpret_cast<const T*>(new_keys + segment * row_bytes),
+        reinterpret_cast<T*>(out_keys + (destination + old_rows) * row_bytes),
+        reinterpret_cast<const T*>(new_values + segment * row_bytes),
+        reinterpret_cast<T*>(out_values + (destination + old_rows) * row_bytes), rg, first, stride);
+  const auto positions = global_ptr(reinterpret_cast<const float*>(d[2]));
   for (int64_t p = first; p < total; p += stride)
     out_positions[destination + p] = p < old_rows ? positions[source + p] : static_cast<float>(logical);
 }
@@ -928,6 +1019,18 @@ extern "C" int lr_compact(const void* keys, const void* values, const float* pos
   });
 }
 
+namespace {
+
+// Workgroups per head for the per-layer appends: one round of kAppendLayerUnroll granules per
+// thread over `rows` rows of `granules_per_row` granules.
+int64_t append_blocks(int64_t rows, int64_t granules_per_row) {
+  int64_t bx = ceil_div(rows * granules_per_row, int64_t{kAppendThreads} * kAppendLayerUnroll);
+  if (bx < 1) bx = 1;
+  return bx < 65535 ? bx : 65535;
+}
+
+}  // namespace
+
 extern "C" int lr_append(const void* keys, const void* values, const float* positions,
                          int64_t rows, const void* new_keys, const void* new_values,
                          const int32_t* cumulative, int64_t heads, int64_t added, int64_t dim,
@@ -945,18 +1048,12 @@ extern "C" int lr_append(const void* keys, const void* values, const float* posi
   const int64_t row_bytes = dim * elem_bytes;
   const int g = granule_for(row_bytes, {keys, values, new_keys, new_values, out_keys, out_values});
   const int64_t covered = max_length + added;
-  const RowLayout layout = make_layout(row_bytes, g, covered * heads, 8);
-  // Two-wave workgroups: one decode step's layer (cfg1: 18 MB) is a single round of copies, and
-  // twice the workgroups of 256 threads spread it evenly over the CUs (measured 13% less device
-  // time per layer than 256-thread workgroups).
-  constexpr int kAppendThreads = 128;
-  int64_t bx = ceil_div(ceil_div(covered, layout.rows_per_group), kAppendThreads >> layout.lanes_log2);
-  if (bx < 1) bx = 1;
-  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads));
+  const int64_t bx = append_blocks(covered, row_bytes / g);
+  dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(heads));
   return dispatch_granule(g, [&]<int G>() {
     head_append_kernel<G, true><<<grid, kAppendThreads, 0, as_stream(stream)>>>(
         bytes(keys), bytes(values), positions, rows, bytes(new_keys), bytes(new_values),
-        cumulative, cumulative, 1, heads, added, covered, logical_start, layout,
+        cumulative, cumulative, 1, heads, added, covered, logical_start, row_bytes,
         bytes(out_keys), bytes(out_values), out_positions, out_cumulative, out_lengths);
     return check_launch("append");
   });
@@ -974,17 +1071,16 @@ extern "C" int lr_append_flattened_cache(const void* cache, int64_t rows, const 
   LR_REQUIRE(rows == 0 || cache, "cache must be CUDA");
   const int64_t row_bytes = dim * elem_bytes;
   const int g = granule_for(row_bytes, {cache, states, out});
-  // Rows per head are bounded by the whole cache plus the new rows.
+  // Rows per head are bounded by the whole cache plus the new rows; the grid covers the mean
+  // head (its threads stride over longer ones).
   const int64_t covered = rows + new_length;
-  const RowLayout layout = make_layout(row_bytes, g, rows + total_heads * new_length, 8);
-  int64_t per_head = ceil_div(rows + total_heads * new_length, total_heads);
-  int64_t bx = ceil_div(ceil_div(per_head, layout.rows_per_group), kThreads >> layout.lanes_log2);
-  if (bx < 1) bx = 1;
-  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(total_heads));
+  const int64_t per_head = ceil_div(rows + total_heads * new_length, total_heads);
+  const int64_t bx = append_blocks(per_head, row_bytes / g);
+  dim3 grid(static_cast<unsigned>(bx), static_cast<unsigned>(total_heads));
   return dispatch_granule(g, [&]<int G>() {
-    head_append_kernel<G, false><<<grid, kThreads, 0, as_stream(stream)>>>(
+    head_append_kernel<G, false><<<grid, kAppendThreads, 0, as_stream(stream)>>>(
         bytes(cache), nullptr, nullptr, rows, bytes(states), nullptr, cu_head_lens, head_lens, 0,
-        total_heads, new_length, covered, 0, layout, bytes(out), nullptr, nullptr, nullptr,
+        total_heads, new_length, covered, 0, row_bytes, bytes(out), nullptr, nullptr, nullptr,
         nullptr);
     return check_launch("append_flattened_cache");
   });

@@ -128,6 +128,38 @@ def test_append(device, dtype, added, dim):
     np.testing.assert_array_equal(got[4].cpu().numpy(), expect[4])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("added,max_length", [(1, 40), (3, 63), (2, 0)])
+def test_append_rows_beyond_max_length_stay_unwritten(device, dtype, added, max_length):
+    """maximum_length sizes the grid as in the reference (csrc/scoring.cu:264-292): a head keeps
+    only its first maximum_length + added rows, old rows first. Through the C-ABI into zeroed
+    outputs, so the rows it must not write read as the oracle's zeros."""
+    lengths, dim = [7, 0, 300, 1, 64, 2, 9, 33], 128
+    heads, rows = len(lengths), sum(lengths)
+    keys, values = rand((rows, dim), dtype, device, 16), rand((rows, dim), dtype, device, 17)
+    positions = torch.arange(rows).float().to(device)[:, None] + 0.25
+    new_k = rand((1, heads, added, dim), dtype, device, 18)
+    new_v = rand((1, heads, added, dim), dtype, device, 19)
+    cumulative = torch.tensor(np.concatenate(([0], np.cumsum(lengths))), dtype=torch.int32, device=device)
+    out_rows = rows + heads * added
+    out_k = torch.zeros((out_rows, dim), dtype=dtype, device=device)
+    out_v = torch.zeros((out_rows, dim), dtype=dtype, device=device)
+    out_p = torch.zeros((out_rows, 1), device=device)
+    out_c = torch.zeros(heads + 1, dtype=torch.int32, device=device)
+    out_l = torch.zeros(heads, dtype=torch.int32, device=device)
+    _lib.call("lr_append", keys.data_ptr(), values.data_ptr(), positions.data_ptr(), rows,
+              new_k.data_ptr(), new_v.data_ptr(), cumulative.data_ptr(), heads, added, dim,
+              keys.element_size(), 777, max_length, out_k.data_ptr(), out_v.data_ptr(),
+              out_p.data_ptr(), out_c.data_ptr(), out_l.data_ptr(), _lib.stream_of(keys))
+    expect = kv_ops.append(bits(keys), bits(values), positions.cpu().numpy(), bits(new_k),
+                           bits(new_v), cumulative.cpu().numpy(), 777, max_length)
+    np.testing.assert_array_equal(bits(out_k), expect[0])
+    np.testing.assert_array_equal(bits(out_v), expect[1])
+    np.testing.assert_array_equal(out_p.cpu().numpy(), expect[2])
+    np.testing.assert_array_equal(out_c.cpu().numpy(), expect[3])
+    np.testing.assert_array_equal(out_l.cpu().numpy(), expect[4])
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("added,dim", [(1, 128), (3, 64), (2, 3)])
 def test_append_layers_matches_per_layer_append(device, dtype, added, dim):
