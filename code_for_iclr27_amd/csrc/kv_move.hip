@@ -688,6 +688,7 @@ __global__ __launch_bounds__(kThreads) void compact_heads_kernel(
 //   [0] keys ptr, [1] values ptr, [2] positions ptr (f32) of the head's first resident row,
 //   [3] resident rows, [4] first entry of the head's recalled run, [5] recalled rows of the
 //   head, [6] first output row of the merged head, [7] unused (0).
+constexpr int kPlanRankMax = 1024;  // runs the plan sorts by rank counting (else bitonic)
 constexpr int kReinsertMax = LR_REINSERT_MAX_PER_HEAD;  // recalled rows of one head (sorted in LDS)
 
 // One workgroup per slot: its recalled entries sorted by position in LDS (bitonic), each one's
@@ -702,19 +703,27 @@ __global__ __launch_bounds__(kThreads) void reinsert_plan_kernel(
     int32_t* __restrict__ cumulative) {
   __shared__ int64_t key[kReinsertMax];
   __shared__ int64_t value[kReinsertMax];
+  __shared__ __align__(16) uint64_t packed[kPlanRankMax + 2];
   const int64_t slot = blockIdx.x;
   const int64_t* entry = table + slot * LR_REINSERT_WORDS;
   const int64_t first = entry[4], r = entry[5];
-  if (head_lens != nullptr && threadIdx.x == 0) {
+  if (head_lens != nullptr && threadIdx.x < 64) {
     // the layer's new metadata (replace_head_lens after insert_payload, cache.py:246): this
-    // head's merged length and its end in the layer's cumulative lengths
+    // head's merged length and its end in the layer's cumulative lengths, the heads up to this
+    // one summed across the first wave (their table rows loaded at once)
     const int64_t layer = slot / heads_per_layer, h = slot - layer * heads_per_layer;
-    int64_t end = 0;
-    for (int64_t k = layer * heads_per_layer; k <= slot; ++k)
-      end += table[k * LR_REINSERT_WORDS + 3] + table[k * LR_REINSERT_WORDS + 5];
-    head_lens[slot] = static_cast<int32_t>(entry[3] + r);
-    cumulative[layer * (heads_per_layer + 1) + h + 1] = static_cast<int32_t>(end);
-    if (h == 0) cumulative[layer * (heads_per_layer + 1)] = 0;
+    int64_t part = 0;
+    for (int64_t k = threadIdx.x; k <= h; k += 64) {
+      const int64_t* row = table + (layer * heads_per_layer + k) * LR_REINSERT_WORDS;
+      part += row[3] + row[5];
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) part += __shfl_xor(part, offset);
+    if (threadIdx.x == 0) {
+      head_lens[slot] = static_cast<int32_t>(entry[3] + r);
+      cumulative[layer * (heads_per_layer + 1) + h + 1] = static_cast<int32_t>(part);
+      if (h == 0) cumulative[layer * (heads_per_layer + 1)] = 0;
+    }
   }
   if (r == 0) return;
   if (r > kReinsertMax) {
@@ -723,12 +732,58 @@ __global__ __launch_bounds__(kThreads) void reinsert_plan_kernel(
   }
   int n2 = 1;
   while (n2 < r) n2 <<= 1;
+  // Runs of up to kPlanRankMax entries whose (position, source) pairs pack into one u64 each
+  // (position in [0, 2^31), source in [0, 2^32)) are sorted by rank counting: every entry
+  // counts the smaller packed pairs in LDS, then moves to its rank. The pairs are unique (one
+  // source per entry), so the ranks are a permutation. Other runs take the bitonic network.
+  bool packable = true;
   for (int k = threadIdx.x; k < n2; k += kThreads) {
-    key[k] = k < r ? grouped[first + k] : INT64_MAX;
-    value[k] = k < r ? grouped[count + first + k] : -1;
+    const int64_t position = k < r ? grouped[first + k] : INT64_MAX;
+    const int64_t source = k < r ? grouped[count + first + k] : -1;
+    key[k] = position;
+    value[k] = source;
+    if (k < r && (position < 0 || position >= (int64_t{1} << 31) || source < 0 ||
+                  source >= (int64_t{1} << 32)))
+      packable = false;
   }
-  __syncthreads();
-  for (int size = 2; size <= n2; size <<= 1) {
+  packable = __syncthreads_and(packable) && r <= kPlanRankMax;
+  if (packable) {
+    for (int k = threadIdx.x; k < r; k += kThreads)
+      packed[k] = (static_cast<uint64_t>(key[k]) << 32) | static_cast<uint64_t>(value[k]);
+    if (threadIdx.x == 0 && (r & 1)) packed[r] = ~uint64_t{0};  // pads the last pair read
+    __syncthreads();
+    // E entries per thread (the fewest that cover the run), each ranked over all pairs
+    auto rank_entries = [&]<int E>() {
+      uint64_t mine[E];
+      uint32_t rank[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int k = threadIdx.x + e * kThreads;
+        mine[e] = k < r ? packed[k] : ~uint64_t{0};
+        rank[e] = 0;
+      }
+      const int pairs = static_cast<int>((r + 1) >> 1);
+#pragma unroll 8
+      for (int j = 0; j < pairs; ++j) {
+        const ulonglong2 c = reinterpret_cast<const ulonglong2*>(packed)[j];
+#pragma unroll
+        for (int e = 0; e < E; ++e) rank[e] += (c.x < mine[e]) + (c.y < mine[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int k = threadIdx.x + e * kThreads;
+        if (k < r) {
+          key[rank[e]] = static_cast<int64_t>(mine[e] >> 32);
+          value[rank[e]] = static_cast<int64_t>(mine[e] & 0xffffffffu);
+        }
+      }
+    };
+    if (r <= kThreads) rank_entries.template operator()<1>();
+    else if (r <= 2 * kThreads) rank_entries.template operator()<2>();
+    else rank_entries.template operator()<kPlanRankMax / kThreads>();
+    __syncthreads();
+  }
+  for (int size = 2; size <= (packable ? 1 : n2); size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int k = threadIdx.x; k < n2; k += kThreads) {
         const int other = k ^ stride;
