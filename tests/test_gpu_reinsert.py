@@ -147,6 +147,19 @@ def test_reinsert_refuses_duplicates_and_bad_identities(device, meta_form):
     check(outcome, layers, payload, meta)
 
 
+@pytest.mark.parametrize("meta_form", ["host", "device"])
+def test_reinsert_long_runs_sorted_both_ways(device, meta_form):
+    """The plan sorts runs of up to 1,024 recalled rows by rank counting (one, two or four
+    entries per thread) and longer ones with the bitonic network: heads with 2,000, 1,024, 700
+    and 300 recalled rows, bit-exact against merge_plan and merge."""
+    layers, payload, meta = make_case(device, [[300, 500, 200, 64]], [2000, 1024, 700, 300], 64,
+                                      seed=9)
+    outcome = reinsert.Reinserter().run(layers, payload.pin_memory(),
+                                        metadata_as(meta, meta_form, device))
+    torch.cuda.synchronize()
+    check(outcome, layers, payload, meta)
+
+
 def test_reinsert_device_grouped_head_limit(device):
     """More than LR_REINSERT_MAX_PER_HEAD recalled rows for one head: refused from the device
     flag, with every launch staying inside its buffers."""
