@@ -97,7 +97,8 @@ def _native():
         address = lambda name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
         planner.bind_data_movement(address("lr_append"), address("lr_compact"),
                                    address("lr_append_layers"), address("lr_batch_append"),
-                                   address("lr_batch_append_host"))
+                                   address("lr_batch_append_host"),
+                                   address("lr_append_layers_host"))
         _native_module = planner
     return _native_module
 

@@ -41,6 +41,7 @@ SIGNATURES = {
     "lr_append": [_P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I, _I64, _I64, _P, _P, _P, _P,
                   _P, _P],
     "lr_append_layers": [_P, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P, _P, _P],
+    "lr_append_layers_host": [_P, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P, _P, _P],
     "lr_compact": [_P, _P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P, _P],
     "lr_pool": [_P, _I64, _P, _I64, _I64, _I64, _P, _P],
     "lr_merge": [_P, _P, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I, _P, _P, _P, _P],

@@ -234,6 +234,7 @@ struct Library {
   decltype(&lr_append) append = nullptr;
   decltype(&lr_compact) compact = nullptr;
   decltype(&lr_append_layers) append_layers = nullptr;
+  decltype(&lr_append_layers_host) append_layers_host = nullptr;
   decltype(&lr_batch_append) batch_append = nullptr;
   decltype(&lr_batch_append_host) batch_append_host = nullptr;
   decltype(&lr_packed_attention) packed_attention = nullptr;
@@ -278,12 +279,14 @@ void bind_library(int64_t score_workspace_bytes, int64_t score_segments, int64_t
 }
 
 void bind_data_movement(int64_t append, int64_t compact, int64_t append_layers,
-                        int64_t batch_append, int64_t batch_append_host) {
+                        int64_t batch_append, int64_t batch_append_host,
+                        int64_t append_layers_host) {
   bind_one(library.append, append);
   bind_one(library.compact, compact);
   bind_one(library.append_layers, append_layers);
   bind_one(library.batch_append, batch_append);
   bind_one(library.batch_append_host, batch_append_host);
+  bind_one(library.append_layers_host, append_layers_host);
 }
 
 void bind_reinsert(int64_t group, int64_t plan_layout, int64_t resident, int64_t recalled) {
@@ -1452,8 +1455,12 @@ std::vector<torch::Tensor> compact_launch(const torch::Tensor& keys, const torch
   return {out_keys, out_values, out_positions};
 }
 
+// The most layers whose append table lr_append_layers_host takes in the launch.
+constexpr int64_t kInlineAppendLayers = 48;
+
 // One decode step's append into every layer (lr_append_layers): the per-layer checks of
-// append_launch for each layer, one pinned table uploaded without blocking, packed outputs and
+// append_launch for each layer, the table (in the launch's kernel arguments for up to
+// kInlineAppendLayers layers, else pinned and uploaded without blocking), packed outputs and
 // one launch. Returns (keys, values, positions [rows, 1], cumulative [L, H + 1] i32, lengths
 // [L, H] i32, first output row of each layer [L + 1]).
 py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
@@ -1472,9 +1479,16 @@ py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
           "Layer lists differ in length");
   const torch::Tensor& k0 = keys[0];
   int64_t heads = 0, added = 0, dim = 0;
-  torch::Tensor table = torch::empty({static_cast<int64_t>(layers) * LR_APPEND_WORDS},
-                                     torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
-  int64_t* rows = table.data_ptr<int64_t>();
+  const bool inline_table = static_cast<int64_t>(layers) <= kInlineAppendLayers;
+  std::vector<int64_t> host_rows;
+  torch::Tensor table;
+  if (inline_table) {
+    host_rows.resize(layers * LR_APPEND_WORDS);
+  } else {
+    table = torch::empty({static_cast<int64_t>(layers) * LR_APPEND_WORDS},
+                         torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
+  }
+  int64_t* rows = inline_table ? host_rows.data() : table.data_ptr<int64_t>();
   py::list firsts(layers + 1);
   int64_t total = 0;
   int elem = 0;
@@ -1515,18 +1529,20 @@ py::tuple append_layers_launch(const std::vector<torch::Tensor>& keys,
   }
   firsts[layers] = py::int_(total);
   const c10::DeviceGuard guard(k0.device());
-  torch::Tensor device_table = table.to(k0.device(), /*non_blocking=*/true);
+  torch::Tensor device_table;
+  if (!inline_table) device_table = table.to(k0.device(), /*non_blocking=*/true);
   torch::Tensor out_keys = torch::empty({total, dim}, k0.options());
   torch::Tensor out_values = torch::empty({total, dim}, k0.options());
   torch::Tensor out_positions = torch::empty({total, 1}, positions[0].options());
   const auto i32 = cumulative[0].options();
   torch::Tensor out_cumulative = torch::empty({static_cast<int64_t>(layers), heads + 1}, i32);
   torch::Tensor out_lengths = torch::empty({static_cast<int64_t>(layers), heads}, i32);
-  check_call(library.append_layers(device_table.data_ptr<int64_t>(), static_cast<int64_t>(layers),
-                                   heads, added, dim, elem, maximum_length, out_keys.data_ptr(),
-                                   out_values.data_ptr(), out_positions.data_ptr<float>(),
-                                   out_cumulative.data_ptr<int32_t>(),
-                                   out_lengths.data_ptr<int32_t>(), current_stream(k0.device())));
+  const auto launch = inline_table ? library.append_layers_host : library.append_layers;
+  check_call(launch(inline_table ? host_rows.data() : device_table.data_ptr<int64_t>(),
+                    static_cast<int64_t>(layers), heads, added, dim, elem, maximum_length,
+                    out_keys.data_ptr(), out_values.data_ptr(), out_positions.data_ptr<float>(),
+                    out_cumulative.data_ptr<int32_t>(), out_lengths.data_ptr<int32_t>(),
+                    current_stream(k0.device())));
   return py::make_tuple(out_keys, out_values, out_positions, out_cumulative, out_lengths, firsts);
 }
 

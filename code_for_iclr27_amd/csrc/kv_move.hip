@@ -440,15 +440,20 @@ __global__ __launch_bounds__(kAppendThreads) void head_append_kernel(
 // One decode step's append into every layer (blockIdx.z = layer): the per-layer append above
 // with its arguments from a table of LR_APPEND_WORDS i64 per layer, all layers' outputs packed
 // into one K, V and positions buffer (layer l from its output row [8]) and one [L, heads + 1]
-// cumulative / [L, heads] lengths pair.
+// cumulative / [L, heads] lengths pair. The table comes from memory, or (up to
+// kInlineLayers layers, their first kAppendRowWords words) in the launch's kernel arguments.
+constexpr int kAppendRowWords = 9;  // the words of a table row the kernel reads
+constexpr int kInlineLayers = 48;
+struct InlineAppendTable {
+  int64_t words[kInlineLayers * kAppendRowWords];
+};
+
 template <int G>
-__global__ __launch_bounds__(kThreads) void append_layers_kernel(
-    const int64_t* __restrict__ table, int64_t heads, int64_t added, int64_t covered_rows,
-    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
-    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
-    int32_t* __restrict__ out_lengths) {
-  const int64_t layer = blockIdx.z;
-  const int64_t* row = table + layer * LR_APPEND_WORDS;
+__device__ __forceinline__ void append_layer(const int64_t (&row)[kAppendRowWords], int64_t layer,
+                                             int64_t heads, int64_t added, int64_t covered_rows,
+                                             const RowLayout& layout, uint8_t* out_keys,
+                                             uint8_t* out_values, float* out_positions,
+                                             int32_t* out_cumulative, int32_t* out_lengths) {
   const int64_t first = row[8];
   const int32_t* cumulative = reinterpret_cast<const int32_t*>(row[4]);
   head_append<G, true, kStreamStores>(
@@ -458,6 +463,34 @@ __global__ __launch_bounds__(kThreads) void append_layers_kernel(
       covered_rows, row[7], layout, out_keys + first * layout.row_bytes,
       out_values + first * layout.row_bytes, out_positions + first,
       out_cumulative + layer * (heads + 1), out_lengths + layer * heads);
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void append_layers_kernel(
+    const int64_t* __restrict__ table, int64_t heads, int64_t added, int64_t covered_rows,
+    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
+    int32_t* __restrict__ out_lengths) {
+  const int64_t layer = blockIdx.z;
+  int64_t row[kAppendRowWords];
+#pragma unroll
+  for (int i = 0; i < kAppendRowWords; ++i) row[i] = table[layer * LR_APPEND_WORDS + i];
+  append_layer<G>(row, layer, heads, added, covered_rows, layout, out_keys, out_values,
+                  out_positions, out_cumulative, out_lengths);
+}
+
+template <int G>
+__global__ __launch_bounds__(kThreads) void append_layers_inline_kernel(
+    const InlineAppendTable table, int64_t heads, int64_t added, int64_t covered_rows,
+    RowLayout layout, uint8_t* __restrict__ out_keys, uint8_t* __restrict__ out_values,
+    float* __restrict__ out_positions, int32_t* __restrict__ out_cumulative,
+    int32_t* __restrict__ out_lengths) {
+  const int64_t layer = blockIdx.z;
+  int64_t row[kAppendRowWords];
+#pragma unroll
+  for (int i = 0; i < kAppendRowWords; ++i) row[i] = table.words[layer * kAppendRowWords + i];
+  append_layer<G>(row, layer, heads, added, covered_rows, layout, out_keys, out_values,
+                  out_positions, out_cumulative, out_lengths);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1426,16 +1459,20 @@ extern "C" int lr_reinsert_recalled(const int64_t* workspace, int64_t count, con
   });
 }
 
-extern "C" int lr_append_layers(const int64_t* table, int64_t layers, int64_t heads,
-                                int64_t added, int64_t dim, int elem_bytes, int64_t max_length,
-                                void* out_keys, void* out_values, float* out_positions,
-                                int32_t* out_cumulative, int32_t* out_lengths, void* stream) {
-  clear_error();
+namespace {
+
+// The checks and launch shape shared by both append_layers entry points; `launch` gets the
+// granule, the row layout and the grid.
+template <typename Launch>
+int append_layers_launch(int64_t layers, int64_t heads, int64_t added, int64_t dim,
+                         int elem_bytes, int64_t max_length, void* out_keys, void* out_values,
+                         float* out_positions, int32_t* out_cumulative, int32_t* out_lengths,
+                         Launch&& launch) {
   LR_REQUIRE(valid_elem_bytes(elem_bytes) && dim > 0, "Invalid KV layout");
   LR_REQUIRE(layers > 0 && layers <= 65535 && heads > 0 && heads <= 65535 && added > 0 &&
                  max_length >= 0,
              "Invalid appended shape");
-  LR_REQUIRE(table && out_keys && out_values && out_positions && out_cumulative && out_lengths,
+  LR_REQUIRE(out_keys && out_values && out_positions && out_cumulative && out_lengths,
              "Expected contiguous CUDA tensor");
   const int64_t row_bytes = dim * elem_bytes;
   // every layer's rows are whole rows of its (16-byte aligned) allocation; the outputs bound
@@ -1445,12 +1482,50 @@ extern "C" int lr_append_layers(const int64_t* table, int64_t layers, int64_t he
   const RowLayout layout = make_layout(row_bytes, g, covered * heads * layers, 8);
   int64_t bx = ceil_div(ceil_div(covered, layout.rows_per_group), kThreads >> layout.lanes_log2);
   if (bx < 1) bx = 1;
-  dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads),
-            static_cast<unsigned>(layers));
-  return dispatch_granule(g, [&]<int G>() {
-    append_layers_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
-        table, heads, added, covered, layout, bytes(out_keys), bytes(out_values), out_positions,
-        out_cumulative, out_lengths);
-    return check_launch("append_layers");
-  });
+  const dim3 grid(static_cast<unsigned>(bx < 65535 ? bx : 65535), static_cast<unsigned>(heads),
+                  static_cast<unsigned>(layers));
+  return dispatch_granule(
+      g, [&]<int G>() { return launch.template operator()<G>(covered, layout, grid); });
+}
+
+}  // namespace
+
+extern "C" int lr_append_layers(const int64_t* table, int64_t layers, int64_t heads,
+                                int64_t added, int64_t dim, int elem_bytes, int64_t max_length,
+                                void* out_keys, void* out_values, float* out_positions,
+                                int32_t* out_cumulative, int32_t* out_lengths, void* stream) {
+  clear_error();
+  LR_REQUIRE(table != nullptr, "Expected contiguous CUDA tensor");
+  return append_layers_launch(
+      layers, heads, added, dim, elem_bytes, max_length, out_keys, out_values, out_positions,
+      out_cumulative, out_lengths,
+      [&]<int G>(int64_t covered, const RowLayout& layout, dim3 grid) {
+        append_layers_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+            table, heads, added, covered, layout, bytes(out_keys), bytes(out_values),
+            out_positions, out_cumulative, out_lengths);
+        return check_launch("append_layers");
+      });
+}
+
+extern "C" int lr_append_layers_host(const int64_t* host_table, int64_t layers, int64_t heads,
+                                     int64_t added, int64_t dim, int elem_bytes,
+                                     int64_t max_length, void* out_keys, void* out_values,
+                                     float* out_positions, int32_t* out_cumulative,
+                                     int32_t* out_lengths, void* stream) {
+  clear_error();
+  LR_REQUIRE(host_table != nullptr, "Invalid appended shape");
+  LR_REQUIRE(layers <= kInlineLayers, "Too many layers for a table in the launch");
+  InlineAppendTable words{};
+  for (int64_t l = 0; l < layers; ++l)
+    for (int i = 0; i < kAppendRowWords; ++i)
+      words.words[l * kAppendRowWords + i] = host_table[l * LR_APPEND_WORDS + i];
+  return append_layers_launch(
+      layers, heads, added, dim, elem_bytes, max_length, out_keys, out_values, out_positions,
+      out_cumulative, out_lengths,
+      [&]<int G>(int64_t covered, const RowLayout& layout, dim3 grid) {
+        append_layers_inline_kernel<G><<<grid, kThreads, 0, as_stream(stream)>>>(
+            words, heads, added, covered, layout, bytes(out_keys), bytes(out_values),
+            out_positions, out_cumulative, out_lengths);
+        return check_launch("append_layers");
+      });
 }

@@ -89,6 +89,16 @@ int lr_append_layers(const int64_t* table, int64_t layers, int64_t heads, int64_
                      void* out_values, float* out_positions, int32_t* out_cumulative,
                      int32_t* out_lengths, void* stream);
 
+/* lr_append_layers with the table in HOST memory (same layout, LR_APPEND_WORDS i64 per layer;
+ * no single reference counterpart, like lr_append_layers): the table is read during the call
+ * and its first nine words per layer travel in the launch's kernel arguments, so the call needs
+ * no device copy of it and the caller may reuse the table as soon as the call returns. At most
+ * 48 layers; the other arguments and the result are those of lr_append_layers. */
+int lr_append_layers_host(const int64_t* host_table, int64_t layers, int64_t heads,
+                          int64_t added, int64_t dim, int elem_bytes, int64_t max_length,
+                          void* out_keys, void* out_values, float* out_positions,
+                          int32_t* out_cumulative, int32_t* out_lengths, void* stream);
+
 /* compact (csrc/scoring.cu:164-188, 294-314). removed [removed_count] i64, sorted, unique.
  * Outputs [rows - removed_count, dim] and positions [rows - removed_count]. */
 int lr_compact(const void* keys, const void* values, const float* positions, int64_t rows,

@@ -200,6 +200,87 @@ def test_append_layers_matches_per_layer_append(device, dtype, added, dim):
                          starts, maximum)
 
 
+def _append_layer_inputs(layer_lengths, heads, added, dim, device, seed):
+    args = {name: [] for name in ("keys", "values", "positions", "new_k", "new_v", "cumulative")}
+    for l, lengths in enumerate(layer_lengths):
+        rows = sum(lengths)
+        args["keys"].append(rand((rows, dim), torch.bfloat16, device, seed + 3 * l))
+        args["values"].append(rand((rows, dim), torch.bfloat16, device, seed + 3 * l + 1))
+        args["positions"].append(torch.arange(rows).float().to(device)[:, None] + l)
+        args["new_k"].append(rand((1, heads, added, dim), torch.bfloat16, device, seed + 3 * l + 2))
+        args["new_v"].append(rand((1, heads, added, dim), torch.bfloat16, device, seed + 3 * l + 3))
+        args["cumulative"].append(torch.tensor(np.concatenate(([0], np.cumsum(lengths))),
+                                               dtype=torch.int32, device=device))
+    return args
+
+
+def test_append_layers_beyond_the_inline_table(device):
+    """50 layers: more than the 48 whose table travels in the kernel arguments, so the table goes
+    up as a device copy; every layer bit-exact against the oracle's per-layer append."""
+    heads, added, dim = 2, 1, 64
+    layer_lengths = [[(7 * l) % 13, (3 * l + 1) % 11] for l in range(50)]
+    args = _append_layer_inputs(layer_lengths, heads, added, dim, device, 300)
+    starts = [1000 + l for l in range(50)]
+    maximum = max(max(lengths) for lengths in layer_lengths)
+    keys, values, positions, cumulative, lengths_out, first = _C.append_layers(
+        args["keys"], args["values"], args["positions"], args["new_k"], args["new_v"],
+        args["cumulative"], starts, maximum)
+    for l in range(50):
+        expect = kv_ops.append(bits(args["keys"][l]), bits(args["values"][l]),
+                               bits(args["positions"][l]).view(np.float32), bits(args["new_k"][l]),
+                               bits(args["new_v"][l]), args["cumulative"][l].cpu().numpy(),
+                               starts[l], maximum)
+        rows = slice(first[l], first[l + 1])
+        np.testing.assert_array_equal(bits(keys[rows]), expect[0])
+        np.testing.assert_array_equal(bits(values[rows]), expect[1])
+        np.testing.assert_array_equal(positions[rows].cpu().numpy(), expect[2])
+        np.testing.assert_array_equal(cumulative[l].cpu().numpy(), expect[3])
+        np.testing.assert_array_equal(lengths_out[l].cpu().numpy(), expect[4])
+
+
+def test_append_layers_host_table_through_the_abi(device):
+    """lr_append_layers_host (the table in the launch's kernel arguments) against
+    lr_append_layers (the same table in device memory), bit-exact, with the host table
+    overwritten right after the call while the device is still held (the overwrite describes
+    the same layers with other logical starts, so a late read would change the positions)."""
+    heads, added, dim, L = 8, 1, 128, 32
+    layer_lengths = [[40 + (5 * l + h) % 17 for h in range(heads)] for l in range(L)]
+    args = _append_layer_inputs(layer_lengths, heads, added, dim, device, 500)
+    table = np.zeros((L, 12), dtype=np.int64)
+    total = 0
+    for l, lengths in enumerate(layer_lengths):
+        table[l, :9] = [args["keys"][l].data_ptr(), args["values"][l].data_ptr(),
+                        args["positions"][l].data_ptr(), sum(lengths), args["cumulative"][l].data_ptr(),
+                        args["new_k"][l].data_ptr(), args["new_v"][l].data_ptr(), 2000 + l, total]
+        total += sum(lengths) + heads * added
+    maximum = max(max(lengths) for lengths in layer_lengths)
+    outs = [(torch.empty((total, dim), dtype=torch.bfloat16, device=device),
+             torch.empty((total, dim), dtype=torch.bfloat16, device=device),
+             torch.empty((total, 1), device=device),
+             torch.empty((L, heads + 1), dtype=torch.int32, device=device),
+             torch.empty((L, heads), dtype=torch.int32, device=device)) for _ in range(2)]
+    stream = _lib.stream_of(args["keys"][0])
+    device_table = torch.from_numpy(table.copy()).to(device)
+    ptrs = lambda o: [t.data_ptr() for t in o]
+    _lib.call("lr_append_layers", device_table.data_ptr(), L, heads, added, dim, 2, maximum,
+              *ptrs(outs[0]), stream)
+    torch.cuda._sleep(5_000_000)
+    _lib.call("lr_append_layers_host", table.ctypes.data, L, heads, added, dim, 2, maximum,
+              *ptrs(outs[1]), stream)
+    table[:, 7] += 77
+    torch.cuda.synchronize()
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(bits(a) if a.dtype == torch.bfloat16 else a.cpu().numpy(),
+                                      bits(b) if b.dtype == torch.bfloat16 else b.cpu().numpy())
+    expect = kv_ops.append(bits(args["keys"][3]), bits(args["values"][3]),
+                           bits(args["positions"][3]).view(np.float32), bits(args["new_k"][3]),
+                           bits(args["new_v"][3]), args["cumulative"][3].cpu().numpy(), 2003,
+                           maximum)
+    rows = slice(int(table[3, 8]), int(table[4, 8]))
+    np.testing.assert_array_equal(bits(outs[1][0][rows]), expect[0])
+    np.testing.assert_array_equal(outs[1][2][rows].cpu().numpy(), expect[2])
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(1, 8, 1, 1), (2, 4, 3, 128), (1, 8, 2, 64)])
 def test_append_flattened_cache(device, dtype, shape):

@@ -96,6 +96,15 @@ def test_batch_append_host_bounds_the_descriptor_table():
     assert status == 1 and "Request metadata mismatch" in _lib.last_error()
 
 
+def test_append_layers_host_bounds_the_table():
+    """An append table in the launch's kernel arguments: at most 48 layers, rejected on the host."""
+    library = _lib.load()
+    table = np.zeros(49 * 12, dtype=np.int64)
+    status = library.lr_append_layers_host(table.ctypes.data, 49, 8, 1, 128, 2, 10, 1, 1, 1, 1,
+                                           1, None)
+    assert status == 1 and "Too many layers" in _lib.last_error()
+
+
 def test_zero_work_calls_succeed_without_launching():
     library = _lib.load()
     assert library.lr_compact(None, None, None, 5, 8, 2, None, 5, None, None, None, None) == 0
